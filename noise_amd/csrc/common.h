@@ -1,0 +1,58 @@
+// Shared device helpers for the gfx950 kernels of libnoise_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Status codes returned by every entry point (0 = ok; positive = hipError_t).
+#define NOISE_OK 0
+#define NOISE_EINVAL (-1)     // bad shape / stride / pointer
+#define NOISE_ENOSPC (-2)     // workspace too small
+#define NOISE_ENOTSUP (-3)    // shape outside what the kernels tile
+
+#define NOISE_CHECK_LAUNCH()                                   \
+  do {                                                         \
+    hipError_t e_ = hipGetLastError();                         \
+    if (e_ != hipSuccess) return (int)e_;                      \
+  } while (0)
+
+// Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950), the same rounding torch uses.
+__device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
+__device__ __forceinline__ float bf16r(float x) { return (float)(bf16)x; }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Butterfly reductions inside groups of lanes.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// XCD-aware workgroup remap: the hardware deals consecutive workgroup ids round-robin over the 8 XCDs;
+// this returns a logical tile id such that each XCD works on one contiguous range of tiles (shared
+// operand rows then stay in that XCD's L2).
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int XCDS = 8;
+  if (nblocks % XCDS != 0) return bid;
+  return (bid % XCDS) * (nblocks / XCDS) + bid / XCDS;
+}

@@ -1,0 +1,115 @@
+"""GPU parity of the low-rank GEMM paths against the CPU oracle (bf16 rounding-point mode).
+
+Tolerance (north star): <= 1e-2 relative error on bf16 activations. The kernels keep the reference's
+autocast rounding points, so the observed error is accumulation-order noise (~1e-3)."""
+import pytest
+import torch
+
+from oracle import model as om
+from tests._util import log_case, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+
+
+def _mlp_inputs(P, T, shared_x, sigma, seed=0, d=512, f=2048):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, d, generator=g) if shared_x else torch.randn(P, T, d, generator=g)
+    w1 = (torch.randn(f, d, generator=g) * d ** -0.5).bfloat16()
+    w2 = (torch.randn(d, f, generator=g) * f ** -0.5).bfloat16()
+    pairs = P // 2
+    a1, b1 = torch.randn(pairs, f, generator=g), torch.randn(pairs, d, generator=g)
+    a2, b2 = torch.randn(pairs, d, generator=g), torch.randn(pairs, f, generator=g)
+    sign = torch.tensor([sigma, -sigma]).repeat(pairs)
+    return x.bfloat16(), w1, w2, a1, b1, a2, b2, sign
+
+
+def _oracle_members(x, w1, w2, a1, b1, a2, b2, sign, members):
+    rep = lambda t: t.repeat_interleave(2, 0)[members]  # noqa: E731
+    xs = x.float() if x.dim() == 2 else x.float()[members]
+    return om.mlp_population(xs, w1.float(), w2.float(), rep(a1), rep(b1), rep(a2), rep(b2), sign[members], 'bf16')
+
+
+@pytest.mark.parametrize('shared_x,sigma', [(False, 1e-3), (True, 1e-3), (False, 5e-2)])
+def test_mlp_small_matches_oracle(shared_x, sigma):
+    from noise_amd import ops
+    P, T = 4, 256
+    log_case(f'mlp small P={P} T={T} shared_x={shared_x} sigma={sigma}')
+    args = _mlp_inputs(P, T, shared_x, sigma)
+    dev = [t.to(DEV) for t in args]
+    y = ops.lowrank_mlp(*dev, T=T, pair_shift=1)
+    torch.cuda.synchronize()
+    ref = _oracle_members(*args, list(range(P)))
+    y = y.cpu()
+    assert rel_err(y, ref) < 1e-2
+    assert rel_err(y, ref) < 4e-3  # accumulation-order noise only
+    # the antithetic difference (the ES signal) survives: compare pair differences
+    d_gpu, d_ref = y[0::2] - y[1::2], ref[0::2] - ref[1::2]
+    assert rel_err(d_gpu, d_ref) < 5e-2, rel_err(d_gpu, d_ref)
+
+
+def test_mlp_bf16_output_and_residual_accumulate():
+    from noise_amd import ops
+    P, T = 2, 128
+    log_case(f'mlp bf16 out / accumulate P={P} T={T}')
+    args = _mlp_inputs(P, T, False, 1e-2, seed=1)
+    dev = [t.to(DEV) for t in args]
+    y16 = ops.lowrank_mlp(*dev, T=T, pair_shift=1, out_dtype=torch.bfloat16)
+    resid = torch.randn(P, T, 512, generator=torch.Generator().manual_seed(3))
+    r = resid.to(DEV)
+    ops.lowrank_mlp(*dev, T=T, pair_shift=1, out=r, accumulate=True)
+    torch.cuda.synchronize()
+    ref = _oracle_members(*args, list(range(P)))
+    assert y16.dtype == torch.bfloat16
+    assert rel_err(y16.cpu().float(), ref) < 1e-2
+    assert rel_err(r.cpu() - resid, ref) < 4e-3
+
+
+def test_lowrank_linear_matches_oracle():
+    from noise_amd import ops
+    g = torch.Generator().manual_seed(4)
+    P, T, din, dout = 4, 256, 512, 1536
+    log_case(f'lowrank_linear P={P} T={T} {din}->{dout}')
+    x = torch.randn(P, T, din, generator=g).bfloat16()
+    w = (torch.randn(dout, din, generator=g) / 20).bfloat16()
+    a, b = torch.randn(P, dout, generator=g), torch.randn(P, din, generator=g)
+    sign = torch.tensor([1e-3, -1e-3, 2e-3, -2e-3])
+    y = ops.lowrank_linear(x.to(DEV), w.to(DEV), a.to(DEV), b.to(DEV), sign.to(DEV))
+    torch.cuda.synchronize()
+    ref = om.lowrank(x.float(), w.float(), a, b, sign, 'bf16')
+    # same rounding points: the bf16 dense part is exact up to accumulation order
+    assert rel_err(y.cpu(), ref) < 1e-3
+    assert (y.cpu() - ref).abs().max() < 2e-2
+
+
+@pytest.mark.parametrize('T', [64, 200])
+def test_lowrank_linear_ragged_rows(T):
+    """M = members * T not a multiple of the 128-row tile (tail rows clamped / masked)."""
+    from noise_amd import ops
+    g = torch.Generator().manual_seed(5)
+    P, din, dout = 3, 512, 512
+    log_case(f'lowrank_linear ragged P={P} T={T}')
+    x = torch.randn(P, T, din, generator=g).bfloat16()
+    w = (torch.randn(dout, din, generator=g) / 20).bfloat16()
+    a, b = torch.randn(P, dout, generator=g), torch.randn(P, din, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 0.0])
+    y = ops.lowrank_linear(x.to(DEV), w.to(DEV), a.to(DEV), b.to(DEV), sign.to(DEV))
+    torch.cuda.synchronize()
+    ref = om.lowrank(x.float(), w.float(), a, b, sign, 'bf16')
+    assert rel_err(y.cpu(), ref) < 1e-3
+
+
+def test_mlp_config1_full_size_sampled_members():
+    """Config 1 at its real shape (P = 256, T = 2048, shared x); three members checked in full."""
+    from noise_amd import ops
+    P, T = 256, 2048
+    log_case(f'mlp config1 P={P} T={T}')
+    args = _mlp_inputs(P, T, True, 1e-3, seed=2)
+    dev = [t.to(DEV) for t in args]
+    y = ops.lowrank_mlp(*dev, T=T, pair_shift=1, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    members = [0, 1, 255]
+    ref = _oracle_members(*args, members)
+    got = y[members].cpu().float()
+    assert rel_err(got, ref) < 1e-2

@@ -1,0 +1,224 @@
+"""Pins of the CPU oracle against closed forms, library routines and brute force (CPU only).
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term, a swapped a/b, a wrong
+window edge, a missing square) fails it; none re-types the oracle's own formula.
+"""
+import math
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from oracle import eggroll as oe
+from oracle import model as om
+
+torch.set_num_threads(8)
+
+
+def test_norm_matches_library_rms_norm():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 7, 512, generator=g) * 3
+    assert torch.equal(om.norm(x), F.rms_norm(x, (512,)))
+    xb = x.bfloat16()
+    assert torch.equal(om.norm(xb), F.rms_norm(xb, (512,)))
+    q = torch.randn(2, 3, 8, 64, generator=g)
+    assert torch.equal(om.norm(q), F.rms_norm(q, (64,)))
+
+
+def test_rotary_is_complex_rotation():
+    g = torch.Generator().manual_seed(1)
+    cos, sin = om.rotary_tables(64)
+    x = torch.randn(2, 64, 3, 64, generator=g)
+    out = om.apply_rotary(x, cos, sin)
+    z = torch.complex(x[..., :32].double(), x[..., 32:].double())
+    theta = torch.complex(cos.double(), -sin.double())[None, :, None, :]
+    r = z * theta
+    assert torch.allclose(out[..., :32].double(), r.real, atol=1e-6)
+    assert torch.allclose(out[..., 32:].double(), r.imag, atol=1e-6)
+    # position 0 is the identity; the tables are bf16 values of cos/sin(t * 10000^(-2i/64))
+    assert torch.equal(out[:, 0], x[:, 0])
+    t, i = 37, 5
+    assert float(cos[t, i]) == float(torch.tensor(math.cos(t * 10000 ** (-2 * i / 64))).bfloat16())
+
+
+def test_window_sizes_follow_sequence_len():
+    assert om.window_sizes() == [1024, 1024, 1024, 2048, 1024, 1024, 1024, 2048]
+    assert om.window_sizes(256) == [128, 128, 128, 256, 128, 128, 128, 256]
+
+
+@pytest.mark.parametrize('window', [3, 7, 100])
+def test_attention_matches_fp64_loops(window):
+    g = torch.Generator().manual_seed(2)
+    B, T, H, D = 2, 9, 2, 8
+    q, k, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
+    out = om.attention(q, k, v, window)
+    ref = torch.zeros(B, T, H, D, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            for s in range(T):
+                keys = [j for j in range(T) if j <= s and s - j <= window]
+                logits = torch.tensor([float(q[b, s, h].double() @ k[b, j, h].double()) / math.sqrt(D) for j in keys])
+                w = torch.exp(logits - logits.max())
+                w = w / w.sum()
+                ref[b, s, h] = sum(w[n] * v[b, j, h].double() for n, j in enumerate(keys))
+    assert torch.allclose(out.double(), ref, atol=1e-5)
+
+
+def _perturbation(g, m, out_dim, in_dim):
+    return torch.randn(m, out_dim, generator=g), torch.randn(m, in_dim, generator=g)
+
+
+def test_lowrank_equals_materialised_perturbed_weight():
+    g = torch.Generator().manual_seed(3)
+    m, T, din, dout = 4, 5, 16, 12
+    x = torch.randn(m, T, din, generator=g)
+    W = torch.randn(dout, din, generator=g)
+    a, b = _perturbation(g, m, dout, din)
+    sign = torch.tensor([0.3, -0.3, 0.1, -0.1])
+    y = om.lowrank(x, W, a, b, sign)
+    for p in range(m):
+        Wp = W.double() + sign[p].double() * torch.outer(a[p].double(), b[p].double())
+        assert torch.allclose(y[p].double(), x[p].double() @ Wp.t(), atol=1e-5)
+    # an antithetic pair (same input, same a/b, opposite signs) averages to the clean output
+    xs = x[:1].expand(2, -1, -1)
+    pair = om.lowrank(xs, W, a[:1].expand(2, -1), b[:1].expand(2, -1), torch.tensor([0.3, -0.3]))
+    assert torch.allclose((pair[0] + pair[1]) / 2, x[0] @ W.t(), atol=1e-5)
+
+
+def test_lowrank_bf16_mode_rounding_points():
+    g = torch.Generator().manual_seed(4)
+    m, T, din, dout = 2, 8, 64, 32
+    x = torch.randn(m, T, din, generator=g)
+    W = torch.randn(dout, din, generator=g) / 8
+    a, b = _perturbation(g, m, dout, din)
+    sign = torch.tensor([1e-3, -1e-3])
+    y = om.lowrank(x, W, a, b, sign, 'bf16')
+    dense = (x.bfloat16().double() @ W.bfloat16().double().t()).float().bfloat16().float()
+    u = (x.bfloat16().double() @ b.bfloat16().double().unsqueeze(-1)).float().bfloat16().float()
+    assert torch.allclose(y, dense + sign[:, None, None] * u * a[:, None, :], atol=1e-6)
+    # the fp32 correction survives on top of the bf16 dense part (it is below bf16 resolution)
+    assert not torch.equal(y[0], y[0].bfloat16().float())
+
+
+def test_lowrank_embed_equals_gathered_perturbed_table():
+    g = torch.Generator().manual_seed(5)
+    V, d, m = 50, 16, 4
+    W = torch.randn(V, d, generator=g)
+    a, b = _perturbation(g, m, V, d)
+    sign = torch.tensor([0.2, -0.2, 0.5, -0.5])
+    idx = torch.randint(0, V, (11,), generator=g)
+    out = om.lowrank_embed(W, a, b, idx, sign)
+    for p in range(m):
+        table = W + sign[p] * torch.outer(a[p], b[p])
+        assert torch.allclose(out[p], table[idx], atol=1e-6)
+
+
+def _tiny_model(seed=0):
+    from noise_amd.model import make_model
+    from noise_amd.synthetic import trained_like
+    model = trained_like(make_model('cpu', seed))
+    return {n: p.detach().clone() for n, p in model.named_parameters()}
+
+
+def test_population_loss_equals_clean_forward_on_perturbed_weights():
+    """Member p of the population is the fixed model at theta + s_p E_p (brute force, tiny T)."""
+    from noise_amd.synthetic import antithetic_signs, population_noise, zipf_tokens
+    p = _tiny_model()
+    shapes = {n: tuple(t.shape) for n, t in p.items()}
+    noise = population_noise(shapes, 2, seed=7)
+    sign = antithetic_signs(4, 0.05)  # large sigma so a dropped perturbation term is visible
+    idx, tgt = zipf_tokens(24, seed=8)
+    losses = om.population_loss(p, noise, sign, idx, tgt)
+    for m in range(4):
+        pm = om.perturbed_params(p, noise, sign, m)
+        ref = om.gpt_forward(pm, idx[None], tgt[None])
+        assert abs(float(losses[m]) - float(ref)) < 2e-5, m
+    assert float((losses[0] - losses[1]).abs()) > 1e-3
+
+
+def test_population_loss_sigma_zero_is_clean_loss():
+    from noise_amd.synthetic import antithetic_signs, population_noise, zipf_tokens
+    p = _tiny_model()
+    noise = population_noise({n: tuple(t.shape) for n, t in p.items()}, 2, seed=7)
+    idx, tgt = zipf_tokens(16, seed=9)
+    losses = om.population_loss(p, noise, antithetic_signs(4, 0.0), idx, tgt)
+    clean = om.gpt_forward(p, idx[None], tgt[None])
+    assert torch.allclose(losses, clean.expand(4), atol=1e-6)
+
+
+def test_head_loss_is_capped_cross_entropy_with_stable_lse():
+    g = torch.Generator().manual_seed(6)
+    m, T, D, V = 2, 3, 8, om.VOCAB
+    h = torch.randn(m, T, D, generator=g)
+    W = torch.randn(V, D, generator=g) * 100  # logits far beyond the cap
+    a, b = _perturbation(g, m, V, D)
+    sign = torch.tensor([0.0, 0.0])
+    tgt = torch.tensor([0, 5, V - 1])
+    out = om.head_loss(h, W, a, b, sign, tgt)
+    z = 15 * torch.tanh((h.double() @ W.double().t()) / 15)
+    lse = torch.logsumexp(z, -1)
+    ce = lse - z.gather(-1, tgt.expand(m, T)[..., None])[..., 0]
+    assert torch.allclose(out.double(), ce.mean(-1), atol=1e-4)
+    assert torch.isfinite(out).all()
+
+
+def test_moments_match_fp64_brute_force():
+    g = torch.Generator().manual_seed(7)
+    o = torch.randn(2, 3, 10, 4, generator=g)
+    m1, m2 = om.attention_moments(o)
+    for p in range(2):
+        for h in range(3):
+            for d in range(4):
+                col = [float(o[p, h, t, d]) for t in range(10)]
+                assert abs(float(m1[p, h, d]) - sum(col) / 10) < 1e-6
+                assert abs(float(m2[p, h, d]) - sum(c * c for c in col) / 10) < 1e-6
+
+
+def test_fitness_closed_form():
+    losses = torch.tensor([1.0, 3.0, 2.0, 1.0, 5.0, 5.5])
+    f, w = oe.fitness(losses, 3)
+    raw = [3.0 - 1.0, 1.0 - 2.0, 5.5 - 5.0]  # odd minus even, no centering
+    mean = sum(raw) / 3
+    std = math.sqrt(sum((r - mean) ** 2 for r in raw) / 2)  # unbiased
+    assert torch.allclose(f, torch.tensor([r / (std + 1e-8) for r in raw]), atol=1e-6)
+    assert torch.allclose(w, f)
+    _, w2 = oe.fitness(losses, 2)  # folding: direction j collects pairs j, j+2, ...
+    assert torch.allclose(w2, torch.tensor([f[0] + f[2], f[1]]), atol=1e-6)
+
+
+def test_update_is_weighted_sum_of_outer_products():
+    g = torch.Generator().manual_seed(8)
+    n, out_d, in_d = 5, 4, 3
+    a, b = torch.randn(n, out_d, generator=g), torch.randn(n, in_d, generator=g)
+    eps = torch.randn(n, 8, generator=g)
+    w = torch.randn(n, generator=g)
+    grads = oe.update(w, {'m': (a, b), 'l': eps}, 10)
+    ref = -sum(w[j] * torch.outer(a[j], b[j]) for j in range(n)) / 10
+    assert torch.allclose(grads['m'], ref, atol=1e-6)
+    assert torch.allclose(grads['l'], -sum(w[j] * eps[j] for j in range(n)) / 10, atol=1e-6)
+
+
+def test_adam_matches_torch_adamw():
+    g = torch.Generator().manual_seed(9)
+    p0 = torch.randn(6, 5, generator=g)
+    ref = p0.clone().requires_grad_(False)
+    opt = torch.optim.AdamW([ref], lr=1e-3, betas=oe.BETAS, eps=1e-8, weight_decay=0.0)
+    mine, m, v = p0.clone(), torch.zeros_like(p0), torch.zeros_like(p0)
+    for step in range(1, 4):
+        grad = torch.randn(6, 5, generator=g)
+        ref.grad = grad.clone()
+        opt.step()
+        oe.adam_step(mine, grad, m, v, step, 1e-3)
+        assert torch.allclose(mine, ref, atol=1e-7, rtol=1e-6)
+
+
+def test_learning_rate_warmdown():
+    assert oe.learning_rate(1, 10) == pytest.approx(1e-3)
+    assert oe.learning_rate(10, 10) == pytest.approx(1e-3 * 0.1 / 0.3)
+    assert oe.learning_rate(8, 10) == pytest.approx(1e-3)
+
+
+def test_member_directions():
+    d = oe.member_directions(0, 4, 4)
+    assert d.tolist() == [0, 1, 2, 3]
+    assert oe.member_directions(8, 4, 4).tolist() == [0, 1, 2, 3]
