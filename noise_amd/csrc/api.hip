@@ -81,7 +81,7 @@ int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* b
   const size_t M = (size_t)members * T;
   Carve c(nullptr);
   c.take<float>(M);                                    // u_fc
-  c.take<float>(M * (f / lowrank_gemm_wave_n()));       // partial dots h.b_proj
+  c.take<float>(M * lowrank_gemm_parts(f));            // partial dots h.b_proj
   c.take<bf16>(M * f);                                  // hidden h
   *bytes = c.used;
   return NOISE_OK;
@@ -94,12 +94,12 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   size_t need = 0;
   if (int rc = noise_lowrank_mlp_workspace_size(members, T, d, f, &need)) return rc;
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
-  if (f % lowrank_gemm_wave_n() || (accumulate && (!y_f32 || y_bf16))) return NOISE_EINVAL;
+  if (!lowrank_gemm_parts(f) || (accumulate && (!y_f32 || y_bf16))) return NOISE_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t M = (size_t)members * T;
   Carve c(workspace);
   float* u_fc = c.take<float>(M);
-  const int parts = f / lowrank_gemm_wave_n();
+  const int parts = lowrank_gemm_parts(f);
   float* upart = c.take<float>(M * parts);
   bf16* hid = c.take<bf16>(M * f);
   if (int rc = rowdot_launch(static_cast<const bf16*>(x), x_ld, x_mstride, (int)M, d, T, pair_shift, b_fc, d, u_fc, s))

@@ -26,10 +26,11 @@ struct LowrankGemmArgs {
   const float* rb_next;
   long rb_next_ld;
   float* upart_out;   // [M, upart_ld]
-  int upart_ld;       // = N / lowrank_gemm_wave_n()
+  int upart_ld;       // = lowrank_gemm_parts(N)
 };
 
-int lowrank_gemm_wave_n();
+// Number of partial row dots EPI_RELU2 writes per row for an N-column output (0: N unsupported).
+int lowrank_gemm_parts(int N);
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream);
 
 // Row dots u[row] = bf16(sum_k x[row, k] * bf16(b[dir, k])) for a bf16 activation (rowops.hip).

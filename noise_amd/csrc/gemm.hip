@@ -1,13 +1,41 @@
 // Low-rank-perturbed GEMM on gfx950 bf16 MFMA: out = x W^T + s_p (x.b_p) a_p^T per member p.
 //
 // Reference: `lowrank` (train/val/eggroll.py:56-58) under bf16 autocast (:144). The dense part runs
-// on v_mfma_f32_16x16x32_bf16 with LDS-staged, XOR-swizzled tiles; the rank-1 part never touches the
-// MFMA pipe: the input-side dot u = bf16(x.b_p) arrives per row (computed by the kernel that produced
-// x) and the epilogue adds (s_p u) a_p[col] in fp32 on top of the bf16-rounded GEMM output, exactly
-// the autocast rounding points (bf16 GEMM output, fp32 correction).
+// on v_mfma_f32_16x16x32_bf16; the rank-1 part never touches the MFMA pipe: the input-side dot
+// u = bf16(x.b_p) arrives per row (computed by the kernel that produced x) and the epilogue adds
+// (s_p u) a_p[col] in fp32 on top of the bf16-rounded GEMM output, exactly the autocast rounding
+// points (bf16 GEMM output, fp32 correction).
 //
 // Layouts (row-major, K contiguous): A [M, K] bf16 with M = members x T rows (member p owns rows
 // p*T .. p*T+T-1); W [N, K] bf16 in the reference's nn.Linear orientation [out, in].
+//
+// Schedule. The kernel is persistent: one workgroup per CU walks a list of BM x BN output tiles.
+// Hardware deals workgroups round-robin over the 8 XCDs, so workgroup b serves XCD b % 8; each XCD
+// owns one contiguous range of tiles (N fastest), which keeps the x rows shared by neighbouring
+// tiles in that XCD's L2.
+//
+// Main loop. K is walked in 32-deep MFMA steps through a STAGES-deep LDS ring of BK-deep stages,
+// filled by direct global->LDS loads (global_load_lds_dwordx4, no VGPR staging). The refill of a
+// stage is issued right after the barrier that retires it, so STAGES - 1 stages are in flight while
+// one feeds the MFMAs. MFMA operands are double-buffered in registers: step t + 1's W fragments and
+// x fragments are read from LDS while step t's MFMAs run (x fragment i right after row i's MFMAs,
+// when its register is dead), so the MFMA pipe never waits on LDS latency. Rows of BK bf16 are
+// stored with their 16-byte chunks XOR-swizzled per 128-byte LDS line: the ds_read_b128 operand
+// fetches (16 consecutive rows, one chunk) are bank-conflict free.
+//
+// Transposed product. The MFMA computes C^T = W x^T: W rows are the MFMA "A" operand and x rows the
+// "B" operand, so each lane ends up holding one token row and CW = 4 x FN output columns. LDS row
+// R of the W tile holds W row band + (r / 4) * CW + 4 j + r % 4 (band = R - R % WN, j = (R % WN) / 16,
+// r = R % 16), so MFMA block j reads 16 consecutive LDS rows and each lane's CW columns are
+// contiguous: the epilogue stores 16-byte vectors from registers and reduces row dots over the 4
+// lanes that share a row.
+//
+// Epilogue overlap. When a tile's last MFMAs are issued, the workgroup issues the global loads of the
+// next tile's epilogue vectors (a_p, b_next, x.b partial sums, sign) and the DMA of the next tile's
+// first STAGES stages, then runs this tile's epilogue from LDS-staged vectors; the stores drain
+// while the next tile's operands land.
+#include <algorithm>
+
 #include "common.h"
 #include "gemm.h"
 
@@ -20,181 +48,415 @@ enum : int {
   EPI_RESID = 2,   // resid += lowrank(x)          -> fp32 read-modify-write
 };
 
-template <int BM, int BN, int BK, int WGM, int WGN>
-struct Tile {
-  static constexpr int NTH = WGM * WGN * 64;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
+struct Cfg {
+  static constexpr int NW = WGM * WGN, NTH = NW * 64;
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int FM = WM / 16, FN = WN / 16;
-  static constexpr int CH = BK / 8;  // 16-byte chunks per LDS row
-  static constexpr int A_LOADS = BM * CH / NTH;
-  static constexpr int B_LOADS = BN * CH / NTH;
-  static_assert(BK == 64, "swizzle assumes 128-byte LDS rows");
-  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be a multiple of 16");
-  static_assert(BM * CH % NTH == 0 && BN * CH % NTH == 0, "tile loads must divide evenly");
+  static constexpr int CW = 4 * FN;              // contiguous output columns per lane
+  static constexpr int CPR = BK / 8;             // 16-byte chunks per LDS row
+  static constexpr int RPL = 8 / CPR;            // rows per 128-byte LDS line
+  static constexpr int ROWS_PER_DMA = 64 / CPR;  // rows one wave-wide 1 KiB DMA fills
+  static constexpr int LA = BM / ROWS_PER_DMA / NW;  // DMA instructions per wave per stage (x tile)
+  static constexpr int LB = BN / ROWS_PER_DMA / NW;  // (W tile)
+  static constexpr int L = LA + LB;
+  static constexpr int STAGE = (BM + BN) * BK;   // bf16 elements per LDS stage
+  static constexpr int UGROUPS = NTH / BM;       // threads summing one row's x.b partials
+  static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
+  static_assert(WM % 16 == 0 && WN % 16 == 0 && FN % 2 == 0, "wave tile must be a multiple of 16 x 32");
+  static_assert(LA * ROWS_PER_DMA * NW == BM && LB * ROWS_PER_DMA * NW == BN, "DMA must tile evenly");
+  static_assert((STAGES - 1) * L <= 63, "vmcnt range");
+  static_assert(STAGES >= 2 && STAGES <= 4, "wait_stage handles up to 3 stages ahead");
+  static_assert(NTH % BM == 0 && NTH >= BN / 2, "epilogue vector staging");
 };
 
-// 16-byte chunk c of LDS row r is stored at chunk c ^ (r & 7): the 8 lanes of a ds_read_b128 phase
-// (consecutive rows, same k chunk) then hit 8 distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+// Element offset of (row r, logical 16-byte chunk c) in a swizzled LDS tile with BK-wide rows.
+template <int BK>
+__device__ __forceinline__ int swz(int r, int c) {
+  constexpr int CPR = BK / 8, RPL = 8 / CPR;
+  return r * BK + ((c ^ ((r / RPL) % CPR)) << 3);
+}
 
-template <int BM, int BN, int BK, int WGM, int WGN, int EPI>
-__global__ void __launch_bounds__(WGM * WGN * 64)
+// s_waitcnt with vmcnt(n) (n <= 63), lgkmcnt(0), expcnt untouched.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+// Wait until every DMA older than the last `ahead` stages (L instructions each) has landed. Vector
+// memory operations complete in issue order, so counting only the unconditionally issued DMA of
+// later stages is safe: any other operation issued after them only makes the wait stricter.
+template <int L, int MAXAHEAD>
+__device__ __forceinline__ void wait_stage(int ahead) {
+  if constexpr (MAXAHEAD >= 3) {
+    if (ahead >= 3) { wait_vm_lgkm0<3 * L>(); return; }
+  }
+  if constexpr (MAXAHEAD >= 2) {
+    if (ahead >= 2) { wait_vm_lgkm0<2 * L>(); return; }
+  }
+  if constexpr (MAXAHEAD >= 1) {
+    if (ahead >= 1) { wait_vm_lgkm0<L>(); return; }
+  }
+  wait_vm_lgkm0<0>();
+}
+
+__device__ __forceinline__ float bf16_lo(unsigned v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned v) { return __uint_as_float(v & 0xffff0000u); }
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+  bf16x2 p = {to_bf16(a), to_bf16(b)};
+  return *reinterpret_cast<unsigned*>(&p);
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI>
+__global__ void __launch_bounds__(WGM * WGN * 64, 1)
 lowrank_gemm_kernel(const LowrankGemmArgs g) {
-  using TL = Tile<BM, BN, BK, WGM, WGN>;
-  constexpr int NTH = TL::NTH, WM = TL::WM, WN = TL::WN, FM = TL::FM, FN = TL::FN, CH = TL::CH;
-  __shared__ __attribute__((aligned(16))) bf16 sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) bf16 sB[2][BN * BK];
+  using C = Cfg<BM, BN, BK, STAGES, WGM, WGN>;
+  constexpr int FM = C::FM, FN = C::FN, WM = C::WM, WN = C::WN, CW = C::CW;
+  constexpr int SUB = BK / 32;
+  __shared__ __attribute__((aligned(1024))) bf16 smem[STAGES * C::STAGE];
+  __shared__ __attribute__((aligned(16))) float ep_a[BN];             // a_p over the tile's columns
+  __shared__ __attribute__((aligned(16))) float ep_b[BN];             // bf16(b_next) (EPI_RELU2)
+  __shared__ float ep_u[C::UGROUPS][BM];                               // partial sums of x.b per row
+  __shared__ float ep_sign;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
-  const int tiles_n = g.N / BN;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = g.N / BN, ntiles = tiles_m * tiles_n;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nslots = gridDim.x >> 3;
+  const int t_lo = (int)((long)xcd * ntiles / 8), t_hi = (int)((long)(xcd + 1) * ntiles / 8);
+  const int KT = g.K / BK, KS = KT * SUB;
 
-  // Per-thread source rows of the global->LDS copies (fixed across the K loop): thread tid copies
-  // chunk (tid % CH) of rows tid / CH + i * (NTH / CH).
-  constexpr int RSTEP = NTH / CH;
-  const int cchunk = tid % CH, r0 = tid / CH;
-  const bf16* a_src = nullptr;
-  long a_step[TL::A_LOADS];
+  // ---- per-tile DMA sources. Instruction d of this wave fills LDS rows
+  // R = (wave * L + d) * ROWS_PER_DMA + lane / CPR at physical chunk lane % CPR, i.e. logical k chunk
+  // (lane % CPR) ^ ((R / RPL) % CPR).
+  const int lrow = lane / C::CPR;
+  long a_src[C::LA];
+  const bf16* b_src[C::LB];
+  auto set_sources = [&](int m0, int n0) {
 #pragma unroll
-  for (int i = 0; i < TL::A_LOADS; ++i) {
-    const int row = min(m0 + r0 + i * RSTEP, g.M - 1);
-    const long off = (long)(row / g.T) * g.a_mstride + (long)(row % g.T) * g.lda + cchunk * 8;
-    a_step[i] = off;
-  }
-  a_src = g.A;
-  const bf16* b_src = g.W + (long)(n0 + r0) * g.ldw + cchunk * 8;
-  const long b_rstep = (long)RSTEP * g.ldw;
-  u32x4 ra[TL::A_LOADS], rb[TL::B_LOADS];
-#define GLOAD(k0)                                                                                   \
-  do {                                                                                              \
-    _Pragma("unroll") for (int i = 0; i < TL::A_LOADS; ++i)                                        \
-      ra[i] = *reinterpret_cast<const u32x4*>(a_src + a_step[i] + (k0));                            \
-    _Pragma("unroll") for (int i = 0; i < TL::B_LOADS; ++i)                                        \
-      rb[i] = *reinterpret_cast<const u32x4*>(b_src + i * b_rstep + (k0));                          \
-  } while (0)
-#define SSTORE(buf)                                                                                 \
-  do {                                                                                              \
-    _Pragma("unroll") for (int i = 0; i < TL::A_LOADS; ++i)                                        \
-      *reinterpret_cast<u32x4*>(&sA[buf][swz(r0 + i * RSTEP, cchunk)]) = ra[i];                     \
-    _Pragma("unroll") for (int i = 0; i < TL::B_LOADS; ++i)                                        \
-      *reinterpret_cast<u32x4*>(&sB[buf][swz(r0 + i * RSTEP, cchunk)]) = rb[i];                     \
-  } while (0)
-
-  f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int KT = g.K / BK;
-  GLOAD(0);
-  SSTORE(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) GLOAD((kt + 1) * BK);
-    const bf16* a_s = sA[buf];
-    const bf16* b_s = sB[buf];
-#pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      const int c = kk * 4 + (lane >> 4);
-      bf16x8 af[FM], bw[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * WM + i * 16 + (lane & 15);
-        af[i] = *reinterpret_cast<const bf16x8*>(&a_s[swz(r, c)]);
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int r = wn * WN + j * 16 + (lane & 15);
-        bw[j] = *reinterpret_cast<const bf16x8*>(&b_s[swz(r, c)]);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bw[j], acc[i][j]);
+    for (int d = 0; d < C::LA; ++d) {
+      const int r = (wave * C::LA + d) * C::ROWS_PER_DMA + lrow;
+      const int c = (lane % C::CPR) ^ ((r / C::RPL) % C::CPR);
+      const int row = min(m0 + r, g.M - 1);
+      a_src[d] = (long)(row / g.T) * g.a_mstride + (long)(row % g.T) * g.lda + c * 8;
     }
-    if (kt + 1 < KT) SSTORE(buf ^ 1);
-    __syncthreads();
-  }
+#pragma unroll
+    for (int d = 0; d < C::LB; ++d) {
+      const int R = (wave * C::LB + d) * C::ROWS_PER_DMA + lrow;
+      const int c = (lane % C::CPR) ^ ((R / C::RPL) % C::CPR);
+      const int loc = R % WN, r = loc & 15;
+      const int n = n0 + (R - loc) + (r >> 2) * CW + (loc >> 4) * 4 + (r & 3);
+      b_src[d] = g.W + (long)n * g.ldw + c * 8;
+    }
+  };
+  auto issue = [&](int kt, int buf) {
+    bf16* sx = smem + buf * C::STAGE;
+    bf16* sw = sx + BM * BK;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int d = 0; d < C::LA; ++d)
+      __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + k0),
+                                       (lds_void_t*)(sx + (wave * C::LA + d) * 512), 16, 0, 0);
+#pragma unroll
+    for (int d = 0; d < C::LB; ++d)
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[d] + k0),
+                                       (lds_void_t*)(sw + (wave * C::LB + d) * 512), 16, 0, 0);
+  };
 
-#undef GLOAD
-#undef SSTORE
-  // ---- epilogue. Lane holds C[row = 4*(lane>>4) + e][col = lane & 15] of each 16x16 block.
-  const int col_base = n0 + wn * WN + (lane & 15);
+  // ---- epilogue vectors of a tile, loaded into registers ahead of time and staged through LDS.
+  // Thread tid sums x.b partial group tid / BM of row tid % BM; threads [0, BN/4) fetch a float4 of
+  // a_p, threads [BN/4, BN/2) a float4 of b_next; thread 0 the sign (whole tile in one member only).
+  float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f);
+  float pre_u = 0.f, pre_sign = 0.f;
+  auto prefetch_ep = [&](int m0, int n0) {
+    const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
+    const int dir = pfirst >> g.pair_shift;
+    if (tid < BN / 4) {
+      pre_ab = *reinterpret_cast<const float4*>(g.ra + (long)dir * g.ra_ld + n0 + 4 * tid);
+    } else if (EPI == EPI_RELU2 && tid < BN / 2) {
+      pre_ab = *reinterpret_cast<const float4*>(g.rb_next + (long)dir * g.rb_next_ld + n0 + 4 * (tid - BN / 4));
+    }
+    if (tid == 0) pre_sign = pfirst == plast ? g.sign[pfirst] : 0.f;
+    const int row = min(m0 + tid % BM, g.M - 1), grp = tid / BM;
+    const int q0 = grp * g.u_parts / C::UGROUPS, q1 = (grp + 1) * g.u_parts / C::UGROUPS;
+    const float* up = g.u + (long)row * g.u_parts;
+    float u = 0.f;
+    for (int q = q0; q < q1; ++q) u += up[q];
+    pre_u = u;
+  };
+  auto stage_ep = [&]() {
+    if (tid < BN / 4) {
+      *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
+    } else if (EPI == EPI_RELU2 && tid < BN / 2) {
+      const float4 b = pre_ab;
+      *reinterpret_cast<float4*>(&ep_b[4 * (tid - BN / 4)]) = make_float4(bf16r(b.x), bf16r(b.y), bf16r(b.z), bf16r(b.w));
+    }
+    if (tid == 0) ep_sign = pre_sign;
+    ep_u[tid / BM][tid % BM] = pre_u;
+  };
+
+  // ---- MFMA operands of one 32-deep k step: x rows wm*WM + 16 i + (lane & 15) and W rows
+  // wn*WN + 16 j + (lane & 15), k chunk kk * 4 + lane / 16.
+  const int xrow0 = wm * WM + (lane & 15), wrow0 = wn * WN + (lane & 15);
+  auto read_w = [&](bf16x8 (&w)[FN], int buf, int kk) {
+    const bf16* sw = smem + buf * C::STAGE + BM * BK;
+    const int c = kk * 4 + (lane >> 4);
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+    for (int j = 0; j < FN; ++j) w[j] = *reinterpret_cast<const bf16x8*>(&sw[swz<BK>(wrow0 + j * 16, c)]);
+  };
+  auto read_x = [&](bf16x8& x, int buf, int kk, int i) {
+    const bf16* sx = smem + buf * C::STAGE;
+    x = *reinterpret_cast<const bf16x8*>(&sx[swz<BK>(xrow0 + i * 16, kk * 4 + (lane >> 4))]);
+  };
+  f32x4 acc[FM][FN];
+  bf16x8 wa[FN], wb[FN], xf[FM];
+
+  // Make step t's stage readable: when t opens a new stage, wait for its DMA, barrier, and refill the
+  // stage retired by the previous step. Before the wait for stage kt, the stages issued are
+  // 0 .. STAGES-1 (prologue) and kt-2+STAGES at most (refills of the earlier opens), so
+  // min(KT-1, max(STAGES-1, kt-2+STAGES)) - kt later stages may stay in flight.
+  auto open = [&](int t) {
+    if (t % SUB == 0) {
+      const int kt = t / SUB;
+      wait_stage<C::L, STAGES - 1>(min(KT - 1, max(STAGES - 1, kt - 2 + STAGES)) - kt);
+      __builtin_amdgcn_s_barrier();
+      if (kt >= 1 && kt - 1 + STAGES < KT) issue(kt - 1 + STAGES, (kt - 1) % STAGES);
+    }
+  };
+  // Step t's MFMAs with (wc, xf) while step t + 1's operands are read into (wn_, xf).
+  auto step_read = [&](int t, const bf16x8 (&wc)[FN], bf16x8 (&wn_)[FN]) {
+    open(t + 1);
+    const int buf = ((t + 1) / SUB) % STAGES, kk = (t + 1) % SUB;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + e;
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(wc[j], xf[i], acc[i][j]);
+      if (i == 0) read_w(wn_, buf, kk);
+      read_x(xf[i], buf, kk, i);
+    }
+  };
+  auto step_last = [&](const bf16x8 (&wc)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(wc[j], xf[i], acc[i][j]);
+  };
+
+  int tile = t_lo + slot;
+  if (tile >= t_hi) return;
+  {
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    prefetch_ep(m0, n0);
+    set_sources(m0, n0);
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+      if (s < KT) issue(s, s);
+  }
+  while (true) {
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    // the previous tile's epilogue has finished reading the staged vectors
+    wait_vm_lgkm0<63>();
+    __builtin_amdgcn_s_barrier();
+    stage_ep();
+
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    open(0);
+    read_w(wa, 0, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) read_x(xf[i], 0, 0, i);
+    // KS is even (K % 64 == 0): pairs of steps alternate the W register sets; the last step reads
+    // nothing.
+    for (int t = 0; t < KS - 2; t += 2) {
+      step_read(t, wa, wb);
+      step_read(t + 1, wb, wa);
+    }
+    step_read(KS - 2, wa, wb);
+    step_last(wb);
+
+    // every wave has read the ring for the last time: prefetch the next tile
+    const int next = tile + nslots;
+    wait_vm_lgkm0<63>();
+    __builtin_amdgcn_s_barrier();
+    if (next < t_hi) {
+      const int nm0 = (next / tiles_n) * BM, nn0 = (next % tiles_n) * BN;
+      prefetch_ep(nm0, nn0);
+      set_sources(nm0, nn0);
+#pragma unroll
+      for (int s = 0; s < STAGES; ++s)
+        if (s < KT) issue(s, s);
+    }
+
+    // ---- epilogue. Lane holds, for token row m0 + wm*WM + i*16 + (lane & 15), the output columns
+    // cb .. cb + CW - 1 with cb = n0 + wn*WN + (lane >> 4) * CW; acc[i][j][e] is column cb + 4j + e.
+    const int lcol = wn * WN + (lane >> 4) * CW, cb = n0 + lcol;
+    const bool uniform = m0 / g.T == min(m0 + BM - 1, g.M - 1) / g.T;
+    const float s_uni = ep_sign;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int lr = wm * WM + i * 16 + (lane & 15), row = m0 + lr;
       const bool live = row < g.M;
-      const int rrow = live ? row : g.M - 1;
-      const int p = rrow / g.T;
-      const int dir = p >> g.pair_shift;
       float u = 0.f;
-      for (int j = 0; j < g.u_parts; ++j) u += g.u[(long)rrow * g.u_parts + j];
-      const float su = g.sign[p] * bf16r(u);
-      const float* arow = g.ra + (long)dir * g.ra_ld;
-      float dot = 0.f;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col = col_base + j * 16;
-        const float v = bf16r(acc[i][j][e]) + su * arow[col];
+      for (int q = 0; q < C::UGROUPS; ++q) u += ep_u[q][lr];
+      float sgn = s_uni;
+      int dir = 0;
+      if (!uniform) {  // tile straddles members: per-row vectors come from global memory
+        const int p = (live ? row : g.M - 1) / g.T;
+        dir = p >> g.pair_shift;
+        sgn = g.sign[p];
+      }
+      const float su = sgn * bf16r(u);
+      float dot = 0.f;
+      // two 4-column blocks at a time: 8 outputs -> one 16-byte bf16 store or two fp32 stores
+#pragma unroll
+      for (int j = 0; j < FN; j += 2) {
+        float av[8], bv[8], v[8];
+        if (uniform) {
+          const float4 a0 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j]);
+          const float4 a1 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j + 4]);
+          av[0] = a0.x, av[1] = a0.y, av[2] = a0.z, av[3] = a0.w, av[4] = a1.x, av[5] = a1.y, av[6] = a1.z, av[7] = a1.w;
+          if constexpr (EPI == EPI_RELU2) {
+            const float4 b0 = *reinterpret_cast<const float4*>(&ep_b[lcol + 4 * j]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&ep_b[lcol + 4 * j + 4]);
+            bv[0] = b0.x, bv[1] = b0.y, bv[2] = b0.z, bv[3] = b0.w, bv[4] = b1.x, bv[5] = b1.y, bv[6] = b1.z, bv[7] = b1.w;
+          }
+        } else {
+          const float* arow = g.ra + (long)dir * g.ra_ld + cb + 4 * j;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) av[e] = arow[e];
+          if constexpr (EPI == EPI_RELU2) {
+            const float* brow = g.rb_next + (long)dir * g.rb_next_ld + cb + 4 * j;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = bf16r(brow[e]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = bf16r(acc[i][j][e]) + su * av[e];
+          v[4 + e] = bf16r(acc[i][j + 1][e]) + su * av[4 + e];
+        }
         if constexpr (EPI == EPI_STORE) {
           if (live) {
-            if (g.out_f32) g.out_f32[(long)row * g.ldo + col] = v;
-            if (g.out_bf16) g.out_bf16[(long)row * g.ldo + col] = to_bf16(v);
+            if (g.out_f32) {
+              float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb + 4 * j);
+              o[0] = make_float4(v[0], v[1], v[2], v[3]);
+              o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+            if (g.out_bf16) {
+              *reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb + 4 * j) =
+                  make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7]));
+            }
           }
-        } else if constexpr (EPI == EPI_RELU2) {
-          const float r = fmaxf(v, 0.f);
-          const bf16 hb = to_bf16(r * r);
-          if (live) g.out_bf16[(long)row * g.ldo + col] = hb;
-          dot += (float)hb * bf16r(g.rb_next[(long)dir * g.rb_next_ld + col]);
+        } else if constexpr (EPI == EPI_RESID) {
+          if (live) {
+            float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb + 4 * j);
+            float4 r0 = o[0], r1 = o[1];
+            r0.x += v[0], r0.y += v[1], r0.z += v[2], r0.w += v[3];
+            r1.x += v[4], r1.y += v[5], r1.z += v[6], r1.w += v[7];
+            o[0] = r0;
+            o[1] = r1;
+          }
         } else {
-          if (live) g.out_f32[(long)row * g.ldo + col] += v;
+          unsigned hp[4];
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float r0v = fmaxf(v[e], 0.f), r1v = fmaxf(v[e + 1], 0.f);
+            const unsigned h2 = pack_bf16(r0v * r0v, r1v * r1v);
+            hp[e / 2] = h2;
+            dot += bf16_lo(h2) * bv[e] + bf16_hi(h2) * bv[e + 1];
+          }
+          if (live)
+            *reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb + 4 * j) = make_uint4(hp[0], hp[1], hp[2], hp[3]);
         }
       }
       if constexpr (EPI == EPI_RELU2) {
-        dot = group_sum<16>(dot);
-        if (live && (lane & 15) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = dot;
+        dot += __shfl_xor(dot, 16, 64);
+        dot += __shfl_xor(dot, 32, 64);
+        if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = dot;
       }
     }
+    if (next >= t_hi) break;
+    tile = next;
   }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int EPI>
+// Tile configurations: <BM, BN, BK, STAGES, WGM, WGN>.
+#ifndef NOISE_GEMM_CFG
+#define NOISE_GEMM_CFG 0
+#endif
+#if NOISE_GEMM_CFG == 0
+#define CFG_BIG 256, 256, 32, 4, 2, 4
+#define CFG_SMALL 256, 128, 32, 4, 4, 2
+#elif NOISE_GEMM_CFG == 1
+#define CFG_BIG 256, 256, 64, 2, 2, 4
+#define CFG_SMALL 256, 128, 64, 2, 4, 2
+#elif NOISE_GEMM_CFG == 3
+#define CFG_BIG 256, 256, 32, 3, 2, 4
+#define CFG_SMALL 256, 128, 32, 3, 4, 2
+#endif
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
+constexpr int cfg_wave_n() { return BN / WGN; }
+
+int num_cus() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI>
 int launch_cfg(const LowrankGemmArgs& g, hipStream_t stream) {
-  if (g.N % BN || g.K % BK) return NOISE_ENOTSUP;
-  const int tiles = ((g.M + BM - 1) / BM) * (g.N / BN);
-  hipLaunchKernelGGL((lowrank_gemm_kernel<BM, BN, BK, WGM, WGN, EPI>), dim3(tiles), dim3(WGM * WGN * 64), 0,
-                     stream, g);
+  if (g.N % BN || g.K % 64) return NOISE_ENOTSUP;
+  const long tiles = (long)((g.M + BM - 1) / BM) * (g.N / BN);
+  if (tiles > 0x7fffffffL) return NOISE_ENOTSUP;
+  // one persistent workgroup per CU (LDS admits no second one), a multiple of 8 for the XCD split
+  long grid = std::min<long>(num_cus(), tiles);
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL((lowrank_gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, EPI>), dim3((unsigned)grid),
+                     dim3(WGM * WGN * 64), 0, stream, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
 
+bool use_big(int N) { return N % 256 == 0; }
+
 template <int EPI>
 int launch_epi(const LowrankGemmArgs& g, hipStream_t stream) {
-  return launch_cfg<128, 128, 64, 2, 2, EPI>(g, stream);
+  if (use_big(g.N)) return launch_cfg<CFG_BIG, EPI>(g, stream);
+  return launch_cfg<CFG_SMALL, EPI>(g, stream);
 }
 
 }  // namespace
 
-int lowrank_gemm_wave_n() { return 64; }
+int lowrank_gemm_parts(int N) {
+  if (N <= 0 || N % 128) return 0;
+  return use_big(N) ? N / cfg_wave_n<CFG_BIG>() : N / cfg_wave_n<CFG_SMALL>();
+}
 
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.ra || !g.u ||
       g.u_parts <= 0 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
-      g.pair_shift < 0 || g.pair_shift > 1)
+      g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64)
     return NOISE_EINVAL;
-  if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return NOISE_EINVAL;
+  if (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.ra) & 15) return NOISE_EINVAL;
+  if (((uintptr_t)g.out_f32 | (uintptr_t)g.out_bf16) & 15) return NOISE_EINVAL;
   switch (epi) {
     case EPI_STORE:
       if (!g.out_f32 && !g.out_bf16) return NOISE_EINVAL;
       return launch_epi<EPI_STORE>(g, stream);
     case EPI_RELU2:
-      if (!g.out_bf16 || !g.rb_next || !g.upart_out || g.upart_ld != g.N / lowrank_gemm_wave_n())
+      if (!g.out_bf16 || !g.rb_next || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N) ||
+          g.rb_next_ld % 4 || ((uintptr_t)g.rb_next & 15))
         return NOISE_EINVAL;
       return launch_epi<EPI_RELU2>(g, stream);
     case EPI_RESID:
