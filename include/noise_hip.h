@@ -1,13 +1,17 @@
-/* C ABI of libnoise_hip.so: the MI355X (gfx950) population-perturbed forward of the Noise 37.7M GPT.
+/* C ABI of libnoise_hip.so: the MI355X (gfx950) population-perturbed forward of the Noise 37.7M GPT
+ * and the EGGROLL update (fitness -> gradient estimate -> Adam).
  *
  * Conventions for every entry point:
  *  - pointers are device pointers (hipMalloc / torch CUDA tensors); bf16 buffers are passed as void*;
  *  - "members" are the population rows; member p uses perturbation row dir = p >> pair_shift
  *    (pair_shift = 1 when antithetic pairs 2j, 2j+1 share a_j, b_j, as train/val/eggroll.py:140-141
- *    builds them; 0 when a, b are given per member) and sign[p] = +-sigma;
- *  - rank-1 vectors follow the reference orientation (train/val/eggroll.py:56-58): for a weight
- *    W [out, in], `a` is [dirs, out] (output side) and `b` is [dirs, in] (input side);
- *  - activations are row-major [members * T, width]; member p owns rows p*T .. p*T+T-1;
+ *    builds them; 0 when a, b are given per member, as population_loss receives them) and
+ *    sign[p] = +-sigma (train/val/eggroll.py:138);
+ *  - rank-1 vectors follow the reference orientation (train/val/eggroll.py:56-63): for a weight
+ *    W [out, in], `a` is [dirs, out] (output side) and `b` is [dirs, in] (input side); for an
+ *    embedding W [V, d], `a` is [dirs, V] and `b` is [dirs, d];
+ *  - activations are row-major [members * T, width]; member p owns rows p*T .. p*T+T-1; width 512
+ *    (d_model) unless stated;
  *  - work is enqueued on `stream` (a hipStream_t); nothing is synchronised, nothing allocated: any
  *    scratch comes from the caller's workspace, sized by the matching *_workspace_size query;
  *  - return 0 on success, a negative NOISE_E* code for a rejected argument, or a positive hipError_t.
@@ -15,6 +19,7 @@
 #ifndef NOISE_HIP_H
 #define NOISE_HIP_H
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -25,16 +30,21 @@ extern "C" {
 #define NOISE_ENOSPC (-2)
 #define NOISE_ENOTSUP (-3)
 
+#define NOISE_FITNESS_ZSCORE 0 /* train/val/eggroll.py:151-152 */
+#define NOISE_FITNESS_RANK 1   /* centred ranks, ties by index (config-4 option) */
+
 typedef void* noise_stream_t; /* hipStream_t */
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int noise_version(void);
 
+/* ---------------------------------------------------------------- rank-1 perturbed linears */
+
 /* y = x W^T + s_p (x . b_p) a_p^T per member, autocast rounding points: bf16 GEMM output, the GEMV
  * x.b rounded to bf16, the correction added in fp32.
  * Replaces `lowrank` (train/val/eggroll.py:56-58).
  *   x       bf16 [members, T, in], row r of member p at x + p*x_mstride + t*x_ld (x_mstride 0: one
- *           activation shared by every member)
+ *           activation shared by every member); in % 64 == 0, out % 128 == 0
  *   w       bf16 [out, in]
  *   y_f32   fp32 [members*T, out] (nullable); accumulate != 0 adds into it (residual update)
  *   y_bf16  bf16 [members*T, out] (nullable)
@@ -52,13 +62,107 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
  *   x       bf16 [members, T, d] (x_mstride as above)
  *   w_fc    bf16 [f, d];  a_fc [dirs, f], b_fc [dirs, d]
  *   w_proj  bf16 [d, f];  a_proj [dirs, d], b_proj [dirs, f]
- *   y_f32 / y_bf16 / accumulate as in noise_lowrank_linear; d % 128 == 0, f % 128 == 0.
+ *   y_f32 / y_bf16 / accumulate as in noise_lowrank_linear; d % 128 == 0, f % 256 == 0.
  * Workspace: noise_lowrank_mlp_workspace_size(). */
 int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* bytes);
 int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc, const void* w_proj, int d, int f,
                       const float* a_fc, const float* b_fc, const float* a_proj, const float* b_proj,
                       const float* sign, int members, int T, int pair_shift, float* y_f32, void* y_bf16,
                       int accumulate, void* workspace, size_t workspace_bytes, noise_stream_t stream);
+
+/* ---------------------------------------------------------------- population forward, per stage
+ * The stages below compose `population_loss` (train/val/eggroll.py:66-103) block by block; the host
+ * (noise_amd/population.py) calls them in the reference's order. */
+
+/* fp32 -> bf16 cast of n values (weights, once per step). split_cols > 0 writes the fp32-head
+ * operand instead: each row of split_cols values becomes [bf16(w) | bf16(w - bf16(w)) | bf16(w)]
+ * (out holds 3 n values). */
+int noise_cast_bf16(const float* in, void* out, long n, int split_cols, noise_stream_t stream);
+
+/* x0 = norm(W[idx] + s_p a_p[idx] b_p) fp32 [members*T, 512].
+ * Replaces `norm(lowrank_embed(p['transformer.wte.weight'], ...))` (train/val/eggroll.py:61-63, :74). */
+int noise_embed_norm(const float* w, long vocab, const float* a, const float* b, const float* sign,
+                     const int64_t* idx, int members, int T, int pair_shift, float* x0, noise_stream_t stream);
+
+/* Block entry: x_out = (lambda_r + s eps_r[dir]) x_in + (lambda_0 + s eps_0[dir]) x0; h = bf16(norm(x_out));
+ * lambda_r / lambda_0 point at this block's entries of resid_lambdas / x0_lambdas (device memory);
+ * u_qkv[row, 0..2] = bf16(h . bf16(b_{q,k,v}[dir])) (row stride 4); when gate_w is not null the value
+ * gate gate[row, 0..7] = 2 sigmoid(lowrank(h[:32], gate_w, gate_a, gate_b)).
+ * Replaces train/val/eggroll.py:76-84, :88. eps_r / eps_0 point at this block's column of the
+ * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. */
+int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h, float* u_qkv, const float* b_q,
+                      const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
+                      const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
+                      const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
+                      noise_stream_t stream);
+
+/* q | k | v = lowrank(h, [W_q; W_k; W_v]) with per-segment a vectors and the u_qkv dots, then rotary +
+ * QK RMSNorm on q and k (utils/model.py:55-58, :46-47; train/val/eggroll.py:90) and, when gate is not
+ * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89). Output bf16
+ * [members*T, 1536] (q | k | v, head h at columns h*64 of each segment).
+ *   w_qkv    bf16 [1536, 512] = c_q ; c_k ; c_v
+ *   rot_cos / rot_sin  bf16 [>= T, 32] (utils/model.py:177-183) */
+int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
+              const float* u_qkv, const float* sign, int members, int T, int pair_shift, const void* rot_cos,
+              const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
+              const float* ve_b, const int64_t* idx, void* qkv, noise_stream_t stream);
+
+/* Windowed causal attention on the q | k | v rows (8 heads x 64): y bf16 [members*T, 512]; a query at s
+ * sees keys s - window .. s (utils/model.py:14-31). When b_proj is not null, writes the c_proj
+ * input-side dot partials upart [members*T, 8]. When mom is not null, writes per-(member, head)
+ * means over tokens of y and y^2, mom [members, 8, 2, 64] ("credit moments"; no reference
+ * function), using mom_work (noise_attention_workspace_size bytes). T % 128 == 0. */
+int noise_attention_workspace_size(int members, int T, size_t* bytes);
+int noise_attention(const void* qkv, int members, int T, int window, const float* b_proj, int pair_shift,
+                    void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
+                    noise_stream_t stream);
+
+/* resid += lowrank(x, w) with the input-side dot given as u_parts partial sums per row (u [rows,
+ * u_parts]): the attention c_proj (u from noise_attention) and the MLP c_proj.
+ * Replaces `x = x + linear('attn.c_proj.weight', y)` (train/val/eggroll.py:92). */
+int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,
+                        const float* sign, int members, int T, int pair_shift, float* resid, noise_stream_t stream);
+
+/* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). */
+int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
+                   int pair_shift, noise_stream_t stream);
+
+/* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] and its dot partials with b_proj
+ * (upart [members*T, noise_mlp_fc_parts(f)]) for the following noise_lowrank_resid. */
+int noise_mlp_fc_parts(int f);
+int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
+                 const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
+                 float* upart, noise_stream_t stream);
+
+/* Per-member mean soft-capped cross-entropy (train/val/eggroll.py:94-103): h = norm(x);
+ * z = h W^T + s (h . b) a; z' = 15 tanh(z / 15); loss[p] = mean_t(logsumexp(z'_t) - z'_t[target_t]).
+ *   fp32_head != 0: w_head is the [vocab, 1536] split operand from noise_cast_bf16(split_cols = 512)
+ *                   and the head is fp32-accurate (~2^-16 relative); 0: w_head bf16 [vocab, 512]
+ *                   with the reference's autocast rounding points.
+ * vocab % 256 == 0. Workspace: noise_head_ce_workspace_size(). */
+int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes);
+int noise_head_ce(const float* x, const void* w_head, int vocab, int fp32_head, const float* a, const float* b,
+                  const float* sign, const int64_t* targets, int members, int T, int pair_shift, float* loss,
+                  void* workspace, size_t workspace_bytes, noise_stream_t stream);
+
+/* ---------------------------------------------------------------- EGGROLL update */
+
+/* fitness[j] = L[2j+1] - L[2j] transformed by mode (z-score: divided by the unbiased std + 1e-8, no
+ * centering; rank: centred ranks); weight[d] = sum of fitness[j] over j = d mod pairs.
+ * Replaces train/val/eggroll.py:151-154. n = number of losses (even, >= 4). */
+int noise_fitness(const float* losses, int n, int pairs, int mode, float* fitness, float* weight,
+                  noise_stream_t stream);
+
+/* grad[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions; a null means out == 1 and
+ * a_j = 1 (the lambda noise). Replaces the update loop of train/val/eggroll.py:155-166 with
+ * scale = -1 / len(fitness). */
+int noise_outer_update(const float* a, long a_ld, const float* b, long b_ld, const float* w, int ndir, int out,
+                       int in, float scale, float* grad, noise_stream_t stream);
+
+/* One torch.optim.AdamW step with weight_decay 0 on n fp32 values (train/val/eggroll.py:205, :167):
+ * step_size = lr / (1 - beta1^t), bc2_sqrt = sqrt(1 - beta2^t). */
+int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
+               float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream);
 
 #ifdef __cplusplus
 }

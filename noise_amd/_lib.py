@@ -10,22 +10,41 @@ import torch  # noqa: F401  (must precede the HIP library load: one libamdhip64 
 
 LIB_PATH = Path(__file__).resolve().parent / 'libnoise_hip.so'
 
-_c_int, _c_long, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
-_fp = ctypes.POINTER(ctypes.c_float)
+I, L, F, S, P = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+SP = ctypes.POINTER(ctypes.c_size_t)
 
 ERRORS = {-1: 'NOISE_EINVAL (rejected argument)', -2: 'NOISE_ENOSPC (workspace too small)',
           -3: 'NOISE_ENOTSUP (shape outside the kernel tiling)'}
 
-# name -> argtypes; every entry point returns int.
+FITNESS_ZSCORE, FITNESS_RANK = 0, 1
+
+# name -> argtypes in declaration order; every entry point returns int. Pointers (device buffers,
+# the stream) are c_void_p.
 SIGNATURES = {
     'noise_version': [],
-    'noise_lowrank_linear_workspace_size': [_c_int, _c_int, ctypes.POINTER(_c_size)],
-    'noise_lowrank_linear': [_vp, _c_long, _c_long, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
-                             _vp, _vp, _c_int, _vp, _c_size, _vp],
-    'noise_lowrank_mlp_workspace_size': [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
-    'noise_lowrank_mlp': [_vp, _c_long, _c_long, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int,
-                          _c_int, _c_int, _vp, _vp, _c_int, _vp, _c_size, _vp],
+    'noise_lowrank_linear_workspace_size': [I, I, SP],
+    'noise_lowrank_linear': [P, L, L, P, I, I, P, P, P, I, I, I, P, P, I, P, S, P],
+    'noise_lowrank_mlp_workspace_size': [I, I, I, I, SP],
+    'noise_lowrank_mlp': [P, L, L, P, P, I, I, P, P, P, P, P, I, I, I, P, P, I, P, S, P],
+    'noise_cast_bf16': [P, P, L, I, P],
+    'noise_embed_norm': [P, L, P, P, P, P, I, I, I, P, P],
+    'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P],
+    'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, P, P],
+    'noise_attention_workspace_size': [I, I, SP],
+    'noise_attention': [P, I, I, I, P, I, P, P, P, P, S, P],
+    'noise_lowrank_resid': [P, P, I, I, P, P, I, P, I, I, I, P, P],
+    'noise_norm_dot': [P, P, P, P, P, I, I, I, P],
+    'noise_mlp_fc_parts': [I],
+    'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, P, P],
+    'noise_head_ce_workspace_size': [I, I, I, I, SP],
+    'noise_head_ce': [P, P, I, I, P, P, P, P, I, I, I, P, P, S, P],
+    'noise_fitness': [P, I, I, I, P, P, P],
+    'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
+    'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
+
+# Entry points whose int result is a value, not a status.
+VALUE_RESULT = {'noise_version', 'noise_mlp_fc_parts'}
 
 _lib = None
 
@@ -46,7 +65,7 @@ def load(path=None):
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = _c_int
+        fn.restype = I
     if path is None:
         _lib = lib
     return lib
@@ -63,7 +82,11 @@ def call(name, *args):
     check(getattr(load(), name)(*args), name)
 
 
+def value(name, *args):
+    return getattr(load(), name)(*args)
+
+
 def size_query(name, *args):
-    out = _c_size(0)
+    out = S(0)
     call(name, *args, ctypes.byref(out))
     return out.value

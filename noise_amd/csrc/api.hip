@@ -1,7 +1,10 @@
 // extern "C" entry points of libnoise_hip.so (declared in include/noise_hip.h).
 #include "../../include/noise_hip.h"
+#include "attention.h"
 #include "common.h"
+#include "eggroll.h"
 #include "gemm.h"
+#include "rowops.h"
 
 namespace {
 
@@ -18,7 +21,7 @@ struct Carve {
   }
 };
 
-constexpr int EPI_STORE = 0, EPI_RELU2 = 1, EPI_RESID = 2;
+constexpr int DM = 512, NH = 8;
 
 LowrankGemmArgs base_args(const void* x, long x_ld, long x_mstride, const void* w, int in, int out, const float* a,
                           const float* sign, int members, int T, int pair_shift) {
@@ -34,16 +37,22 @@ LowrankGemmArgs base_args(const void* x, long x_ld, long x_mstride, const void* 
   g.T = T;
   g.pair_shift = pair_shift;
   g.sign = sign;
-  g.ra = a;
+  g.ra[0] = a;
+  g.seg_n = out;
   g.ra_ld = out;
+  g.round_bf16 = 1;
   return g;
+}
+
+bool bad_members(int members, int T, int pair_shift) {
+  return members <= 0 || T <= 0 || pair_shift < 0 || pair_shift > 1 || (long)members * T > 0x7fffffffL;
 }
 
 }  // namespace
 
 extern "C" {
 
-int noise_version(void) { return 100; }
+int noise_version(void) { return 200; }
 
 int noise_lowrank_linear_workspace_size(int members, int T, size_t* bytes) {
   if (members <= 0 || T <= 0 || !bytes) return NOISE_EINVAL;
@@ -59,6 +68,7 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
                          noise_stream_t stream) {
   size_t need = 0;
   if (int rc = noise_lowrank_linear_workspace_size(members, T, &need)) return rc;
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
   if (accumulate && (!y_f32 || y_bf16)) return NOISE_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -70,6 +80,7 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
   LowrankGemmArgs g = base_args(x, x_ld, x_mstride, w, in, out, a, sign, members, T, pair_shift);
   g.u = u;
   g.u_parts = 1;
+  g.u_ld = 1;
   g.out_f32 = y_f32;
   g.out_bf16 = static_cast<bf16*>(y_bf16);
   g.ldo = out;
@@ -77,12 +88,12 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
 }
 
 int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* bytes) {
-  if (members <= 0 || T <= 0 || d <= 0 || f <= 0 || !bytes) return NOISE_EINVAL;
+  if (members <= 0 || T <= 0 || d <= 0 || f <= 0 || !bytes || !lowrank_gemm_parts(f)) return NOISE_EINVAL;
   const size_t M = (size_t)members * T;
   Carve c(nullptr);
-  c.take<float>(M);                                    // u_fc
-  c.take<float>(M * lowrank_gemm_parts(f));            // partial dots h.b_proj
-  c.take<bf16>(M * f);                                  // hidden h
+  c.take<float>(M);                            // u_fc
+  c.take<float>(M * lowrank_gemm_parts(f));    // partial dots h.b_proj
+  c.take<bf16>(M * f);                         // hidden h
   *bytes = c.used;
   return NOISE_OK;
 }
@@ -93,8 +104,9 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
                       int accumulate, void* workspace, size_t workspace_bytes, noise_stream_t stream) {
   size_t need = 0;
   if (int rc = noise_lowrank_mlp_workspace_size(members, T, d, f, &need)) return rc;
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
-  if (!lowrank_gemm_parts(f) || (accumulate && (!y_f32 || y_bf16))) return NOISE_EINVAL;
+  if (accumulate && (!y_f32 || y_bf16)) return NOISE_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t M = (size_t)members * T;
   Carve c(workspace);
@@ -107,6 +119,7 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   LowrankGemmArgs g1 = base_args(x, x_ld, x_mstride, w_fc, d, f, a_fc, sign, members, T, pair_shift);
   g1.u = u_fc;
   g1.u_parts = 1;
+  g1.u_ld = 1;
   g1.out_bf16 = hid;
   g1.ldo = f;
   g1.rb_next = b_proj;
@@ -117,10 +130,215 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   LowrankGemmArgs g2 = base_args(hid, f, (long)T * f, w_proj, f, d, a_proj, sign, members, T, pair_shift);
   g2.u = upart;
   g2.u_parts = parts;
+  g2.u_ld = parts;
   g2.out_f32 = y_f32;
   g2.out_bf16 = static_cast<bf16*>(y_bf16);
   g2.ldo = d;
   return lowrank_gemm_launch(accumulate ? EPI_RESID : EPI_STORE, g2, s);
+}
+
+int noise_cast_bf16(const float* in, void* out, long n, int split_cols, noise_stream_t stream) {
+  return cast_launch(in, static_cast<bf16*>(out), n, split_cols, split_cols > 0, static_cast<hipStream_t>(stream));
+}
+
+int noise_embed_norm(const float* w, long vocab, const float* a, const float* b, const float* sign,
+                     const int64_t* idx, int members, int T, int pair_shift, float* x0, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  EmbedNormArgs g{w, a, b, vocab, sign, idx, members * T, T, pair_shift, x0};
+  return embed_norm_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h, float* u_qkv, const float* b_q,
+                      const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
+                      const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
+                      const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
+                      noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  BlockEntryArgs g{};
+  g.x_in = x_in;
+  g.x0 = x0;
+  g.x_out = x_out;
+  g.h = static_cast<bf16*>(h);
+  g.u_qkv = u_qkv;
+  g.b_qkv[0] = b_q;
+  g.b_qkv[1] = b_k;
+  g.b_qkv[2] = b_v;
+  g.lambda_r = lambda_r;
+  g.lambda_0 = lambda_0;
+  g.eps_r = eps_r;
+  g.eps_0 = eps_0;
+  g.eps_ld = eps_ld;
+  g.sign = sign;
+  g.M = members * T;
+  g.T = T;
+  g.pair_shift = pair_shift;
+  g.gate_w = gate_w;
+  g.gate_a = gate_a;
+  g.gate_b = gate_b;
+  g.gate = gate;
+  return block_entry_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
+              const float* u_qkv, const float* sign, int members, int T, int pair_shift, const void* rot_cos,
+              const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
+              const float* ve_b, const int64_t* idx, void* qkv, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  LowrankGemmArgs g = base_args(h, DM, (long)T * DM, w_qkv, DM, 3 * DM, a_q, sign, members, T, pair_shift);
+  g.ra[1] = a_k;
+  g.ra[2] = a_v;
+  g.seg_n = DM;
+  g.ra_ld = DM;
+  g.u = u_qkv;
+  g.u_parts = 1;
+  g.u_ld = 4;
+  g.out_bf16 = static_cast<bf16*>(qkv);
+  g.ldo = 3 * DM;
+  g.rot_cos = static_cast<const bf16*>(rot_cos);
+  g.rot_sin = static_cast<const bf16*>(rot_sin);
+  g.gate = gate;
+  g.ve_w = ve_w;
+  g.ve_a = ve_a;
+  g.ve_b = ve_b;
+  g.ve_v = vocab;
+  g.idx = idx;
+  return lowrank_gemm_launch(EPI_QKV, g, static_cast<hipStream_t>(stream));
+}
+
+int noise_attention_workspace_size(int members, int T, size_t* bytes) {
+  if (members <= 0 || T <= 0 || !bytes) return NOISE_EINVAL;
+  *bytes = (size_t)attention_moment_partials(members, T, NH) * sizeof(float);
+  return NOISE_OK;
+}
+
+int noise_attention(const void* qkv, int members, int T, int window, const float* b_proj, int pair_shift,
+                    void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
+                    noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  if (mom) {
+    size_t need = 0;
+    noise_attention_workspace_size(members, T, &need);
+    if (!mom_work || mom_work_bytes < need) return NOISE_ENOSPC;
+  }
+  if ((b_proj == nullptr) != (upart == nullptr)) return NOISE_EINVAL;
+  AttnArgs g{};
+  g.qkv = static_cast<const bf16*>(qkv);
+  g.ldq = 3 * DM;
+  g.koff = DM;
+  g.voff = 2 * DM;
+  g.y = static_cast<bf16*>(y);
+  g.ldy = DM;
+  g.members = members;
+  g.T = T;
+  g.H = NH;
+  g.window = window;
+  g.b_proj = b_proj;
+  g.b_ld = DM;
+  g.pair_shift = pair_shift;
+  g.upart = upart;
+  g.upart_ld = NH;
+  g.mom = mom ? static_cast<float*>(mom_work) : nullptr;
+  g.mom_out = mom;
+  return attention_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,
+                        const float* sign, int members, int T, int pair_shift, float* resid, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift) || u_parts <= 0) return NOISE_EINVAL;
+  LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, a, sign, members, T, pair_shift);
+  g.u = u;
+  g.u_parts = u_parts;
+  g.u_ld = u_parts;
+  g.out_f32 = resid;
+  g.ldo = out;
+  return lowrank_gemm_launch(EPI_RESID, g, static_cast<hipStream_t>(stream));
+}
+
+int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
+                   int pair_shift, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  NormDotArgs g{x, static_cast<bf16*>(h), b, u, sign, members * T, T, pair_shift};
+  return norm_dot_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_mlp_fc_parts(int f) { return lowrank_gemm_parts(f); }
+
+int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
+                 const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
+                 float* upart, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift) || !lowrank_gemm_parts(f)) return NOISE_EINVAL;
+  LowrankGemmArgs g = base_args(h, d, (long)T * d, w_fc, d, f, a_fc, sign, members, T, pair_shift);
+  g.u = u;
+  g.u_parts = 1;
+  g.u_ld = 1;
+  g.out_bf16 = static_cast<bf16*>(hidden);
+  g.ldo = f;
+  g.rb_next = b_proj;
+  g.rb_next_ld = f;
+  g.upart_out = upart;
+  g.upart_ld = lowrank_gemm_parts(f);
+  return lowrank_gemm_launch(EPI_RELU2, g, static_cast<hipStream_t>(stream));
+}
+
+int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes) {
+  if (members <= 0 || T <= 0 || !bytes || !lowrank_gemm_parts(vocab)) return NOISE_EINVAL;
+  const size_t M = (size_t)members * T;
+  Carve c(nullptr);
+  c.take<bf16>(M * (fp32_head ? 3 : 1) * DM);      // head operand
+  c.take<float>(M);                                // h . b
+  c.take<float>(M * lowrank_gemm_parts(vocab));    // partial sums of exp(z')
+  c.take<float>(M);                                // z' at the target
+  *bytes = c.used;
+  return NOISE_OK;
+}
+
+int noise_head_ce(const float* x, const void* w_head, int vocab, int fp32_head, const float* a, const float* b,
+                  const float* sign, const int64_t* targets, int members, int T, int pair_shift, float* loss,
+                  void* workspace, size_t workspace_bytes, noise_stream_t stream) {
+  size_t need = 0;
+  if (int rc = noise_head_ce_workspace_size(members, T, vocab, fp32_head, &need)) return rc;
+  if (bad_members(members, T, pair_shift) || !x || !w_head || !loss) return NOISE_EINVAL;
+  if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t M = (size_t)members * T;
+  const int K = (fp32_head ? 3 : 1) * DM, parts = lowrank_gemm_parts(vocab);
+  Carve c(workspace);
+  bf16* hop = c.take<bf16>(M * K);
+  float* u = c.take<float>(M);
+  float* part = c.take<float>(M * parts);
+  float* tgt = c.take<float>(M);
+  HeadNormArgs hn{x, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
+  if (int rc = head_norm_launch(hn, s)) return rc;
+  LowrankGemmArgs g = base_args(hop, K, (long)T * K, w_head, K, vocab, a, sign, members, T, pair_shift);
+  g.u = u;
+  g.u_parts = 1;
+  g.u_ld = 1;
+  g.round_bf16 = fp32_head ? 0 : 1;
+  g.targets = targets;
+  g.ce_tgt = tgt;
+  g.upart_out = part;
+  g.upart_ld = parts;
+  g.ldo = vocab;
+  if (int rc = lowrank_gemm_launch(EPI_CE, g, s)) return rc;
+  CeFinalizeArgs f{part, tgt, parts, members, T, loss};
+  return ce_finalize_launch(f, s);
+}
+
+int noise_fitness(const float* losses, int n, int pairs, int mode, float* fitness, float* weight,
+                  noise_stream_t stream) {
+  return fitness_launch(losses, n, pairs, mode, fitness, weight, static_cast<hipStream_t>(stream));
+}
+
+int noise_outer_update(const float* a, long a_ld, const float* b, long b_ld, const float* w, int ndir, int out,
+                       int in, float scale, float* grad, noise_stream_t stream) {
+  OuterUpdateArgs g{a, a_ld, b, b_ld, w, ndir, out, in, scale, grad};
+  return outer_update_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
+               float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream) {
+  AdamArgs g{param, grad, exp_avg, exp_avg_sq, n, step_size, beta1, beta2, eps, bc2_sqrt};
+  return adam_launch(g, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -1,0 +1,26 @@
+// Internal interface of the attention kernel (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+
+struct AttnArgs {
+  const __bf16* qkv;  // [members * T, ldq] rows; q at column h*64, k at koff + h*64, v at voff + h*64
+  long ldq;
+  int koff, voff;
+  __bf16* y;          // [members * T, ldy], head h at columns h*64 .. h*64+63
+  long ldy;
+  int members, T, H, window;
+  // c_proj input-side dot partials: upart[row * upart_ld + h] = sum_d y[row, h*64+d] bf16(b_proj[dir, h*64+d])
+  const float* b_proj;
+  long b_ld;
+  int pair_shift;
+  float* upart;       // nullable
+  int upart_ld;
+  // per-(member, head) moments of y over tokens: partials [members, H, T/128, 2, 64] reduced into
+  // mom_out [members, H, 2, 64] (mean of y, mean of y^2); nullable
+  float* mom;
+  float* mom_out;
+};
+
+// Floats of the moment partials workspace.
+long attention_moment_partials(int members, int T, int H);
+int attention_launch(const AttnArgs& g, hipStream_t s);

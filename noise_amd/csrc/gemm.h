@@ -1,6 +1,18 @@
 // Internal interface of the low-rank-perturbed GEMM (not part of the C ABI).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// Epilogue kinds of lowrank_gemm_launch.
+enum : int {
+  EPI_STORE = 0,  // out = lowrank(x)                       -> fp32 and/or bf16 store
+  EPI_RELU2 = 1,  // h = bf16(relu(lowrank(x))^2)            -> bf16 store + partial dots h.b_next per row
+  EPI_RESID = 2,  // resid += lowrank(x)                     -> fp32 read-modify-write
+  EPI_QKV = 3,    // q|k|v = lowrank(x) per 512-column segment; rotary + RMSNorm on q and k, gated value
+                  // embedding added to v                   -> bf16 store
+  EPI_CE = 4,     // z = 15 tanh(lowrank(x) / 15); per row partial sum of exp(z) over each wave's columns
+                  // and z at the target column             -> fp32 partials
+};
 
 struct LowrankGemmArgs {
   // A operand: row r (member p = r / T, token t = r % T) starts at A + p * a_mstride + t * lda.
@@ -11,28 +23,44 @@ struct LowrankGemmArgs {
   const __bf16* W;  // [N, K], K contiguous (nn.Linear orientation)
   long ldw;
   int M, N, K;
-  int T;           // rows per member
-  int pair_shift;  // perturbation row of member p is p >> pair_shift (1: antithetic pairs share a, b)
+  int T;              // rows per member
+  int pair_shift;     // perturbation row of member p is p >> pair_shift (1: antithetic pairs share a, b)
   const float* sign;  // [members] +-sigma
-  const float* ra;    // output-side vectors a, row dir at ra + dir * ra_ld, N entries
+  // Output-side rank-1 vectors, per column segment of seg_n columns: column n of member p uses
+  // ra[n / seg_n][dir(p) * ra_ld + n % seg_n]. One segment unless EPI_QKV.
+  const float* ra[3];
+  int seg_n;
   long ra_ld;
-  const float* u;     // input-side dots x.b per row, as u_parts partial sums: u[row * u_parts + j]
+  // Input-side dots x.b, as u_parts partial sums: row r, segment s: sum_q u[r * u_ld + s * u_parts + q].
+  const float* u;
   int u_parts;
+  int u_ld;
+  // 1: autocast rounding points (the dense product and the dot rounded to bf16); 0: fp32 throughout.
+  int round_bf16;
   // outputs
   float* out_f32;     // EPI_STORE (optional) / EPI_RESID (accumulated in place)
-  __bf16* out_bf16;   // EPI_STORE (optional) / EPI_RELU2
+  __bf16* out_bf16;   // EPI_STORE (optional) / EPI_RELU2 / EPI_QKV
   long ldo;
   // EPI_RELU2: partial dots of the bf16 output with the next layer's input-side vector b_next
   const float* rb_next;
   long rb_next_ld;
   float* upart_out;   // [M, upart_ld]
   int upart_ld;       // = lowrank_gemm_parts(N)
+  // EPI_QKV: rotary tables (bf16 [>= T, 32]); optional gated value embedding for the v segment:
+  // v += gate[r, head] * (ve_w[idx[t]] + s_p ve_a[dir, idx[t]] ve_b[dir]).
+  const __bf16* rot_cos;
+  const __bf16* rot_sin;
+  const float* gate;     // [M, 8] (null: no value embedding)
+  const float* ve_w;     // [V, 512]
+  const float* ve_a;     // [dirs, V]
+  const float* ve_b;     // [dirs, 512]
+  long ve_v;             // V (row stride of ve_a)
+  const int64_t* idx;    // [T] token ids
+  // EPI_CE: targets [T]; partial sums of exp(z) [M, upart_ld]; z at the target [M]
+  const int64_t* targets;
+  float* ce_tgt;
 };
 
-// Number of partial row dots EPI_RELU2 writes per row for an N-column output (0: N unsupported).
+// Number of per-row partials EPI_RELU2 / EPI_CE write for an N-column output (0: N unsupported).
 int lowrank_gemm_parts(int N);
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream);
-
-// Row dots u[row] = bf16(sum_k x[row, k] * bf16(b[dir, k])) for a bf16 activation (rowops.hip).
-int rowdot_launch(const __bf16* x, long ldx, long x_mstride, int M, int K, int T, int pair_shift,
-                  const float* b, long ldb, float* u, hipStream_t stream);

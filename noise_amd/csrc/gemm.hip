@@ -41,13 +41,6 @@
 
 namespace {
 
-// Epilogue kinds.
-enum : int {
-  EPI_STORE = 0,   // out = lowrank(x)            -> fp32 and/or bf16 store
-  EPI_RELU2 = 1,   // h = bf16(relu(lowrank(x))^2) -> bf16 store + partial dots h.b_next per row
-  EPI_RESID = 2,   // resid += lowrank(x)          -> fp32 read-modify-write
-};
-
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
@@ -172,16 +165,16 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   float pre_u = 0.f, pre_sign = 0.f;
   auto prefetch_ep = [&](int m0, int n0) {
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
-    const int dir = pfirst >> g.pair_shift;
+    const int dir = pfirst >> g.pair_shift, seg = n0 / g.seg_n, ncol = n0 - seg * g.seg_n;
     if (tid < BN / 4) {
-      pre_ab = *reinterpret_cast<const float4*>(g.ra + (long)dir * g.ra_ld + n0 + 4 * tid);
+      pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
     } else if (EPI == EPI_RELU2 && tid < BN / 2) {
       pre_ab = *reinterpret_cast<const float4*>(g.rb_next + (long)dir * g.rb_next_ld + n0 + 4 * (tid - BN / 4));
     }
     if (tid == 0) pre_sign = pfirst == plast ? g.sign[pfirst] : 0.f;
     const int row = min(m0 + tid % BM, g.M - 1), grp = tid / BM;
     const int q0 = grp * g.u_parts / C::UGROUPS, q1 = (grp + 1) * g.u_parts / C::UGROUPS;
-    const float* up = g.u + (long)row * g.u_parts;
+    const float* up = g.u + (long)row * g.u_ld + seg * g.u_parts;
     float u = 0.f;
     for (int q = q0; q < q1; ++q) u += up[q];
     pre_u = u;
@@ -294,90 +287,146 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     // ---- epilogue. Lane holds, for token row m0 + wm*WM + i*16 + (lane & 15), the output columns
     // cb .. cb + CW - 1 with cb = n0 + wn*WN + (lane >> 4) * CW; acc[i][j][e] is column cb + 4j + e.
     const int lcol = wn * WN + (lane >> 4) * CW, cb = n0 + lcol;
+    const int seg = n0 / g.seg_n, scol = cb - seg * g.seg_n;  // column inside the segment
     const bool uniform = m0 / g.T == min(m0 + BM - 1, g.M - 1) / g.T;
     const float s_uni = ep_sign;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int lr = wm * WM + i * 16 + (lane & 15), row = m0 + lr;
       const bool live = row < g.M;
+      const int rrow = live ? row : g.M - 1;
       float u = 0.f;
 #pragma unroll
       for (int q = 0; q < C::UGROUPS; ++q) u += ep_u[q][lr];
       float sgn = s_uni;
-      int dir = 0;
-      if (!uniform) {  // tile straddles members: per-row vectors come from global memory
-        const int p = (live ? row : g.M - 1) / g.T;
-        dir = p >> g.pair_shift;
-        sgn = g.sign[p];
-      }
-      const float su = sgn * bf16r(u);
-      float dot = 0.f;
-      // two 4-column blocks at a time: 8 outputs -> one 16-byte bf16 store or two fp32 stores
+      const int p = rrow / g.T, dir = p >> g.pair_shift;
+      if (!uniform) sgn = g.sign[p];  // tile straddles members: per-row vectors from global memory
+      const float su = sgn * (g.round_bf16 ? bf16r(u) : u);
+      // v = dense + s u a over the lane's CW columns
+      float v[CW];
 #pragma unroll
-      for (int j = 0; j < FN; j += 2) {
-        float av[8], bv[8], v[8];
+      for (int j = 0; j < FN; ++j) {
+        float av[4];
         if (uniform) {
-          const float4 a0 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j]);
-          const float4 a1 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j + 4]);
-          av[0] = a0.x, av[1] = a0.y, av[2] = a0.z, av[3] = a0.w, av[4] = a1.x, av[5] = a1.y, av[6] = a1.z, av[7] = a1.w;
-          if constexpr (EPI == EPI_RELU2) {
-            const float4 b0 = *reinterpret_cast<const float4*>(&ep_b[lcol + 4 * j]);
-            const float4 b1 = *reinterpret_cast<const float4*>(&ep_b[lcol + 4 * j + 4]);
-            bv[0] = b0.x, bv[1] = b0.y, bv[2] = b0.z, bv[3] = b0.w, bv[4] = b1.x, bv[5] = b1.y, bv[6] = b1.z, bv[7] = b1.w;
-          }
+          const float4 a4 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j]);
+          av[0] = a4.x, av[1] = a4.y, av[2] = a4.z, av[3] = a4.w;
         } else {
-          const float* arow = g.ra + (long)dir * g.ra_ld + cb + 4 * j;
+          const float* arow = g.ra[seg] + (long)dir * g.ra_ld + scol + 4 * j;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) av[e] = arow[e];
-          if constexpr (EPI == EPI_RELU2) {
-            const float* brow = g.rb_next + (long)dir * g.rb_next_ld + cb + 4 * j;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) bv[e] = bf16r(brow[e]);
-          }
+          for (int e = 0; e < 4; ++e) av[e] = arow[e];
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = bf16r(acc[i][j][e]) + su * av[e];
-          v[4 + e] = bf16r(acc[i][j + 1][e]) + su * av[4 + e];
-        }
-        if constexpr (EPI == EPI_STORE) {
-          if (live) {
-            if (g.out_f32) {
-              float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb + 4 * j);
-              o[0] = make_float4(v[0], v[1], v[2], v[3]);
-              o[1] = make_float4(v[4], v[5], v[6], v[7]);
-            }
-            if (g.out_bf16) {
-              *reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb + 4 * j) =
-                  make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7]));
-            }
-          }
-        } else if constexpr (EPI == EPI_RESID) {
-          if (live) {
-            float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb + 4 * j);
-            float4 r0 = o[0], r1 = o[1];
-            r0.x += v[0], r0.y += v[1], r0.z += v[2], r0.w += v[3];
-            r1.x += v[4], r1.y += v[5], r1.z += v[6], r1.w += v[7];
-            o[0] = r0;
-            o[1] = r1;
-          }
-        } else {
-          unsigned hp[4];
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float r0v = fmaxf(v[e], 0.f), r1v = fmaxf(v[e + 1], 0.f);
-            const unsigned h2 = pack_bf16(r0v * r0v, r1v * r1v);
-            hp[e / 2] = h2;
-            dot += bf16_lo(h2) * bv[e] + bf16_hi(h2) * bv[e + 1];
-          }
-          if (live)
-            *reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb + 4 * j) = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-        }
+        for (int e = 0; e < 4; ++e) v[4 * j + e] = (g.round_bf16 ? bf16r(acc[i][j][e]) : acc[i][j][e]) + su * av[e];
       }
-      if constexpr (EPI == EPI_RELU2) {
+      if constexpr (EPI == EPI_STORE) {
+        if (live) {
+          if (g.out_f32) {
+            float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) o[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+          }
+          if (g.out_bf16) {
+            uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+#pragma unroll
+            for (int e = 0; e < CW; e += 8)
+              o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
+                                    pack_bf16(v[e + 6], v[e + 7]));
+          }
+        }
+      } else if constexpr (EPI == EPI_RESID) {
+        if (live) {
+          float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb);
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            float4 r = o[j];
+            r.x += v[4 * j];
+            r.y += v[4 * j + 1];
+            r.z += v[4 * j + 2];
+            r.w += v[4 * j + 3];
+            o[j] = r;
+          }
+        }
+      } else if constexpr (EPI == EPI_RELU2) {
+        float dot = 0.f;
+        unsigned hp[CW / 2];
+#pragma unroll
+        for (int e = 0; e < CW; e += 2) {
+          float b0, b1;
+          if (uniform) {
+            b0 = ep_b[lcol + e], b1 = ep_b[lcol + e + 1];
+          } else {
+            const float* brow = g.rb_next + (long)dir * g.rb_next_ld + cb;
+            b0 = bf16r(brow[e]), b1 = bf16r(brow[e + 1]);
+          }
+          const float r0v = fmaxf(v[e], 0.f), r1v = fmaxf(v[e + 1], 0.f);
+          const unsigned h2 = pack_bf16(r0v * r0v, r1v * r1v);
+          hp[e / 2] = h2;
+          dot += bf16_lo(h2) * b0 + bf16_hi(h2) * b1;
+        }
+        if (live) {
+          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+#pragma unroll
+          for (int e = 0; e < CW / 2; e += 4) o[e / 4] = make_uint4(hp[e], hp[e + 1], hp[e + 2], hp[e + 3]);
+        }
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
         if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = dot;
+      } else if constexpr (EPI == EPI_QKV) {
+        // the wave's WN = 64 columns are one head; lane group lane / 16 holds head dims 16 (lane / 16) ..
+        const int t = rrow % g.T;
+        if (seg < 2) {
+          // rotary (utils/model.py:55-58): dims d and d + 32 pair up, held by lanes l and l ^ 32
+          const int dd = (lane >> 4) * CW & 31;
+          const bool first = (lane >> 4) < 2;
+          const __bf16* cr = g.rot_cos + (long)t * 32 + dd;
+          const __bf16* sr = g.rot_sin + (long)t * 32 + dd;
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < CW; ++e) {
+            const float partner = __shfl_xor(v[e], 32, 64);
+            const float c = (float)cr[e], sn = (float)sr[e];
+            const float y = first ? v[e] * c + partner * sn : v[e] * c - partner * sn;
+            v[e] = y;
+            ss += y * y;
+          }
+          // QK RMSNorm over the head's 64 dims (eps = 2^-23, utils/model.py:46-47)
+          ss += __shfl_xor(ss, 16, 64);
+          ss += __shfl_xor(ss, 32, 64);
+          const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f);
+#pragma unroll
+          for (int e = 0; e < CW; ++e) v[e] *= r;
+        } else if (g.gate) {
+          // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
+          const long tok = g.idx[t];
+          const float gt = g.gate[(long)rrow * 8 + scol / 64];
+          const float sa = sgn * g.ve_a[(long)dir * g.ve_v + tok];
+          const float* wr = g.ve_w + tok * 512 + scol;
+          const float* br = g.ve_b + (long)dir * 512 + scol;
+#pragma unroll
+          for (int e = 0; e < CW; ++e) v[e] += gt * (wr[e] + sa * br[e]);
+        }
+        if (live) {
+          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+#pragma unroll
+          for (int e = 0; e < CW; e += 8)
+            o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
+                                  pack_bf16(v[e + 6], v[e + 7]));
+        }
+      } else {  // EPI_CE
+        // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,
+        // so the sum of exp(z') over 4096 columns needs no running maximum.
+        const long tg = g.targets[rrow % g.T];
+        float se = 0.f;
+#pragma unroll
+        for (int e = 0; e < CW; ++e) {
+          const float ez = __expf(v[e] * (2.f / 15.f));
+          const float zc = 15.f - 30.f / (ez + 1.f);
+          se += __expf(zc);
+          if (live && tg == cb + e) g.ce_tgt[row] = zc;
+        }
+        se += __shfl_xor(se, 16, 64);
+        se += __shfl_xor(se, 32, 64);
+        if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = se;
       }
     }
     if (next >= t_hi) break;
@@ -444,11 +493,16 @@ int lowrank_gemm_parts(int N) {
 }
 
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.ra || !g.u ||
-      g.u_parts <= 0 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
-      g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64)
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
+      g.u_ld < g.u_parts || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
+      g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
+      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.N / g.seg_n > 3)
     return NOISE_EINVAL;
-  if (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.ra) & 15) return NOISE_EINVAL;
+  const int nseg = g.N / g.seg_n;
+  if (g.u_ld < nseg * g.u_parts) return NOISE_EINVAL;
+  for (int s = 0; s < nseg; ++s)
+    if (!g.ra[s] || ((uintptr_t)g.ra[s] & 15)) return NOISE_EINVAL;
+  if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return NOISE_EINVAL;
   if (((uintptr_t)g.out_f32 | (uintptr_t)g.out_bf16) & 15) return NOISE_EINVAL;
   switch (epi) {
     case EPI_STORE:
@@ -462,6 +516,14 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     case EPI_RESID:
       if (!g.out_f32) return NOISE_EINVAL;
       return launch_epi<EPI_RESID>(g, stream);
+    case EPI_QKV:
+      if (!g.out_bf16 || g.seg_n != 512 || nseg != 3 || !g.rot_cos || !g.rot_sin ||
+          (g.gate && (!g.ve_w || !g.ve_a || !g.ve_b || !g.idx || g.ve_v <= 0)))
+        return NOISE_EINVAL;
+      return launch_epi<EPI_QKV>(g, stream);
+    case EPI_CE:
+      if (!g.targets || !g.ce_tgt || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N)) return NOISE_EINVAL;
+      return launch_epi<EPI_CE>(g, stream);
   }
   return NOISE_EINVAL;
 }

@@ -1,0 +1,73 @@
+// Internal interface of the row kernels (not part of the C ABI). Rows are [M = members x T, 512];
+// member p = row / T uses perturbation row dir = p >> pair_shift and sign[p].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct EmbedNormArgs {
+  const float* w;        // [V, 512] embedding table
+  const float* a;        // [dirs, V] output-side (row) vectors
+  const float* b;        // [dirs, 512] input-side vectors
+  long V;
+  const float* sign;
+  const int64_t* idx;    // [T]
+  int M, T, pair_shift;
+  float* x0;             // [M, 512] fp32 out
+};
+
+struct BlockEntryArgs {
+  const float* x_in;     // [M, 512] residual stream before the mix (x0 itself at block 0)
+  const float* x0;
+  float* x_out;          // mixed stream (may alias x_in)
+  __bf16* h;             // [M, 512] bf16(norm(x))
+  float* u_qkv;          // [M, 4] bf16-rounded dots with b_q, b_k, b_v (4th slot zero)
+  const float* b_qkv[3];  // [dirs, 512] each
+  const float* lambda_r;  // this block's resid_lambdas / x0_lambdas entries
+  const float* lambda_0;
+  const float* eps_r;    // resid_lambdas noise: eps_r[dir * eps_ld]
+  const float* eps_0;
+  long eps_ld;
+  const float* sign;
+  int M, T, pair_shift;
+  // value-embedding gate (null gate_w: none at this block)
+  const float* gate_w;   // [8, 32]
+  const float* gate_a;   // [dirs, 8]
+  const float* gate_b;   // [dirs, 32]
+  float* gate;           // [M, 8] 2 sigmoid(...)
+};
+
+struct NormDotArgs {
+  const float* x;
+  __bf16* h;
+  const float* b;        // [dirs, 512]
+  float* u;              // [M]
+  const float* sign;
+  int M, T, pair_shift;
+};
+
+struct HeadNormArgs {
+  const float* x;
+  __bf16* h;             // fp32 head: [M, 1536] = [hi | hi | lo]; bf16 head: [M, 512]
+  const float* b;        // [dirs, 512]
+  float* u;              // [M]
+  const float* sign;
+  int M, T, pair_shift;
+  int fp32_head;
+};
+
+struct CeFinalizeArgs {
+  const float* part;     // [members * T, parts] sums of exp(z)
+  const float* tgt;      // [members * T] z at the target
+  int parts, members, T;
+  float* loss;           // [members]
+};
+
+int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s);
+int block_entry_launch(const BlockEntryArgs& g, hipStream_t s);
+int norm_dot_launch(const NormDotArgs& g, hipStream_t s);
+int head_norm_launch(const HeadNormArgs& g, hipStream_t s);
+int ce_finalize_launch(const CeFinalizeArgs& g, hipStream_t s);
+int cast_launch(const float* in, __bf16* out, long n, int cols, int split, hipStream_t s);
+// Row dots u[row] = bf16(sum_k x[row, k] * bf16(b[dir, k])) for a bf16 activation.
+int rowdot_launch(const __bf16* x, long ldx, long x_mstride, int M, int K, int T, int pair_shift,
+                  const float* b, long ldb, float* u, hipStream_t stream);

@@ -1,11 +1,270 @@
-// Row-wise kernels of the population forward (HBM-bound; one wave per row group).
+// Row kernels of the population forward: embedding gather + RMSNorm, the per-block residual mix +
+// RMSNorm + rank-1 dots, the final RMSNorm feeding the head, and the cross-entropy finalisation.
+//
+// All of them are HBM-bound: one wave owns one 512-wide row (8 contiguous elements per lane), reads
+// it once and writes what the next GEMM needs (bf16 operand, the x.b dots its epilogue adds).
+// Rounding points follow the reference under bf16 autocast (train/val/eggroll.py:144): the residual
+// stream and norms are fp32, a GEMM operand is the bf16 rounding of its fp32 input, and the rank-1
+// GEMV x @ b is bf16 x bf16 with fp32 accumulation, rounded to bf16.
 #include "common.h"
 #include "gemm.h"
+#include "rowops.h"
 
 namespace {
 
-// u[row] = bf16(sum_k x[row, k] * bf16(b[dir, k])): the rank-1 GEMV `x @ b` of `lowrank`
-// (train/val/eggroll.py:58) under autocast (bf16 operands, fp32 accumulation, bf16 result).
+constexpr int D = 512;
+constexpr float NORM_EPS = 1.1920928955078125e-07f;  // finfo(float32).eps: F.rms_norm default
+
+struct Row8 {
+  float v[8];
+};
+
+__device__ __forceinline__ Row8 load8(const float* p) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  return Row8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+}
+__device__ __forceinline__ void store8(float* p, const Row8& r) {
+  *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
+}
+__device__ __forceinline__ void store8_bf16(bf16* p, const Row8& r) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = to_bf16(r.v[e]);
+  *reinterpret_cast<bf16x8*>(p) = o;
+}
+// RMSNorm of a 512-wide row spread 8 per lane over one wave: x * rsqrt(mean(x^2) + eps), fp32.
+__device__ __forceinline__ void rms_norm_row(Row8& r) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += r.v[e] * r.v[e];
+  ss = group_sum<64>(ss);
+  const float s = rsqrtf(ss * (1.f / D) + NORM_EPS);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r.v[e] *= s;
+}
+// bf16(sum_c bf16(h_c) bf16(b_c)) over the row: the autocast rank-1 GEMV.
+__device__ __forceinline__ float dot_bf16(const Row8& h, const float* b) {
+  const Row8 bv = load8(b);
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc += bf16r(h.v[e]) * bf16r(bv.v[e]);
+  return bf16r(group_sum<64>(acc));
+}
+
+// x0 = norm(W[idx] + s a[:, idx] b) (train/val/eggroll.py:61-63, :74).
+__global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int p = (int)(row / g.T), t = (int)(row % g.T), dir = p >> g.pair_shift;
+  const long tok = g.idx[t];
+  const float sa = g.sign[p] * g.a[(long)dir * g.V + tok];
+  Row8 w = load8(g.w + tok * D + lane * 8);
+  const Row8 b = load8(g.b + (long)dir * D + lane * 8);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w.v[e] = w.v[e] + sa * b.v[e];
+  rms_norm_row(w);
+  store8(g.x0 + row * D + lane * 8, w);
+}
+
+// Block entry (train/val/eggroll.py:77-88): x = (l_r + s e_r) x + (l_0 + s e_0) x0; h = norm(x);
+// q/k/v input-side dots; the value-embedding gate 2 sigmoid(lowrank(h[:32], ve_gate)).
+__global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  const float s = g.sign[p];
+  const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
+  const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
+  Row8 x = load8(g.x_in + row * D + lane * 8);
+  const Row8 x0 = load8(g.x0 + row * D + lane * 8);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x.v[e] = lr * x.v[e] + l0 * x0.v[e];
+  store8(g.x_out + row * D + lane * 8, x);
+  rms_norm_row(x);
+  store8_bf16(g.h + row * D + lane * 8, x);
+  float u[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) u[k] = dot_bf16(x, g.b_qkv[k] + (long)dir * D + lane * 8);
+  if (lane == 0) {
+    float* ur = g.u_qkv + row * 4;
+    ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = 0.f;
+  }
+  if (g.gate_w) {
+    // lanes 0..3 hold h[:32]; every lane computes one (gate head, partial) product set
+    float hv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hv[e] = bf16r(x.v[e]);
+    float ub = 0.f;
+    if (lane < 4) {
+      const float* br = g.gate_b + (long)dir * 32 + lane * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ub += hv[e] * bf16r(br[e]);
+    }
+    ub = group_sum<4>(ub);  // lanes 0..3 now all hold sum over the 32 gate channels
+    const float ubr = bf16r(ub);
+    float z[8];
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      float d = 0.f;
+      if (lane < 4) {
+        const float* wr = g.gate_w + hh * 32 + lane * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d += hv[e] * bf16r(wr[e]);
+      }
+      z[hh] = group_sum<4>(d);
+    }
+    if (lane == 0) {
+      const float* ar = g.gate_a + (long)dir * 8;
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh) {
+        const float gl = bf16r(z[hh]) + s * ubr * ar[hh];
+        g.gate[row * 8 + hh] = 2.f / (1.f + __expf(-gl));
+      }
+    }
+  }
+}
+
+// h = norm(x) as the bf16 operand of the next GEMM, plus its input-side dot (MLP entry,
+// train/val/eggroll.py:93).
+__global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  Row8 x = load8(g.x + row * D + lane * 8);
+  rms_norm_row(x);
+  store8_bf16(g.h + row * D + lane * 8, x);
+  const float u = dot_bf16(x, g.b + (long)dir * D + lane * 8);
+  if (lane == 0) g.u[row] = u;
+}
+
+// Final norm feeding the head (train/val/eggroll.py:94-99). fp32 head: the operand is the bf16
+// split [hi | hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)) against [W_hi | W_lo | W_hi], so one
+// bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16 relative; the dot h.b is fp32. bf16 head: the
+// operand is bf16(h) and the dot follows autocast.
+__global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  Row8 x = load8(g.x + row * D + lane * 8);
+  rms_norm_row(x);
+  if (g.fp32_head) {
+    Row8 lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
+    bf16* o = g.h + row * (3 * D) + lane * 8;
+    store8_bf16(o, x);
+    store8_bf16(o + D, x);
+    store8_bf16(o + 2 * D, lo);
+    const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += x.v[e] * bv.v[e];
+    acc = group_sum<64>(acc);
+    if (lane == 0) g.u[row] = acc;
+  } else {
+    store8_bf16(g.h + row * D + lane * 8, x);
+    const float u = dot_bf16(x, g.b + (long)dir * D + lane * 8);
+    if (lane == 0) g.u[row] = u;
+  }
+}
+
+// Per-member mean cross-entropy (train/val/eggroll.py:101-102): row r's loss is
+// log(sum_j part[r, j]) - z[r, target]; one workgroup sums its member's T rows in a fixed order.
+__global__ void __launch_bounds__(256) ce_finalize_kernel(CeFinalizeArgs g) {
+  __shared__ float red[256];
+  const int p = blockIdx.x, tid = threadIdx.x;
+  float acc = 0.f;
+  for (int t = tid; t < g.T; t += 256) {
+    const long row = (long)p * g.T + t;
+    const float* pr = g.part + row * g.parts;
+    float s = 0.f;
+    for (int j = 0; j < g.parts; ++j) s += pr[j];
+    acc += __logf(s) - g.tgt[row];
+  }
+  red[tid] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) g.loss[p] = red[0] / (float)g.T;
+}
+
+// fp32 -> bf16 (round to nearest even); with split != 0 also writes [hi | lo | hi] rows of width
+// `cols` (the fp32 head operand): out row r = [bf16(w_r) | bf16(w_r - bf16(w_r)) | bf16(w_r)].
+__global__ void __launch_bounds__(256) cast_kernel(const float* __restrict__ in, bf16* __restrict__ out, long n, int cols,
+                                                   int split) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = in[i];
+  const bf16 hi = to_bf16(v);
+  if (!split) {
+    out[i] = hi;
+    return;
+  }
+  const long r = i / cols, c = i % cols;
+  bf16* o = out + r * 3 * cols + c;
+  o[0] = hi;
+  o[cols] = to_bf16(v - (float)hi);
+  o[2 * cols] = hi;
+}
+
+int grid_rows(long M) { return (int)((M + 3) / 4); }
+
+}  // namespace
+
+int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s) {
+  if (g.M <= 0 || g.T <= 0 || !g.w || !g.a || !g.b || !g.sign || !g.idx || !g.x0 || g.V <= 0) return NOISE_EINVAL;
+  hipLaunchKernelGGL(embed_norm_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
+  if (g.M <= 0 || g.T <= 0 || !g.x_in || !g.x0 || !g.x_out || !g.h || !g.u_qkv || !g.sign || !g.eps_r || !g.eps_0 ||
+      !g.lambda_r || !g.lambda_0 || !g.b_qkv[0] || !g.b_qkv[1] || !g.b_qkv[2])
+    return NOISE_EINVAL;
+  if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate)) return NOISE_EINVAL;
+  hipLaunchKernelGGL(block_entry_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+int norm_dot_launch(const NormDotArgs& g, hipStream_t s) {
+  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign) return NOISE_EINVAL;
+  hipLaunchKernelGGL(norm_dot_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+int head_norm_launch(const HeadNormArgs& g, hipStream_t s) {
+  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign) return NOISE_EINVAL;
+  hipLaunchKernelGGL(head_norm_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+int ce_finalize_launch(const CeFinalizeArgs& g, hipStream_t s) {
+  if (g.members <= 0 || g.T <= 0 || g.parts <= 0 || !g.part || !g.tgt || !g.loss) return NOISE_EINVAL;
+  hipLaunchKernelGGL(ce_finalize_kernel, dim3(g.members), dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+int cast_launch(const float* in, bf16* out, long n, int cols, int split, hipStream_t s) {
+  if (!in || !out || n <= 0 || (split && (cols <= 0 || n % cols))) return NOISE_EINVAL;
+  hipLaunchKernelGGL(cast_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n, cols, split);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
+// ---- rank-1 GEMV for a bf16 activation (config-1 MLP entry): u[row] = bf16(x.bf16(b_dir)).
+namespace {
 __global__ void __launch_bounds__(256)
 rowdot_kernel(const bf16* __restrict__ x, long ldx, long x_mstride, int M, int K, int T, int pair_shift,
               const float* __restrict__ b, long ldb, float* __restrict__ u) {
@@ -29,7 +288,6 @@ rowdot_kernel(const bf16* __restrict__ x, long ldx, long x_mstride, int M, int K
     if (lane == 0) u[row] = bf16r(acc);
   }
 }
-
 }  // namespace
 
 int rowdot_launch(const bf16* x, long ldx, long x_mstride, int M, int K, int T, int pair_shift, const float* b,

@@ -1,0 +1,248 @@
+"""Population-perturbed forward of the fixed 37.7M GPT on the gfx950 kernels (the drop-in for
+`population_loss`, train/val/eggroll.py:66-103).
+
+The host side only orders kernel launches and owns device buffers (torch tensors); every op of the
+forward runs in libnoise_hip.so. Members are evaluated in chunks so activations stay bounded: a chunk
+of m members at T tokens holds about m * T * 17 KiB of activations (fp32 residual stream and x0,
+bf16 q|k|v, attention output and the 2048-wide MLP hidden).
+"""
+import torch
+
+from . import _lib
+from .model import GPTConfig, has_ve, window_sizes
+
+D, H, HD, F = 512, 8, 64, 2048
+HEAD_MODES = ('fp32', 'bf16')
+
+
+def _p(t):
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need_cuda(t, dtype, name):
+    if t.device.type != 'cuda':
+        raise ValueError(f'{name} must be a CUDA tensor (no CPU path)')
+    if t.dtype != dtype:
+        raise TypeError(f'{name} must be {dtype}, got {t.dtype}')
+    if not t.is_contiguous():
+        raise ValueError(f'{name} must be contiguous')
+
+
+class Weights:
+    """Per-step device copies of the shared weights in the kernels' formats: bf16 GEMM operands (the
+    autocast cast the reference performs inside every matmul, done once per step) and the fp32-head
+    split operand. Built from `p` = name -> fp32 parameter (train/val/eggroll.py:113)."""
+
+    def __init__(self, p, config=None, head='fp32'):
+        if head not in HEAD_MODES:
+            raise ValueError(f'head must be one of {HEAD_MODES}')
+        self.config = config or GPTConfig()
+        self.head = head
+        self.p = p
+        dev = p['transformer.wte.weight'].device
+        s = _stream()
+        L = self.config.n_layer
+        self.qkv = torch.empty(L, 3 * D, D, device=dev, dtype=torch.bfloat16)
+        self.proj = torch.empty(L, D, D, device=dev, dtype=torch.bfloat16)
+        self.fc = torch.empty(L, F, D, device=dev, dtype=torch.bfloat16)
+        self.mproj = torch.empty(L, D, F, device=dev, dtype=torch.bfloat16)
+        for i in range(L):
+            pre = f'transformer.h.{i}.'
+            for k, name in enumerate(('attn.c_q.weight', 'attn.c_k.weight', 'attn.c_v.weight')):
+                self._cast(p[pre + name], self.qkv[i, k * D:(k + 1) * D], s)
+            self._cast(p[pre + 'attn.c_proj.weight'], self.proj[i], s)
+            self._cast(p[pre + 'mlp.c_fc.weight'], self.fc[i], s)
+            self._cast(p[pre + 'mlp.c_proj.weight'], self.mproj[i], s)
+        w_head = p['lm_head.weight']
+        V = w_head.shape[0]
+        if head == 'fp32':
+            self.head_w = torch.empty(V, 3 * D, device=dev, dtype=torch.bfloat16)
+            _need_cuda(w_head, torch.float32, 'lm_head.weight')
+            _lib.call('noise_cast_bf16', w_head.data_ptr(), self.head_w.data_ptr(), w_head.numel(), D, s)
+        else:
+            self.head_w = torch.empty(V, D, device=dev, dtype=torch.bfloat16)
+            self._cast(w_head, self.head_w, s)
+
+    @staticmethod
+    def _cast(src, dst, s):
+        _need_cuda(src, torch.float32, 'weight')
+        if src.shape != dst.shape:
+            raise ValueError(f'weight shape {tuple(src.shape)} != {tuple(dst.shape)}')
+        _lib.call('noise_cast_bf16', src.data_ptr(), dst.data_ptr(), src.numel(), 0, s)
+
+
+class Buffers:
+    """Activation buffers for one chunk of `members` members at `T` tokens (reused across chunks)."""
+
+    def __init__(self, members, T, device, head='fp32', vocab=4096):
+        M = members * T
+        self.members, self.T = members, T
+        f32, b16 = torch.float32, torch.bfloat16
+        self.x = torch.empty(M, D, device=device, dtype=f32)
+        self.x0 = torch.empty(M, D, device=device, dtype=f32)
+        self.h = torch.empty(M, D, device=device, dtype=b16)
+        self.u_qkv = torch.empty(M, 4, device=device, dtype=f32)
+        self.gate = torch.empty(M, H, device=device, dtype=f32)
+        self.qkv = torch.empty(M, 3 * D, device=device, dtype=b16)
+        self.y = torch.empty(M, D, device=device, dtype=b16)
+        self.u_attn = torch.empty(M, H, device=device, dtype=f32)
+        self.u_fc = torch.empty(M, device=device, dtype=f32)
+        self.parts = _lib.value('noise_mlp_fc_parts', F)
+        self.hidden = torch.empty(M, F, device=device, dtype=b16)
+        self.u_mlp = torch.empty(M, self.parts, device=device, dtype=f32)
+        ws = _lib.size_query('noise_head_ce_workspace_size', members, T, vocab, int(head == 'fp32'))
+        self.head_ws = torch.empty(ws, device=device, dtype=torch.uint8)
+
+    def fits(self, members, T):
+        return members <= self.members and T == self.T
+
+
+def _noise_rows(noise, name, lo, hi):
+    """Rows lo..hi of a (a, b) pair or of an eps matrix, as contiguous device tensors."""
+    n = noise[name]
+    if isinstance(n, tuple):
+        return tuple(t[lo:hi] for t in n)
+    return n[lo:hi]
+
+
+def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, windows):
+    """Losses of members 0..m-1 of `sign` (m = len(sign)) into out[0:m]; noise rows are indexed by
+    p >> pair_shift. Follows train/val/eggroll.py:72-103 op for op."""
+    cfg = W.config
+    p = W.p
+    m, T = sign.shape[0], idx.shape[0]
+    s = _stream()
+    ps = pair_shift
+    a, b = noise['transformer.wte.weight']
+    V = p['transformer.wte.weight'].shape[0]
+    _lib.call('noise_embed_norm', _p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(sign), _p(idx), m, T, ps,
+              _p(buf.x0), s)
+    eps_r, eps_0 = noise['resid_lambdas'], noise['x0_lambdas']
+    lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
+    for i in range(cfg.n_layer):
+        pre = f'transformer.h.{i}.'
+        aq, bq = noise[pre + 'attn.c_q.weight']
+        ak, bk = noise[pre + 'attn.c_k.weight']
+        av, bv = noise[pre + 'attn.c_v.weight']
+        ve = has_ve(i, cfg.n_layer)
+        if ve:
+            gw = p[pre + 'attn.ve_gate.weight']
+            ga, gb = noise[pre + 'attn.ve_gate.weight']
+            vw = p[f'value_embeds.{i}.weight']
+            va, vb = noise[f'value_embeds.{i}.weight']
+        x_in = buf.x0 if i == 0 else buf.x
+        _lib.call('noise_block_entry', _p(x_in), _p(buf.x0), _p(buf.x), _p(buf.h), _p(buf.u_qkv), _p(bq), _p(bk),
+                  _p(bv), lam_r.data_ptr() + 4 * i, lam_0.data_ptr() + 4 * i, eps_r.data_ptr() + 4 * i,
+                  eps_0.data_ptr() + 4 * i, eps_r.stride(0), _p(gw) if ve else 0, _p(ga) if ve else 0,
+                  _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, s)
+        _lib.call('noise_qkv', _p(buf.h), _p(W.qkv[i]), _p(aq), _p(ak), _p(av), _p(buf.u_qkv), _p(sign), m, T, ps,
+                  _p(cos), _p(sin), _p(buf.gate) if ve else 0, _p(vw) if ve else 0, V, _p(va) if ve else 0,
+                  _p(vb) if ve else 0, _p(idx), _p(buf.qkv), s)
+        ap, bp = noise[pre + 'attn.c_proj.weight']
+        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], _p(bp), ps, _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
+        _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, _p(sign), m, T,
+                  ps, _p(buf.x), s)
+        af, bf_ = noise[pre + 'mlp.c_fc.weight']
+        am, bm = noise[pre + 'mlp.c_proj.weight']
+        _lib.call('noise_norm_dot', _p(buf.x), _p(buf.h), _p(bf_), _p(buf.u_fc), _p(sign), m, T, ps, s)
+        _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
+                  _p(buf.hidden), _p(buf.u_mlp), s)
+        _lib.call('noise_lowrank_resid', _p(buf.hidden), _p(W.mproj[i]), F, D, _p(am), _p(buf.u_mlp), buf.parts,
+                  _p(sign), m, T, ps, _p(buf.x), s)
+    ah, bh = noise['lm_head.weight']
+    Vh = W.head_w.shape[0]
+    _lib.call('noise_head_ce', _p(buf.x), _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
+              _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), s)
+
+
+def check_noise(noise, shapes, rows):
+    for name, shape in shapes.items():
+        n = noise[name]
+        if len(shape) == 2:
+            a, b = n
+            _need_cuda(a, torch.float32, f'noise[{name}][0]')
+            _need_cuda(b, torch.float32, f'noise[{name}][1]')
+            if a.shape[0] < rows or b.shape[0] < rows or a.shape[1] != shape[0] or b.shape[1] != shape[1]:
+                raise ValueError(f'noise[{name}] must be ([>= {rows}, {shape[0]}], [>= {rows}, {shape[1]}])')
+        else:
+            _need_cuda(n, torch.float32, f'noise[{name}]')
+            if n.shape[0] < rows or n.shape[1] != shape[0]:
+                raise ValueError(f'noise[{name}] must be [>= {rows}, {shape[0]}]')
+
+
+class Population:
+    """Evaluates populations of one model: keeps the kernels' weight formats and activation buffers.
+
+    chunk -- members per forward pass (activation memory ~ chunk * T * 17 KiB);
+    head  -- 'fp32' (fp32-accurate head) or 'bf16' (the reference's autocast head)."""
+
+    def __init__(self, model, chunk=256, head='fp32'):
+        self.model = model
+        self.config = model.config
+        self.chunk, self.head = chunk, head
+        self.windows = [w for w, _ in model.window_sizes]
+        self._buf = None
+        self._cos_sin = None
+
+    def tables(self, T):
+        cos = self.model.cos[0, :, 0, :]
+        sin = self.model.sin[0, :, 0, :]
+        if cos.shape[0] < T:
+            raise ValueError(f'rotary tables cover {cos.shape[0]} positions < T = {T}')
+        if self._cos_sin is None or self._cos_sin[0].device != cos.device:
+            self._cos_sin = (cos.to(torch.bfloat16).contiguous(), sin.to(torch.bfloat16).contiguous())
+        return self._cos_sin
+
+    def buffers(self, members, T, device):
+        if self._buf is None or not self._buf.fits(members, T):
+            self._buf = None
+            self._buf = Buffers(members, T, device, self.head, self.model.lm_head.weight.shape[0])
+        return self._buf
+
+    def loss(self, p, noise, sign, idx, targets, pair_shift=0, weights=None):
+        """Per-member mean CE [m] fp32 (train/val/eggroll.py:66-103). noise rows are per member
+        (pair_shift 0, as population_loss receives them) or per antithetic pair (pair_shift 1)."""
+        m, T = sign.shape[0], idx.shape[0]
+        dev = sign.device
+        _need_cuda(sign, torch.float32, 'sign')
+        _need_cuda(idx, torch.int64, 'idx')
+        _need_cuda(targets, torch.int64, 'targets')
+        if targets.shape[0] != T:
+            raise ValueError('idx and targets must have the same length')
+        if T % 128:
+            raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')
+        V = p['transformer.wte.weight'].shape[0]
+        lo = torch.minimum(idx.min(), targets.min()).item()
+        hi = torch.maximum(idx.max(), targets.max()).item()
+        if lo < 0 or hi >= V:
+            raise IndexError(f'token ids must lie in [0, {V}), got [{lo}, {hi}]')
+        rows = (m + (1 << pair_shift) - 1) >> pair_shift
+        check_noise(noise, {n: tuple(t.shape) for n, t in p.items()}, rows)
+        W = weights or Weights(p, self.config, self.head)
+        cos, sin = self.tables(T)
+        out = torch.empty(m, device=dev, dtype=torch.float32)
+        step = self.chunk if pair_shift == 0 else self.chunk - self.chunk % 2
+        buf = self.buffers(min(step, m), T, dev)
+        for c0 in range(0, m, step):
+            c1 = min(m, c0 + step)
+            r0, r1 = c0 >> pair_shift, (c1 + (1 << pair_shift) - 1) >> pair_shift
+            chunk_noise = {n: _noise_rows(noise, n, r0, r1) for n in p}
+            forward_chunk(W, buf, chunk_noise, sign[c0:c1], idx, targets, pair_shift, out[c0:c1], cos, sin,
+                          self.windows)
+        return out
+
+
+def population_loss(model, p, noise, sign, idx, targets, head='fp32', chunk=256):
+    """Drop-in for `population_loss(model, p, noise, sign, idx, targets)` (train/val/eggroll.py:66-103):
+    mean cross-entropy [m] of m perturbed models on one sequence, evaluated by the HIP kernels."""
+    return Population(model, chunk=chunk, head=head).loss(p, noise, sign, idx, targets)
+
+
+def clean_forward(model, idx, targets=None, loss_reduction='mean'):
+    """GPT.forward (utils/model.py:193-210) is the P = 1, sigma = 0 case of the population forward; the
+    per-sequence token layout it needs is not wired into the kernels yet."""
+    raise NotImplementedError('GPT.forward on the HIP kernels is not available yet; use population_loss')

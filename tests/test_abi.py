@@ -1,5 +1,6 @@
-"""The C-ABI library loads and exports every symbol include/*.h declares; the host wrappers reject bad
-arguments before any GPU call. CPU only (no compute calls)."""
+"""The C-ABI library loads and exports every symbol include/*.h declares, the ctypes signatures match
+the header's prototypes argument by argument, and the entry points reject bad arguments before any
+GPU work. CPU only (no compute calls)."""
 import ctypes
 import re
 from pathlib import Path
@@ -10,38 +11,73 @@ import torch
 from noise_amd import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
-_lib_EINVAL, _lib_ENOSPC = -1, -2
+EINVAL, ENOSPC = -1, -2
+
+C_TYPES = {
+    'int': ctypes.c_int, 'long': ctypes.c_long, 'float': ctypes.c_float, 'size_t': ctypes.c_size_t,
+    'size_t*': ctypes.POINTER(ctypes.c_size_t), 'noise_stream_t': ctypes.c_void_p,
+}
 
 
-def declared_symbols():
-    names = set()
+def declarations():
+    """name -> list of ctypes types parsed from the prototypes in include/*.h."""
+    out = {}
     for h in (ROOT / 'include').glob('*.h'):
         text = re.sub(r'/\*.*?\*/', '', h.read_text(), flags=re.S)
-        names |= set(re.findall(r'^\s*int\s+(noise_\w+)\s*\(', text, flags=re.M))
-    return names
+        for m in re.finditer(r'^\s*int\s+(noise_\w+)\s*\(([^)]*)\)\s*;', text, flags=re.M):
+            name, params = m.group(1), ' '.join(m.group(2).split())
+            types = []
+            if params and params != 'void':
+                for prm in params.split(','):
+                    prm = prm.strip()
+                    decl = re.sub(r'\s*\b\w+$', '', prm).replace('const ', '').replace(' ', '')
+                    types.append(ctypes.c_void_p if decl.endswith('*') and decl != 'size_t*' else C_TYPES[decl])
+            out[name] = types
+    return out
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
-    declared = declared_symbols()
-    assert declared, 'no declarations parsed'
+    declared = declarations()
+    assert len(declared) >= 20, sorted(declared)
     for name in declared:
         assert hasattr(lib, name), name
-    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    assert set(declared) == set(_lib.SIGNATURES), set(declared) ^ set(_lib.SIGNATURES)
+
+
+def test_ctypes_signatures_match_header():
+    for name, types in declarations().items():
+        bound = _lib.SIGNATURES[name]
+        assert len(bound) == len(types), (name, len(bound), len(types))
+        for i, (b, t) in enumerate(zip(bound, types)):
+            assert b == t, (name, i, b, t)
 
 
 def test_version_and_size_queries_run_on_cpu():
-    assert _lib.load().noise_version() >= 100
+    assert _lib.load().noise_version() >= 200
     n = _lib.size_query('noise_lowrank_mlp_workspace_size', 4, 256, 512, 2048)
     assert n >= 4 * 256 * 2048 * 2
     with pytest.raises(_lib.NoiseHipError):
         _lib.size_query('noise_lowrank_mlp_workspace_size', 0, 256, 512, 2048)
+    assert _lib.size_query('noise_head_ce_workspace_size', 2, 256, 4096, 1) > _lib.size_query(
+        'noise_head_ce_workspace_size', 2, 256, 4096, 0)
+    assert _lib.value('noise_mlp_fc_parts', 2048) == 32
+    assert _lib.value('noise_mlp_fc_parts', 100) == 0
 
 
-def test_null_workspace_is_rejected_without_touching_the_gpu():
-    rc = _lib.load().noise_lowrank_linear(None, 512, 0, None, 512, 512, None, None, None, 1, 16, 0, None, None, 0,
-                                          None, 0, None)
-    assert rc in (_lib_EINVAL, _lib_ENOSPC)
+def test_bad_arguments_are_rejected_without_touching_the_gpu():
+    lib = _lib.load()
+    rc = lib.noise_lowrank_linear(None, 512, 0, None, 512, 512, None, None, None, 1, 16, 0, None, None, 0, None, 0,
+                                  None)
+    assert rc in (EINVAL, ENOSPC)
+    assert lib.noise_fitness(None, 8, 4, 0, None, None, None) == EINVAL
+    assert lib.noise_fitness(1, 7, 4, 0, 1, 1, None) == EINVAL        # odd number of losses
+    assert lib.noise_fitness(1, 8, 4, 5, 1, 1, None) == EINVAL        # unknown mode
+    assert lib.noise_adam(None, None, None, None, 10, 1e-3, .5, .95, 1e-8, 1.0, None) == EINVAL
+    assert lib.noise_attention(1, 1, 100, 50, None, 0, 1, None, None, None, 0, None) == EINVAL  # T % 128
+    assert lib.noise_head_ce(1, 1, 4096, 1, 1, 1, 1, 1, 1, 256, 0, 1, None, 0, None) == ENOSPC
+    assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
+    assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
 
 
 def test_ops_refuse_cpu_tensors():

@@ -1,0 +1,366 @@
+"""GPU parity of the population forward and of the EGGROLL update kernels against the CPU oracle.
+
+Tolerances (north star): <= 1e-2 relative error on bf16 activations, <= 1e-4 absolute error on
+per-member fp32 losses. The oracle runs in its bf16 rounding-point mode (the reference under CUDA
+autocast) with the fp32 head; the kernels keep those rounding points.
+
+The 1e-4 loss bar is applied at the reference's own initialisation (make_model seed 0), where the
+bf16 path's sensitivity to summation order is ~4e-5. At trained-scale weights (`trained_like`) the
+same path is chaotic at the 1e-3 level: the oracle itself moves by ~1.5e-3 when its GEMMs accumulate
+in fp64 instead of fp32. There the bound is twice that measured floor (plus 1e-4), computed in the
+test from two oracle runs."""
+import math
+
+import pytest
+import torch
+
+from noise_amd import _lib
+from noise_amd.model import make_model
+from noise_amd.synthetic import antithetic_signs, population_noise, trained_like, zipf_tokens
+from oracle import eggroll as oe
+from oracle import model as om
+from tests._util import log_case, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+
+
+def _dev(noise):
+    return {n: tuple(t.to(DEV) for t in v) if isinstance(v, tuple) else v.to(DEV) for n, v in noise.items()}
+
+
+@pytest.fixture(scope='module')
+def trained():
+    torch.manual_seed(0)
+    model = trained_like(make_model('cpu', 0))
+    params = {n: p.detach().clone() for n, p in model.named_parameters()}
+    return model, params
+
+
+def _gpu_model(model):
+    m = make_model('cpu', 0)
+    m.load_state_dict(model.state_dict())
+    return m.to(DEV)
+
+
+# ---------------------------------------------------------------- stage kernels
+
+def test_embed_norm_matches_oracle():
+    g = torch.Generator().manual_seed(1)
+    V, T, m = 4096, 128, 4
+    w = torch.randn(V, 512, generator=g)
+    a, b = torch.randn(2, V, generator=g), torch.randn(2, 512, generator=g)
+    sign = antithetic_signs(m, 1e-2)
+    idx, _ = zipf_tokens(T, seed=3)
+    log_case(f'embed_norm m={m} T={T}')
+    x0 = torch.empty(m * T, 512, device=DEV)
+    d = [t.to(DEV) for t in (w, a, b, sign, idx)]  # device copies stay referenced until the kernel ran
+    _lib.call('noise_embed_norm', d[0].data_ptr(), V, d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(),
+              d[4].data_ptr(), m, T, 1, x0.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    rep = lambda t: t.repeat_interleave(2, 0)  # noqa: E731
+    ref = om.norm(om.lowrank_embed(w, rep(a), rep(b), idx, sign)).reshape(m * T, 512)
+    assert (x0.cpu() - ref).abs().max() < 2e-5
+
+
+def test_block_entry_and_qkv_match_oracle():
+    """Block entry (mix, norm, q/k/v dots, value gate) and the QKV GEMM epilogue (segment rank-1,
+    rotary, QK-norm, gated value embedding) against the oracle ops at sigma = 0.05."""
+    g = torch.Generator().manual_seed(8)
+    m, T, V = 4, 128, 4096
+    sign = antithetic_signs(m, 0.05)
+    x = torch.randn(m, T, 512, generator=g) * 2
+    x0 = torch.randn(m, T, 512, generator=g)
+    lam_r, lam_0 = torch.tensor([0.9]), torch.tensor([0.15])
+    eps = torch.randn(m, 8, generator=g), torch.randn(m, 8, generator=g)
+    wq, wk, wv = (torch.randn(512, 512, generator=g) / 22 for _ in range(3))
+    (aq, bq), (ak, bk), (av, bv) = ((torch.randn(m, 512, generator=g), torch.randn(m, 512, generator=g))
+                                    for _ in range(3))
+    gw = torch.randn(8, 32, generator=g) * 0.2
+    ga, gb = torch.randn(m, 8, generator=g), torch.randn(m, 32, generator=g)
+    vw = torch.randn(V, 512, generator=g) * 0.1
+    va, vb = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    idx, _ = zipf_tokens(T, seed=9)
+    cos, sin = om.rotary_tables()
+    d = {k: t.to(DEV) for k, t in dict(x=x, x0=x0, lr=lam_r, l0=lam_0, er=eps[0], e0=eps[1], bq=bq, bk=bk, bv=bv,
+                                        aq=aq, ak=ak, av=av, gw=gw, ga=ga, gb=gb, vw=vw, va=va, vb=vb, idx=idx,
+                                        sign=sign, cos=cos.contiguous(), sin=sin.contiguous()).items()}
+    wqkv = torch.cat([wq, wk, wv]).to(DEV)
+    wqkv16 = torch.empty(1536, 512, device=DEV, dtype=torch.bfloat16)
+    M = m * T
+    xo, h = torch.empty(M, 512, device=DEV), torch.empty(M, 512, device=DEV, dtype=torch.bfloat16)
+    u, gate = torch.empty(M, 4, device=DEV), torch.empty(M, 8, device=DEV)
+    qkv = torch.empty(M, 1536, device=DEV, dtype=torch.bfloat16)
+    s = torch.cuda.current_stream().cuda_stream
+    log_case(f'block_entry + qkv m={m} T={T}')
+    _lib.call('noise_cast_bf16', wqkv.data_ptr(), wqkv16.data_ptr(), wqkv.numel(), 0, s)
+    _lib.call('noise_block_entry', d['x'].data_ptr(), d['x0'].data_ptr(), xo.data_ptr(), h.data_ptr(), u.data_ptr(),
+              d['bq'].data_ptr(), d['bk'].data_ptr(), d['bv'].data_ptr(), d['lr'].data_ptr(), d['l0'].data_ptr(),
+              d['er'].data_ptr() + 4 * 3, d['e0'].data_ptr() + 4 * 3, 8, d['gw'].data_ptr(), d['ga'].data_ptr(),
+              d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, s)
+    _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
+              u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), gate.data_ptr(),
+              d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(), d['idx'].data_ptr(), qkv.data_ptr(), s)
+    torch.cuda.synchronize()
+    sg = sign[:, None, None]
+    xr = (lam_r + sg * eps[0][:, 3, None, None]) * x + (lam_0 + sg * eps[1][:, 3, None, None]) * x0
+    assert (xo.cpu().view(m, T, 512) - xr).abs().max() < 1e-5
+    hr = om.norm(xr)
+    assert (h.cpu().float().view(m, T, 512) - om.bf(hr)).abs().max() <= 2 ** -7 * hr.abs().max()
+    for k, bb in enumerate((bq, bk, bv)):
+        ur = om.bf(om.bf(hr) @ om.bf(bb).unsqueeze(-1))[..., 0]
+        assert torch.allclose(u.cpu()[:, k].view(m, T), ur, atol=2e-2, rtol=1e-2)
+    gr = 2 * torch.sigmoid(om.lowrank(hr[..., :32], gw, ga, gb, sign, 'bf16'))
+    assert torch.allclose(gate.cpu().view(m, T, 8), gr, atol=2e-3)
+    # q | k | v from the GPU's own h, u and gate (isolates the GEMM epilogue)
+    hg = h.cpu().float().view(m, T, 512)
+    ug = u.cpu().view(m, T, 4)
+
+    def lin(w, a, k):
+        return om.bf(hg @ om.bf(w).t()) + sg * ug[..., k:k + 1] * a[:, None, :]
+    q, kk_, vv = lin(wq, aq, 0), lin(wk, ak, 1), lin(wv, av, 2)
+    ve = om.lowrank_embed(vw, va, vb, idx, sign)
+    vv = vv.view(m, T, 8, 64) + gate.cpu().view(m, T, 8).unsqueeze(-1) * ve.view(m, T, 8, 64)
+    c, sn = cos[:T], sin[:T]
+    qr = om.norm(om.apply_rotary(q.view(m, T, 8, 64), c, sn))
+    kr = om.norm(om.apply_rotary(kk_.view(m, T, 8, 64), c, sn))
+    got = qkv.cpu().float().view(m, T, 3, 8, 64)
+    for k, ref in enumerate((qr, kr, vv)):
+        assert rel_err(got[:, :, k], om.bf(ref)) < 5e-3, k
+        assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
+
+
+def test_attention_matches_oracle_and_moments():
+    g = torch.Generator().manual_seed(2)
+    m, T = 2, 256
+    for window in (T, 100):
+        log_case(f'attention m={m} T={T} window={window}')
+        q, k, v = (torch.randn(m, T, 8, 64, generator=g).bfloat16() for _ in range(3))
+        qkv = torch.cat([q.reshape(m * T, 512), k.reshape(m * T, 512), v.reshape(m * T, 512)], 1).to(DEV)
+        y = torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
+        bp = torch.randn(m, 512, generator=g)
+        bpd = bp.to(DEV)
+        up = torch.empty(m * T, 8, device=DEV)
+        mom = torch.empty(m, 8, 2, 64, device=DEV)
+        ws = torch.empty(_lib.size_query('noise_attention_workspace_size', m, T), device=DEV, dtype=torch.uint8)
+        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, bpd.data_ptr(), 0, y.data_ptr(),
+                  up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
+        got = y.cpu().float().view(m, T, 8, 64)
+        assert rel_err(got, ref) < 1e-2
+        assert (got - ref).abs().max() < 2e-2
+        # c_proj dot partials: sum over heads equals y . bf16(b_proj)
+        dot = (got.reshape(m, T, 512) * om.bf(bp)[:, None, :]).reshape(m, T, 8, 64).sum(-1)
+        assert torch.allclose(up.cpu().view(m, T, 8), dot, atol=1e-3, rtol=1e-3)
+        # credit moments over tokens of the bf16 output
+        m1, m2 = om.attention_moments(got.permute(0, 2, 1, 3))
+        assert torch.allclose(mom.cpu()[:, :, 0], m1, atol=1e-5)
+        assert torch.allclose(mom.cpu()[:, :, 1], m2, atol=1e-5)
+
+
+def test_head_ce_matches_oracle_fp32_and_bf16_heads():
+    g = torch.Generator().manual_seed(4)
+    m, T, V = 4, 256, 4096
+    x = torch.randn(m * T, 512, generator=g) * 3
+    W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
+    _, targets = zipf_tokens(T, seed=5)
+    s = torch.cuda.current_stream().cuda_stream
+    h = om.norm(x.view(m, T, 512))
+    xd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (x, W, a, b, sign, targets))
+    for fp32 in (1, 0):
+        log_case(f'head_ce m={m} T={T} fp32_head={fp32}')
+        wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+        loss = torch.empty(m, device=DEV)
+        ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV,
+                         dtype=torch.uint8)
+        _lib.call('noise_head_ce', xd.data_ptr(), wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
+                  sd.data_ptr(), td.data_ptr(), m, T, 0, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
+        torch.cuda.synchronize()
+        if fp32:
+            ref = om.head_loss(h, W, a, b, sign, targets, 'fp32', 'fp32')
+            assert (loss.cpu() - ref).abs().max() < 1e-4, (loss.cpu(), ref)
+        else:
+            ref = om.head_loss(h, W, a, b, sign, targets, 'bf16', 'bf16')
+            assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
+
+
+# ---------------------------------------------------------------- whole population forward
+
+def _population_case(model, params, P, T, sigma, seed, head='fp32'):
+    from noise_amd.population import Population
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    noise = population_noise(shapes, P // 2, seed=seed)
+    sign = antithetic_signs(P, sigma)
+    idx, tgt = zipf_tokens(T, seed=seed + 1)
+    gm = _gpu_model(model)
+    gp = dict(gm.named_parameters())
+    pop = Population(gm, chunk=P, head=head)
+    got = pop.loss(gp, _dev(noise), sign.to(DEV), idx.to(DEV), tgt.to(DEV)).cpu()
+    return got, noise, sign, idx, tgt
+
+
+def _oracle_with_floor(params, noise, sign, idx, tgt):
+    """bf16-mode oracle losses, and how far they move when every GEMM accumulates in fp64 instead of
+    fp32 (the summation-order sensitivity of the bf16 path at these weights)."""
+    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    orig = om.lowrank
+
+    def lowrank64(x, weight, a, b, s, mode='fp32'):
+        if mode == 'fp32':
+            return orig(x, weight, a, b, s, mode)
+        u = om.bf((om.bf(x).double() @ om.bf(b).double().unsqueeze(-1)).float())
+        dense = om.bf((om.bf(x).double() @ om.bf(weight).double().t()).float())
+        return dense + s[:, None, None] * u * a[:, None, :]
+
+    om.lowrank = lowrank64
+    try:
+        alt = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    finally:
+        om.lowrank = orig
+    floor = float((alt - ref).abs().max())
+    pair_floor = float(((alt[1::2] - alt[0::2]) - (ref[1::2] - ref[0::2])).abs().max())
+    return ref, floor, pair_floor
+
+
+def test_population_loss_config0_at_reference_init():
+    """Config 0 (P = 8, T = 256, sigma = 1e-3) on the reference's seed-0 weights: losses and the
+    antithetic differences within 1e-4 of the bf16-mode oracle."""
+    model = make_model('cpu', 0)
+    params = {n: p.detach().clone() for n, p in model.named_parameters()}
+    P, T = 8, 256
+    log_case(f'population_loss P={P} T={T} reference init')
+    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11)
+    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max() < 1e-4, (got, ref)
+    dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
+    assert (dg - dr).abs().max() < 1e-4, (dg, dr)
+
+
+def test_population_loss_trained_weights_within_rounding_floor(trained):
+    model, params = trained
+    P, T = 8, 256
+    log_case(f'population_loss P={P} T={T} trained-scale weights')
+    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11)
+    ref, floor, pair_floor = _oracle_with_floor(params, noise, sign, idx, tgt)
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max() <= 2 * floor + 1e-4, (got, ref, floor)
+    dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
+    assert (dg - dr).abs().max() <= 2 * pair_floor + 1e-4, (dg, dr, pair_floor)
+
+
+def test_population_loss_large_sigma_and_chunking(trained):
+    """sigma = 0.05 makes every rank-1 term matter; two chunks exercise the chunk slicing."""
+    from noise_amd.population import Population
+    model, params = trained
+    P, T = 8, 128
+    log_case(f'population_loss P={P} T={T} sigma=0.05 chunked')
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    noise = population_noise(shapes, P // 2, seed=21)
+    sign = antithetic_signs(P, 0.05)
+    idx, tgt = zipf_tokens(T, seed=22)
+    gm = _gpu_model(model)
+    pop = Population(gm, chunk=4)
+    got = pop.loss(dict(gm.named_parameters()), _dev(noise), sign.to(DEV), idx.to(DEV), tgt.to(DEV)).cpu()
+    ref, floor, _ = _oracle_with_floor(params, noise, sign, idx, tgt)
+    # one alternative summation order samples the chaotic spread once; at sigma = 0.05 allow 3x
+    assert (got - ref).abs().max() <= 3 * floor + 1e-4, (got, ref, floor)
+    assert (got[0] - got[1]).abs() > 1e-3
+
+
+def test_population_loss_pair_shift_equals_per_member(trained):
+    """Per-direction noise with pair_shift = 1 gives the same losses as the repeated per-member noise."""
+    from noise_amd.population import Population
+    model, params = trained
+    P, T = 8, 128
+    log_case(f'population_loss pair_shift P={P} T={T}')
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    per_dir = population_noise(shapes, P // 2, seed=31, per_member=False)
+    per_mem = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
+               for n, v in per_dir.items()}
+    sign = antithetic_signs(P, 1e-3).to(DEV)
+    idx, tgt = (t.to(DEV) for t in zipf_tokens(T, seed=32))
+    gm = _gpu_model(model)
+    gp = dict(gm.named_parameters())
+    pop = Population(gm, chunk=P)
+    a = pop.loss(gp, _dev(per_dir), sign, idx, tgt, pair_shift=1)
+    b = pop.loss(gp, _dev(per_mem), sign, idx, tgt, pair_shift=0)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
+
+
+def test_population_loss_golden_reference_fp32(golden):
+    """The kernels against the reference's own fp32 CPU losses (tests/golden): the difference is the
+    bf16 rounding of the autocast path, bounded well inside the antithetic signal's scale."""
+    model = trained_like(make_model('cpu', 0))
+    params = {n: p.detach().clone() for n, p in model.named_parameters()}
+    P, T = 2 * golden['pairs'], golden['T']
+    log_case(f'population_loss vs golden P={P} T={T}')
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    noise = population_noise(shapes, golden['pairs'])
+    sign = antithetic_signs(P, golden['sigma'])
+    idx, tgt = zipf_tokens(T)
+    gm = _gpu_model(model)
+    from noise_amd.population import Population
+    got = Population(gm, chunk=P).loss(dict(gm.named_parameters()), _dev(noise), sign.to(DEV), idx.to(DEV),
+                                       tgt.to(DEV)).cpu()
+    ref = torch.tensor(golden['losses_trained'])
+    assert (got - ref).abs().max() < 2e-2, (got, ref)
+
+
+# ---------------------------------------------------------------- update path
+
+def test_fitness_update_adam_match_oracle():
+    g = torch.Generator().manual_seed(7)
+    pairs, nl = 6, 24
+    losses = torch.randn(nl, generator=g) * 0.01 + 5
+    s = torch.cuda.current_stream().cuda_stream
+    log_case(f'fitness n={nl} pairs={pairs}')
+    fit = torch.empty(nl // 2, device=DEV)
+    w = torch.empty(pairs, device=DEV)
+    ld = losses.to(DEV)
+    _lib.call('noise_fitness', ld.data_ptr(), nl, pairs, 0, fit.data_ptr(), w.data_ptr(), s)
+    f_ref, w_ref = oe.fitness(losses, pairs)
+    torch.cuda.synchronize()
+    assert torch.allclose(fit.cpu(), f_ref, atol=1e-5)
+    assert torch.allclose(w.cpu(), w_ref, atol=1e-5)
+    # rank mode: a permutation of centred ranks
+    _lib.call('noise_fitness', ld.data_ptr(), nl, pairs, 1, fit.data_ptr(), w.data_ptr(), s)
+    torch.cuda.synchronize()
+    ranks = torch.argsort(torch.argsort(losses[1::2] - losses[0::2], stable=True), stable=True).float()
+    assert torch.allclose(fit.cpu(), ranks / (nl // 2 - 1) - 0.5, atol=1e-6)
+
+    log_case('outer_update')
+    out_d, in_d = 70, 130
+    a, b = torch.randn(pairs, out_d, generator=g), torch.randn(pairs, in_d, generator=g)
+    eps = torch.randn(pairs, 8, generator=g)
+    grad = torch.empty(out_d, in_d, device=DEV)
+    ad, bd, wd, ed = (t.to(DEV) for t in (a, b, w_ref, eps))
+    _lib.call('noise_outer_update', ad.data_ptr(), out_d, bd.data_ptr(), in_d, wd.data_ptr(), pairs, out_d, in_d,
+              -1.0 / (nl // 2), grad.data_ptr(), s)
+    gl = torch.empty(1, 8, device=DEV)
+    _lib.call('noise_outer_update', 0, 0, ed.data_ptr(), 8, wd.data_ptr(), pairs, 1, 8, -1.0 / (nl // 2),
+              gl.data_ptr(), s)
+    ref = oe.update(w_ref, {'m': (a, b), 'l': eps}, nl // 2)
+    torch.cuda.synchronize()
+    assert torch.allclose(grad.cpu(), ref['m'], atol=1e-5)
+    assert torch.allclose(gl.cpu()[0], ref['l'], atol=1e-6)
+
+    log_case('adam')
+    p0 = torch.randn(1000, generator=g)
+    param, m_, v_ = p0.clone().to(DEV), torch.zeros(1000, device=DEV), torch.zeros(1000, device=DEV)
+    ref_p = p0.clone()
+    opt = torch.optim.AdamW([ref_p], lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    for step in range(1, 4):
+        gr = torch.randn(1000, generator=g)
+        ref_p.grad = gr.clone()
+        opt.step()
+        grd = gr.to(DEV)
+        _lib.call('noise_adam', param.data_ptr(), grd.data_ptr(), m_.data_ptr(), v_.data_ptr(), 1000,
+                  1e-3 / (1 - 0.5 ** step), 0.5, 0.95, 1e-8, math.sqrt(1 - 0.95 ** step), s)
+        torch.cuda.synchronize()
+    assert torch.allclose(param.cpu(), ref_p, atol=1e-6, rtol=1e-6)
