@@ -1,12 +1,17 @@
-"""Benchmark of the population-perturbed fused relu^2 MLP on one MI355X.
+"""Benchmark of the population-perturbed forward + EGGROLL update on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload step|mlp] [--no-cpu-baseline]
 
-One step = one pass of the low-rank relu^2 MLP (noise_lowrank_mlp) over the whole population:
-P = 256 members (128 antithetic pairs, sigma = 1e-3) of y_p = relu^2(x W1_p^T) W2_p^T with
-W_p = W + s_p a_p b_p^T, x [2048 tokens, 512] shared, W1 [2048, 512], W2 [512, 2048], bf16 operands with
-fp32 accumulation, bf16 output [256, 2048, 512]. Inputs are synthetic and resident in HBM before the
-timed region. Prints one JSON line (rank 0).
+Default workload (the full population step on one GPU's share): the 37.7M
+model (8 layers, d 512, vocab 4096) with bf16 GEMM weights and an fp32 head, 3072 members = 1536
+antithetic pairs of rank-1 perturbations on every matrix and embedding (Gaussian on the 16 mixing
+scalars), sigma = 1e-3, one 2048-token Zipf(1.1) sequence; then the rank-normalised fitness, the
+fitness-weighted sum of the perturbation outer products and an Adam step on all 37,749,776 weights.
+One step = all of that (Eggroll.step). Weights are the reference's seed-0 initialisation, data is
+synthetic and resident in HBM before the timed region.
+
+`--workload mlp` times BASELINE config 1 alone (the rank-1-perturbed relu^2 MLP, P = 256, T = 2048,
+shared x). Prints one JSON line.
 """
 import argparse
 import json
@@ -22,38 +27,67 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = 'perturbed member-tokens/sec on 1 GPU; fused-MLP MFMA % of bf16 peak'
 PEAK_BF16_TFLOPS = 2500.0         # MI355X dense bf16 MFMA
-PEAK_HBM_GBS = 8000.0
-P, T, D, F = 256, 2048, 512, 2048
+D, F, T, V, L = 512, 2048, 2048, 4096, 8
 SIGMA = 1e-3
-FLOP_PER_MEMBER_TOKEN = 2 * (2 * D * F)  # both GEMMs, counted per member
+MLP_FLOP_PER_MEMBER_TOKEN = 2 * (2 * D * F)  # both MLP GEMMs, counted per member
+# per member-token algorithmic FLOPs of the forward: dense GEMMs (q, k, v, proj, fc, mlp proj per layer,
+# ve_gate, head) and window-aware attention at T = 2048 (QK^T and PV over the visible keys)
+DENSE_FLOP = L * 2 * (4 * D * D + 2 * D * F) + 4 * 2 * 32 * 8 + 2 * D * V
 
 
-def make_inputs(device, seed=0):
-    g = torch.Generator().manual_seed(seed)
-    x = torch.randn(T, D, generator=g).bfloat16()
-    w1 = (torch.randn(F, D, generator=g) * D ** -0.5).bfloat16()
-    w2 = (torch.randn(D, F, generator=g) * F ** -0.5).bfloat16()
-    pairs = P // 2
-    a1, b1 = torch.randn(pairs, F, generator=g), torch.randn(pairs, D, generator=g)
-    a2, b2 = torch.randn(pairs, D, generator=g), torch.randn(pairs, F, generator=g)
-    sign = torch.tensor([SIGMA, -SIGMA]).repeat(pairs)
-    return [t.to(device) for t in (x, w1, w2, a1, b1, a2, b2, sign)]
+def attention_flop_per_token(T, windows, H=8, hd=64):
+    pairs = sum(sum(min(q, w) + 1 for q in range(T)) for w in windows)
+    return 4 * hd * H * pairs / T
 
 
-def cpu_baseline(budget_s=12.0):
-    """The CPU oracle (port of the reference MLP sublayer, bf16 rounding-point mode) on a bounded
-    sample: whole 2048-token members, as many as fit the time budget."""
+def roofline_traffic():
+    path = ROOT / 'profiles' / 'mlp_traffic.json'
+    if path.exists():
+        return json.loads(path.read_text()).get('hbm_bytes_per_launch')
+    return None
+
+
+def cpu_baseline_step(budget_s=15.0):
+    """The CPU oracle (fp32 port of population_loss: what the reference computes on a CPU) on a bounded
+    sample of the config-4 workload: antithetic pairs of members on the same 2048-token sequence, as
+    many as fit the time budget (at least one pair)."""
     from oracle import model as om
-    threads = int(os.environ.get('OMP_NUM_THREADS', os.cpu_count() or 1))
-    threads = min(threads, os.cpu_count() or 1)
+    from noise_amd.model import make_model
+    from noise_amd.synthetic import antithetic_signs, population_noise, zipf_tokens
+    threads = min(int(os.environ.get('OMP_NUM_THREADS', os.cpu_count() or 1)), os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    x, w1, w2, a1, b1, a2, b2, sign = make_inputs('cpu')
-    xf, w1f, w2f = x.float(), w1.float(), w2.float()
+    model = make_model('cpu', 0)
+    params = {n: p.detach() for n, p in model.named_parameters()}
+    shapes = {n: tuple(p.shape) for n, p in params.items()}
+    idx, tgt = zipf_tokens(T, seed=1)
     done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and done < P:
-        m = [done, done + 1]
-        om.mlp_population(xf, w1f, w2f, a1[[done // 2] * 2], b1[[done // 2] * 2], a2[[done // 2] * 2],
-                          b2[[done // 2] * 2], sign[m], 'bf16')
+    while done == 0 or time.perf_counter() - t0 < budget_s:
+        noise = population_noise(shapes, 1, seed=2 + done)
+        om.population_loss(params, noise, antithetic_signs(2, SIGMA), idx, tgt, mode='fp32', head='fp32')
+        done += 2
+        if done >= 64:
+            break
+    dt = time.perf_counter() - t0
+    return {'value': done * T / dt, 'unit': 'member-tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': f'{done} members ({done // 2} antithetic pairs) x {T} tokens of the config-4 forward through '
+                      f'oracle.model.population_loss (torch CPU fp32, dense masked attention), {dt:.1f} s'}
+
+
+def cpu_baseline_mlp(budget_s=12.0):
+    """The CPU oracle of the config-1 MLP (bf16 rounding points emulated in fp32) on whole 2048-token
+    members of one antithetic pair, repeated for the time budget."""
+    from oracle import model as om
+    threads = min(int(os.environ.get('OMP_NUM_THREADS', os.cpu_count() or 1)), os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, D, generator=g).bfloat16().float()
+    w1 = (torch.randn(F, D, generator=g) * D ** -0.5).bfloat16().float()
+    w2 = (torch.randn(D, F, generator=g) * F ** -0.5).bfloat16().float()
+    a1, b1, a2, b2 = (torch.randn(2, n, generator=g) for n in (F, D, D, F))
+    sign = torch.tensor([SIGMA, -SIGMA])
+    done, t0 = 0, time.perf_counter()
+    while done == 0 or time.perf_counter() - t0 < budget_s:
+        om.mlp_population(x, w1, w2, a1, b1, a2, b2, sign, 'bf16')
         done += 2
     dt = time.perf_counter() - t0
     return {'value': done * T / dt, 'unit': 'member-tokens/s', 'cores': threads, 'kind': 'port',
@@ -61,33 +95,85 @@ def cpu_baseline(budget_s=12.0):
                       f'(torch CPU, bf16 rounding points emulated in fp32), {dt:.1f} s'}
 
 
-def load_traffic():
-    path = ROOT / 'profiles' / 'traffic_mlp.json'
-    if path.exists():
-        return json.loads(path.read_text()).get('hbm_bytes_per_launch')
-    return None
-
-
-def main():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--no-cpu-baseline', action='store_true')
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f'bench.py measures one GPU only: every box in this build has a single MI355X; '
-              f'--gpus {args.gpus} is not supported (the member dimension shards across GPUs by design, '
-              f'see DESIGN.md).', file=sys.stderr)
-        sys.exit(2)
-    if not torch.cuda.is_available():
-        print('bench.py needs a GPU', file=sys.stderr)
-        sys.exit(2)
-    from noise_amd import ops
+def run_step(args):
+    from noise_amd import population
+    from noise_amd.eggroll import Eggroll, LR, BETAS
+    from noise_amd.model import make_model
+    from noise_amd.optim import Adam
+    from noise_amd.synthetic import zipf_tokens
 
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
-    x, w1, w2, a1, b1, a2, b2, sign = make_inputs(dev)
+    pairs = args.pairs
+    P = 2 * pairs
+    model = make_model(dev, 0)
+    es = Eggroll(model, pairs, chunk=args.chunk, head='fp32', fitness='rank', sigma=SIGMA)
+    opt = Adam(model.parameters(), lr=LR, betas=BETAS, eps=1e-8)
+    idx, tgt = zipf_tokens(T, seed=1)
+    x, y = idx[None].to(dev), tgt[None].to(dev)
+    for w in range(args.warmup):
+        es.step(x, y, opt, w + 1)
+    torch.cuda.synchronize()
+    timer = population.StageTimer()
+    population.TIMER = timer
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        loss = es.step(x, y, opt, args.warmup + k + 1)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    population.TIMER = population._NoTimer()
+    stages = timer.collect()
+    ms_step = wall * 1e3 / args.steps
+    windows = [w for w, _ in model.window_sizes]
+    flop_tok = DENSE_FLOP + attention_flop_per_token(T, windows)
+    # the fused MLP (c_fc relu^2 GEMM + c_proj GEMM) of every layer and chunk, timed with HIP events on the
+    # launch stream inside the timed steps
+    mlp_launches = timer.count['mlp']
+    mlp_ms = stages['mlp'] / mlp_launches
+    mlp_flop = MLP_FLOP_PER_MEMBER_TOKEN * (P * T) * L * args.steps / mlp_launches  # per launch (one layer, one chunk)
+    achieved = mlp_flop / (mlp_ms * 1e-3) / 1e12
+    result = {
+        'metric': METRIC,
+        'value': P * T / (ms_step * 1e-3),
+        'unit': 'member-tokens/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': ms_step,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'bf16',
+        'data': 'synthetic (Zipf(1.1) tokens, seed-0 reference init, N(0,1) noise buffer)',
+        'config': {'workload': 'config4_population_step', 'members': P, 'pairs': pairs, 'tokens': T,
+                   'model': '37.7M GPT (8 x 512, vocab 4096)', 'head': 'fp32 (bf16 hi/lo split on MFMA)',
+                   'sigma': SIGMA, 'fitness': 'rank', 'optimizer': 'Adam (HIP)', 'chunk_members': args.chunk,
+                   'parallelism': 'single GPU'},
+        'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
+                     'kernel': 'fused relu^2 MLP: lowrank_gemm<EPI_RELU2> (c_fc) + lowrank_gemm<EPI_RESID> (c_proj)',
+                     'flop_per_launch': mlp_flop, 'ms_per_launch': mlp_ms},
+        'forward_tflops': flop_tok * P * T / (sum(v for k, v in stages.items()) / args.steps * 1e-3) / 1e12,
+        'stage_ms_per_step': {k: v / args.steps for k, v in stages.items()},
+        'mean_population_loss': loss,
+    }
+    return result
+
+
+def run_mlp(args):
+    from noise_amd import ops
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    P = 256
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, D, generator=g).bfloat16()
+    w1 = (torch.randn(F, D, generator=g) * D ** -0.5).bfloat16()
+    w2 = (torch.randn(D, F, generator=g) * F ** -0.5).bfloat16()
+    pairs = P // 2
+    a1, b1 = torch.randn(pairs, F, generator=g), torch.randn(pairs, D, generator=g)
+    a2, b2 = torch.randn(pairs, D, generator=g), torch.randn(pairs, F, generator=g)
+    sign = torch.tensor([SIGMA, -SIGMA]).repeat(pairs)
+    x, w1, w2, a1, b1, a2, b2, sign = (t.to(dev) for t in (x, w1, w2, a1, b1, a2, b2, sign))
     y = torch.empty(P, T, D, device=dev, dtype=torch.bfloat16)
     ws = torch.empty(ops.mlp_workspace_bytes(P, T, D, F), device=dev, dtype=torch.uint8)
 
@@ -108,31 +194,45 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     ms_launch = ev0.elapsed_time(ev1) / args.steps
-    flop = FLOP_PER_MEMBER_TOKEN * P * T
+    flop = MLP_FLOP_PER_MEMBER_TOKEN * P * T
     achieved = flop / (ms_launch * 1e-3) / 1e12
-    result = {
-        'metric': METRIC,
-        'value': P * T / (ms_step * 1e-3),
-        'unit': 'member-tokens/s',
-        'n_gpus': 1,
-        'steps': args.steps,
-        'warmup': args.warmup,
-        'ms_per_step': ms_step,
-        'higher_is_better': True,
-        'scaling': 'weak',
-        'vs_baseline': None,
-        'dtype': 'bf16',
-        'data': 'synthetic',
-        'config': {'workload': 'config1_fused_relu2_mlp_rank1', 'members': P, 'pairs': P // 2, 'tokens': T,
+    return {
+        'metric': METRIC, 'value': P * T / (ms_step * 1e-3), 'unit': 'member-tokens/s', 'n_gpus': 1,
+        'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': ms_step, 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+        'config': {'workload': 'config1_fused_relu2_mlp_rank1', 'members': P, 'pairs': pairs, 'tokens': T,
                    'd_model': D, 'd_hidden': F, 'sigma': SIGMA, 'x': 'shared [2048, 512]', 'output': 'bf16',
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': load_traffic(),
+                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
                      'kernel': 'noise_lowrank_mlp (rowdot + relu2 GEMM + proj GEMM)',
                      'flop_per_launch': flop, 'ms_per_launch': ms_launch},
     }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=3)
+    ap.add_argument('--warmup', type=int, default=1)
+    ap.add_argument('--workload', choices=('step', 'mlp'), default='step')
+    ap.add_argument('--pairs', type=int, default=1536)
+    ap.add_argument('--chunk', type=int, default=1024, help='members per kernel pass')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only: every box in this build has a single MI355X; --gpus {args.gpus} '
+              f'is not supported (members shard across GPUs by design; see DESIGN.md).', file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print('bench.py needs a GPU', file=sys.stderr)
+        sys.exit(2)
+    if args.workload == 'step':
+        result = run_step(args)
+    else:
+        result = run_mlp(args)
     if not args.no_cpu_baseline:
-        result['cpu_baseline'] = cpu_baseline()
+        result['cpu_baseline'] = cpu_baseline_step() if args.workload == 'step' else cpu_baseline_mlp()
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,117 @@
+"""EGGROLL population step on the HIP kernels: the drop-in for `Eggroll` (train/val/eggroll.py:106-168).
+
+Perturbation bookkeeping (the fixed N(0, 1) buffer, per-step offsets, the member -> direction and
+member -> sequence layout) follows the reference exactly; the population forward, the fitness, the
+gradient estimate and (with noise_amd.optim.Adam) the optimizer step run in libnoise_hip.so.
+"""
+import torch
+
+from . import _lib
+from .population import Population, Weights
+
+BATCH = 8            # sequences per update (train/val/eggroll.py:28)
+SEED = 0
+PAIRS = 131072
+SIGMA = 0.002
+LR, BETAS = 0.001, (0.5, 0.95)
+WARMDOWN = 0.3
+CHUNK = 256          # pairs per batched forward in the reference; members per kernel pass here is `chunk`
+NOISE = 2 ** 28
+
+FITNESS = {'zscore': _lib.FITNESS_ZSCORE, 'rank': _lib.FITNESS_RANK}
+
+
+class Eggroll:
+    """Perturbation bookkeeping + the population step (train/val/eggroll.py:106-168).
+
+    chunk   -- members per forward pass of the kernels (a multiple of 2; bounded by activation memory);
+    head    -- 'fp32' or 'bf16' head (see noise_amd.population.Population);
+    fitness -- 'zscore' (the reference, :151-152) or 'rank' (centred ranks);
+    sigma, noise_len -- SIGMA and NOISE of the reference by default."""
+
+    def __init__(self, model, pairs, rank=0, world=1, chunk=512, head='fp32', fitness='zscore', sigma=SIGMA,
+                 noise_len=NOISE):
+        if chunk % 2:
+            raise ValueError('chunk must be even (antithetic pairs stay together)')
+        self.model, self.pairs, self.rank, self.world = model, pairs, rank, world
+        self.device = next(model.parameters()).device
+        self.params = dict(model.named_parameters())
+        self.sigma, self.noise_len = sigma, noise_len
+        self.fitness_mode = FITNESS[fitness]
+        self.buffer = torch.randn(noise_len, device=self.device,
+                                  generator=torch.Generator(self.device).manual_seed(SEED))
+        self.pop = Population(model, chunk=chunk, head=head)
+        self.last_losses = None
+
+    def offsets(self, step):
+        """name -> int64 [pairs] slice starts (train/val/eggroll.py:117-120)."""
+        g = torch.Generator(self.device).manual_seed(1_000_003 * SEED + step)
+        return {name: torch.randint(0, self.noise_len - sum(p.shape), (self.pairs,), device=self.device, generator=g)
+                for name, p in self.params.items()}
+
+    def noise(self, offsets, directions):
+        """name -> (a [n, out], b [n, in]) for matrices and embeddings, eps [n, L] for the mixing scalars
+        (train/val/eggroll.py:122-128), as contiguous tensors."""
+        out = {}
+        for name, p in self.params.items():
+            rows = self.buffer[offsets[name][directions, None] + torch.arange(sum(p.shape), device=self.device)]
+            out[name] = tuple(t.contiguous() for t in rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+        return out
+
+    @torch.no_grad()
+    def step(self, x, y, optimizer, step):
+        """Evaluate this rank's share of the population, gather the losses, rebuild the update
+        (train/val/eggroll.py:130-168). Returns the mean population loss."""
+        pairs = self.pairs
+        members = max(2 * pairs, 2 * len(x))
+        per_seq, per_rank = members // len(x), members // self.world
+        if per_seq % 2 or per_rank % 2 or members % len(x) or members % self.world:
+            raise ValueError('every sequence and every rank must host whole antithetic pairs')
+        offsets = self.offsets(step)
+        losses = torch.empty(per_rank, device=self.device)
+        weights = Weights(self.params, self.model.config, self.pop.head)
+        chunk = min(self.pop.chunk, per_seq)
+        lo, hi = self.rank * per_rank, (self.rank + 1) * per_rank
+        start = lo
+        while start < hi:
+            seq = start // per_seq
+            end = min(hi, start + chunk, (seq + 1) * per_seq)
+            directions = torch.arange(start, end, 2, device=self.device) % (2 * pairs) // 2
+            noise = self.noise(offsets, directions)
+            sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat((end - start) // 2)
+            losses[start - lo:end - lo] = self.pop.loss(self.params, noise, sign, x[seq], y[seq], pair_shift=1,
+                                                        weights=weights)
+            start = end
+        if self.world > 1:
+            gathered = [torch.empty_like(losses) for _ in range(self.world)]
+            torch.distributed.all_gather(gathered, losses)
+            losses = torch.cat(gathered)
+        self.last_losses = losses
+        nfit = len(losses) // 2
+        fit = torch.empty(nfit, device=self.device)
+        weight = torch.empty(pairs, device=self.device)
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call('noise_fitness', losses.data_ptr(), len(losses), pairs, self.fitness_mode, fit.data_ptr(),
+                  weight.data_ptr(), s)
+        grads = {name: torch.empty_like(p) for name, p in self.params.items()}
+        for d0 in range(0, pairs, CHUNK if pairs > 8 * CHUNK else pairs):
+            d1 = min(pairs, d0 + (CHUNK if pairs > 8 * CHUNK else pairs))
+            dirs = torch.arange(d0, d1, device=self.device)
+            w = weight[d0:d1].contiguous()
+            for name, n in self.noise(offsets, dirs).items():
+                p = self.params[name]
+                tmp = grads[name] if d0 == 0 else torch.empty_like(p)
+                if isinstance(n, tuple):
+                    a, b = n
+                    _lib.call('noise_outer_update', a.data_ptr(), a.shape[1], b.data_ptr(), b.shape[1], w.data_ptr(),
+                              d1 - d0, p.shape[0], p.shape[1], -1.0 / nfit, tmp.data_ptr(), s)
+                else:
+                    _lib.call('noise_outer_update', 0, 0, n.data_ptr(), n.shape[1], w.data_ptr(), d1 - d0, 1,
+                              p.shape[0], -1.0 / nfit, tmp.data_ptr(), s)
+                if d0 != 0:
+                    grads[name] += tmp
+        optimizer.zero_grad(set_to_none=True)
+        for name, p in self.params.items():
+            p.grad = grads[name]
+        optimizer.step()
+        return losses.mean().item()

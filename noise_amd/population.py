@@ -109,9 +109,51 @@ def _noise_rows(noise, name, lo, hi):
     return n[lo:hi]
 
 
+class StageTimer:
+    """Optional per-stage timing of forward_chunk: HIP events recorded on the launch stream around each
+    stage (embed, entry, qkv, attention, attn_proj, mlp, head); `ms` accumulates milliseconds per
+    stage once `collect()` has synchronised."""
+
+    def __init__(self):
+        self.pending = []
+        self.ms = {}
+        self.count = {}
+
+    def mark(self, stage):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(torch.cuda.current_stream())
+        return stage, ev
+
+    def close(self, opened):
+        stage, ev0 = opened
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev1.record(torch.cuda.current_stream())
+        self.pending.append((stage, ev0, ev1))
+
+    def collect(self):
+        torch.cuda.synchronize()
+        for stage, e0, e1 in self.pending:
+            self.ms[stage] = self.ms.get(stage, 0.0) + e0.elapsed_time(e1)
+            self.count[stage] = self.count.get(stage, 0) + 1
+        self.pending = []
+        return self.ms
+
+
+class _NoTimer:
+    def mark(self, stage):
+        return None
+
+    def close(self, opened):
+        pass
+
+
+TIMER = _NoTimer()
+
+
 def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, windows):
     """Losses of members 0..m-1 of `sign` (m = len(sign)) into out[0:m]; noise rows are indexed by
     p >> pair_shift. Follows train/val/eggroll.py:72-103 op for op."""
+    tm = TIMER
     cfg = W.config
     p = W.p
     m, T = sign.shape[0], idx.shape[0]
@@ -119,8 +161,10 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     ps = pair_shift
     a, b = noise['transformer.wte.weight']
     V = p['transformer.wte.weight'].shape[0]
+    t0 = tm.mark('embed')
     _lib.call('noise_embed_norm', _p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(sign), _p(idx), m, T, ps,
               _p(buf.x0), s)
+    tm.close(t0)
     eps_r, eps_0 = noise['resid_lambdas'], noise['x0_lambdas']
     lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
     for i in range(cfg.n_layer):
@@ -135,28 +179,42 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
             vw = p[f'value_embeds.{i}.weight']
             va, vb = noise[f'value_embeds.{i}.weight']
         x_in = buf.x0 if i == 0 else buf.x
+        t0 = tm.mark('entry')
         _lib.call('noise_block_entry', _p(x_in), _p(buf.x0), _p(buf.x), _p(buf.h), _p(buf.u_qkv), _p(bq), _p(bk),
                   _p(bv), lam_r.data_ptr() + 4 * i, lam_0.data_ptr() + 4 * i, eps_r.data_ptr() + 4 * i,
                   eps_0.data_ptr() + 4 * i, eps_r.stride(0), _p(gw) if ve else 0, _p(ga) if ve else 0,
                   _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, s)
+        tm.close(t0)
+        t0 = tm.mark('qkv')
         _lib.call('noise_qkv', _p(buf.h), _p(W.qkv[i]), _p(aq), _p(ak), _p(av), _p(buf.u_qkv), _p(sign), m, T, ps,
                   _p(cos), _p(sin), _p(buf.gate) if ve else 0, _p(vw) if ve else 0, V, _p(va) if ve else 0,
                   _p(vb) if ve else 0, _p(idx), _p(buf.qkv), s)
+        tm.close(t0)
         ap, bp = noise[pre + 'attn.c_proj.weight']
+        t0 = tm.mark('attention')
         _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], _p(bp), ps, _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
+        tm.close(t0)
+        t0 = tm.mark('attn_proj')
         _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, _p(sign), m, T,
                   ps, _p(buf.x), s)
+        tm.close(t0)
         af, bf_ = noise[pre + 'mlp.c_fc.weight']
         am, bm = noise[pre + 'mlp.c_proj.weight']
+        t0 = tm.mark('mlp_entry')
         _lib.call('noise_norm_dot', _p(buf.x), _p(buf.h), _p(bf_), _p(buf.u_fc), _p(sign), m, T, ps, s)
+        tm.close(t0)
+        t0 = tm.mark('mlp')
         _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
                   _p(buf.hidden), _p(buf.u_mlp), s)
         _lib.call('noise_lowrank_resid', _p(buf.hidden), _p(W.mproj[i]), F, D, _p(am), _p(buf.u_mlp), buf.parts,
                   _p(sign), m, T, ps, _p(buf.x), s)
+        tm.close(t0)
     ah, bh = noise['lm_head.weight']
     Vh = W.head_w.shape[0]
+    t0 = tm.mark('head')
     _lib.call('noise_head_ce', _p(buf.x), _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
               _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), s)
+    tm.close(t0)
 
 
 def check_noise(noise, shapes, rows):
