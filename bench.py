@@ -11,7 +11,9 @@ One step = all of that (Eggroll.step). Weights are the reference's seed-0 initia
 synthetic and resident in HBM before the timed region.
 
 `--workload mlp` times BASELINE config 1 alone (the rank-1-perturbed relu^2 MLP, P = 256, T = 2048,
-shared x). Prints one JSON line.
+shared x); `--workload attention` config 2 (windowed causal attention + per-head moments, P = 256,
+8 heads, T = 2048); `--workload head` config 3 (RMSNorm with gain + fp32 head + soft-capped CE,
+P = 512, T = 2048). Prints one JSON line.
 """
 import argparse
 import json
@@ -210,12 +212,100 @@ def run_mlp(args):
     }
 
 
+def _timed(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        fn()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps, ev0.elapsed_time(ev1) / steps
+
+
+def _common(args, value, ms_step, config, roofline):
+    return {'metric': METRIC, 'value': value, 'unit': 'member-tokens/s', 'n_gpus': 1, 'steps': args.steps,
+            'warmup': args.warmup, 'ms_per_step': ms_step, 'higher_is_better': True, 'scaling': 'weak',
+            'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic', 'config': config, 'roofline': roofline}
+
+
+def run_attention(args):
+    """Config 2: windowed causal attention + credit moments on q | k | v rows (P = 256, H = 8, T = 2048)."""
+    from noise_amd import _lib
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    P, window = 256, args.window
+    g = torch.Generator(device=dev).manual_seed(0)
+    qkv = torch.randn(P * T, 3 * D, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(P * T, D, device=dev, dtype=torch.bfloat16)
+    up = torch.empty(P * T, 8, device=dev)
+    bp = torch.randn(P, D, device=dev, generator=g)
+    mom = torch.empty(P, 8, 2, 64, device=dev)
+    ws = torch.empty(_lib.size_query('noise_attention_workspace_size', P, T), device=dev, dtype=torch.uint8)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, bp.data_ptr(), 0, y.data_ptr(), up.data_ptr(),
+                  mom.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    ms_step, ms_launch = _timed(step, args.steps, args.warmup)
+    pairs = sum(min(q, window) + 1 for q in range(T))
+    flop = 4 * 64 * 8 * P * pairs
+    achieved = flop / (ms_launch * 1e-3) / 1e12
+    return _common(args, P * T / (ms_step * 1e-3), ms_step,
+                   {'workload': 'config2_attention_moments', 'members': P, 'heads': 8, 'tokens': T, 'head_dim': 64,
+                    'window': window, 'outputs': 'y bf16, c_proj dot partials, per-head mean of y and y^2',
+                    'parallelism': 'single GPU'},
+                   {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
+                    'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None, 'kernel': 'attention_kernel + moments_reduce',
+                    'flop_per_launch': flop, 'ms_per_launch': ms_launch})
+
+
+def run_head(args):
+    """Config 3: RMSNorm (gain ~ U(0.9, 1.1)) + fp32 head (rank-1 perturbed) + soft-capped CE, P = 512."""
+    from noise_amd import _lib
+    from noise_amd.synthetic import antithetic_signs, zipf_tokens
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    P = 512
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(P * T, D, device=dev, generator=g).to(torch.bfloat16)
+    gain = 0.9 + 0.2 * torch.rand(D, device=dev, generator=g)
+    W = torch.randn(V, D, device=dev, generator=g) * D ** -0.5
+    a, b = torch.randn(P // 2, V, device=dev, generator=g), torch.randn(P // 2, D, device=dev, generator=g)
+    sign = antithetic_signs(P, SIGMA).to(dev)
+    tgt = zipf_tokens(T, seed=1)[1].to(dev)
+    s = torch.cuda.current_stream().cuda_stream
+    wsplit = torch.empty(V, 3 * D, device=dev, dtype=torch.bfloat16)
+    _lib.call('noise_cast_bf16', W.data_ptr(), wsplit.data_ptr(), W.numel(), D, s)
+    loss = torch.empty(P, device=dev)
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', P, T, V, 1), device=dev, dtype=torch.uint8)
+
+    def step():
+        _lib.call('noise_head_ce', h.data_ptr(), 1, gain.data_ptr(), wsplit.data_ptr(), V, 1, a.data_ptr(),
+                  b.data_ptr(), sign.data_ptr(), tgt.data_ptr(), P, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    ms_step, ms_launch = _timed(step, args.steps, args.warmup)
+    flop = 2 * D * V * P * T  # algorithmic fp32 head FLOPs (run as 3 bf16 MFMA passes)
+    achieved = flop / (ms_launch * 1e-3) / 1e12
+    return _common(args, P * T / (ms_step * 1e-3), ms_step,
+                   {'workload': 'config3_norm_head_ce', 'members': P, 'tokens': T, 'd_model': D, 'vocab': V,
+                    'head': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'sigma': SIGMA, 'parallelism': 'single GPU'},
+                   {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
+                    'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None,
+                    'kernel': 'head_norm + lowrank_gemm<EPI_CE> + ce_finalize', 'flop_per_launch': flop,
+                    'ms_per_launch': ms_launch})
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=3)
     ap.add_argument('--warmup', type=int, default=1)
-    ap.add_argument('--workload', choices=('step', 'mlp'), default='step')
+    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head'), default='step')
+    ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
     ap.add_argument('--pairs', type=int, default=1536)
     ap.add_argument('--chunk', type=int, default=1024, help='members per kernel pass')
     ap.add_argument('--no-cpu-baseline', action='store_true')
@@ -227,12 +317,9 @@ def main():
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
         sys.exit(2)
-    if args.workload == 'step':
-        result = run_step(args)
-    else:
-        result = run_mlp(args)
+    result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head}[args.workload](args)
     if not args.no_cpu_baseline:
-        result['cpu_baseline'] = cpu_baseline_step() if args.workload == 'step' else cpu_baseline_mlp()
+        result['cpu_baseline'] = cpu_baseline_mlp() if args.workload == 'mlp' else cpu_baseline_step()
     print(json.dumps(result), flush=True)
 
 

@@ -134,16 +134,19 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
                  float* upart, noise_stream_t stream);
 
-/* Per-member mean soft-capped cross-entropy (train/val/eggroll.py:94-103): h = norm(x);
+/* Per-member mean soft-capped cross-entropy (train/val/eggroll.py:94-103): h = norm(x) (times gain
+ * when gain is not null: the config-3 extension; null reproduces utils/model.py:46-47);
  * z = h W^T + s (h . b) a; z' = 15 tanh(z / 15); loss[p] = mean_t(logsumexp(z'_t) - z'_t[target_t]).
+ *   x       [members*T, 512] fp32 (x_bf16 == 0) or bf16 (x_bf16 != 0)
+ *   gain    [512] fp32 or null
  *   fp32_head != 0: w_head is the [vocab, 1536] split operand from noise_cast_bf16(split_cols = 512)
  *                   and the head is fp32-accurate (~2^-16 relative); 0: w_head bf16 [vocab, 512]
  *                   with the reference's autocast rounding points.
  * vocab % 256 == 0. Workspace: noise_head_ce_workspace_size(). */
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes);
-int noise_head_ce(const float* x, const void* w_head, int vocab, int fp32_head, const float* a, const float* b,
-                  const float* sign, const int64_t* targets, int members, int T, int pair_shift, float* loss,
-                  void* workspace, size_t workspace_bytes, noise_stream_t stream);
+int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
+                  const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
+                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, noise_stream_t stream);
 
 /* ---------------------------------------------------------------- EGGROLL update */
 

@@ -37,7 +37,7 @@ SIGNATURES = {
     'noise_mlp_fc_parts': [I],
     'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, P, P],
     'noise_head_ce_workspace_size': [I, I, I, I, SP],
-    'noise_head_ce': [P, P, I, I, P, P, P, P, I, I, I, P, P, S, P],
+    'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P],
     'noise_fitness': [P, I, I, I, P, P, P],
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],

@@ -292,9 +292,9 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
   return NOISE_OK;
 }
 
-int noise_head_ce(const float* x, const void* w_head, int vocab, int fp32_head, const float* a, const float* b,
-                  const float* sign, const int64_t* targets, int members, int T, int pair_shift, float* loss,
-                  void* workspace, size_t workspace_bytes, noise_stream_t stream) {
+int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
+                  const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
+                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, noise_stream_t stream) {
   size_t need = 0;
   if (int rc = noise_head_ce_workspace_size(members, T, vocab, fp32_head, &need)) return rc;
   if (bad_members(members, T, pair_shift) || !x || !w_head || !loss) return NOISE_EINVAL;
@@ -307,7 +307,7 @@ int noise_head_ce(const float* x, const void* w_head, int vocab, int fp32_head, 
   float* u = c.take<float>(M);
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
-  HeadNormArgs hn{x, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
+  HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
   if (int rc = head_norm_launch(hn, s)) return rc;
   LowrankGemmArgs g = base_args(hop, K, (long)T * K, w_head, K, vocab, a, sign, members, T, pair_shift);
   g.u = u;

@@ -1,20 +1,23 @@
-// Windowed causal attention of the population forward on gfx950 bf16 MFMA, with the c_proj
-// input-side dot and optional per-head output moments fused into the epilogue.
+// Windowed causal attention of the population forward on gfx950 MFMA, with the c_proj input-side
+// dot and optional per-head output moments fused into the epilogue.
 //
 // Reference: `attention` / `window_mask` (utils/model.py:14-31) called from population_loss
 // (train/val/eggroll.py:91): softmax(q k^T / sqrt(64)) v, a query at s seeing keys k with
 // s - window <= k <= s. q, k, v arrive bf16 (rotary and QK-norm already applied by the QKV GEMM).
 //
-// One workgroup = one (member, head, 128-query block); 4 waves of 32 queries. K/V blocks of 64 keys
-// go through a double-buffered LDS ring (K rows, V transposed to V^T so the key dimension is the
-// MFMA contraction dimension of both products). Per wave and key block:
-//   S^T = K Q^T   (MFMA A = K rows, B = Q rows): lane l holds 16 scores of query l % 16;
-//   online softmax in fp32 (exp2, row max/sum across the 4 lanes of a query by two shuffles);
-//   O^T += V^T P^T (MFMA A = V^T rows, B = P): the scores' register layout IS the B operand once
-//   the K rows of each 16-row MFMA block are interleaved (block kb, row r <-> key
-//   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so P never leaves registers. P enters as the bf16
-//   pair hi = bf16(P), lo = bf16(P - hi) (two MFMAs): the probabilities keep ~16 mantissa bits,
-//   so the only rounding of the attention path is that of q, k, v and y to bf16.
+// One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; two workgroups per CU.
+// K/V blocks of 128 keys go through a double-buffered LDS ring with one barrier per block: K rows as
+// they are (bf16), V transposed to V^T and converted to fp16 while it is staged, so the key dimension
+// is the MFMA contraction dimension of both products. Per wave and key block:
+//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 32 scores of query l % 16;
+//   online softmax in fp32 with a lazy maximum: the running max moves only when a block's maximum
+//   exceeds it by more than 2^8 in probability, so P <= 256 and the rescale of O is skipped unless
+//   some lane of the wave moved; exp2 on the FMA-folded argument (s - m) * log2(e) / 8;
+//   O^T += V^T P^T (fp16 MFMA, A = V^T rows, B = P): the scores' register layout IS the B operand
+//   once the K rows of each 16-row MFMA block are interleaved (block kb, row r <-> key
+//   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so P never leaves registers. P is rounded to
+//   fp16 (11-bit significand, the precision class of the reference's TF32 attention); V is bf16 and
+//   converts to fp16 exactly.
 // V^T rows are interleaved the same way (block db, row r <-> dim 16 (r / 4) + 4 db + r % 4), so each
 // lane ends with 16 contiguous output dims of one query: 16-byte stores, and the c_proj dot
 // y . b_proj over the head's 64 dims is a 4-lane reduction.
@@ -23,12 +26,25 @@
 
 namespace {
 
-constexpr int HD = 64, BQ = 128, BKV = 64, NWAVE = 4, NTH = NWAVE * 64;
+constexpr int HD = 64, BQ = 128, BKV = 128, NWAVE = 4, NTH = NWAVE * 64;
+constexpr int KB = BKV / 16;       // 16-key MFMA blocks per key block
+constexpr int KC = BKV / 32;       // 32-key contraction steps of P V
+constexpr float LAZY = 8.f;        // max moves only beyond 2^8 of headroom
 
-// Element offset of (row r, 16-byte chunk c) in a [64 x 64] bf16 LDS tile, chunk XOR-swizzled.
-__device__ __forceinline__ int tswz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// LDS row of key k (0..63) in the interleaved K tile, and of dim d in the interleaved V^T tile.
+__device__ __forceinline__ f32x4 mfma16x16x32_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// K tile [BKV keys][64 dims] bf16, rows of 128 B, 16-byte chunks XOR-swizzled by row.
+__device__ __forceinline__ int kswz(int r, int c) { return r * HD + ((c ^ (r & 7)) << 3); }
+// V^T tile [64 dims][BKV keys] fp16, rows of 256 B (16 chunks), chunk XOR-swizzled by row.
+__device__ __forceinline__ int vswz(int r, int c) { return r * BKV + ((c ^ (r & 7)) << 3); }
+
+// LDS row of key k (0..BKV-1) in the interleaved K tile, and of dim d in the interleaved V^T tile.
 __device__ __forceinline__ int krow(int k) {
   const int grp = k >> 5, w = k & 31;
   const int kb = 2 * grp + ((w & 7) >> 2), r = 4 * (w >> 3) + (w & 3);
@@ -46,7 +62,7 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
 
 __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) bf16 sk[2][BKV * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][HD * BKV];
+  __shared__ __attribute__((aligned(16))) f16 sv[2][HD * BKV];
   __shared__ float smom[NWAVE][2][HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
@@ -69,132 +85,134 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   const int k_lo = max(0, q0 - g.window), k_hi = min(g.T - 1, q0 + BQ - 1);
   const int j0 = k_lo / BKV, j1 = k_hi / BKV;
 
-  // global -> register staging of one K/V block: 2 K chunks and one V key pair per thread
-  uint4 rk[2], rv[2];
-  auto gload = [&](int j) {
-    const int kstart = j * BKV;
+  // global -> register staging of one key block: 4 K chunks and 2 V (key pair, dim chunk) items per
+  // thread; K is fetched at the top of the previous block, V after its softmax
+  uint4 rk[4], rv[2][2];
+  auto gload_k = [&](int j) {
+    const long kr0 = rbase + (long)j * BKV;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int item = tid + s * NTH, k = item >> 3, c = item & 7;
+      rk[s] = *reinterpret_cast<const uint4*>(qkv + (kr0 + k) * g.ldq + kcol + 8 * c);
+    }
+  };
+  auto gload_v = [&](int j) {
+    const long kr0 = rbase + (long)j * BKV;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      rk[s] = *reinterpret_cast<const uint4*>(qkv + (rbase + kstart + k) * g.ldq + kcol + 8 * c);
+      const int item = tid + s * NTH, kp = item >> 3, c = item & 7;
+      rv[s][0] = *reinterpret_cast<const uint4*>(qkv + (kr0 + 2 * kp) * g.ldq + vcol + 8 * c);
+      rv[s][1] = *reinterpret_cast<const uint4*>(qkv + (kr0 + 2 * kp + 1) * g.ldq + vcol + 8 * c);
     }
-    const int kp = tid >> 3, c = tid & 7;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-      rv[s] = *reinterpret_cast<const uint4*>(qkv + (rbase + kstart + 2 * kp + s) * g.ldq + vcol + 8 * c);
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < 4; ++s) {
       const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      *reinterpret_cast<uint4*>(&sk[buf][tswz(krow(k), c)]) = rk[s];
+      *reinterpret_cast<uint4*>(&sk[buf][kswz(krow(k), c)]) = rk[s];
     }
-    const int kp = tid >> 3, c = tid & 7;
-    const bf16* v0 = reinterpret_cast<const bf16*>(&rv[0]);
-    const bf16* v1 = reinterpret_cast<const bf16*>(&rv[1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int R = drow(8 * c + e);
-      // keys 2 kp, 2 kp + 1 of V^T row R: chunk kp / 4, element 2 (kp % 4)
-      bf16x2 pr = {v0[e], v1[e]};
-      *reinterpret_cast<bf16x2*>(&sv[buf][R * 64 + (((kp >> 2) ^ (R & 7)) << 3) + 2 * (kp & 3)]) = pr;
+    for (int s = 0; s < 2; ++s) {
+      const int item = tid + s * NTH, kp = item >> 3, c = item & 7;
+      const bf16* v0 = reinterpret_cast<const bf16*>(&rv[s][0]);
+      const bf16* v1 = reinterpret_cast<const bf16*>(&rv[s][1]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int R = drow(8 * c + e);
+        // keys 2 kp, 2 kp + 1 of V^T row R: chunk kp / 4, element 2 (kp % 4)
+        f16x2 pr = {(f16)(float)v0[e], (f16)(float)v1[e]};
+        *reinterpret_cast<f16x2*>(&sv[buf][vswz(R, kp >> 2) + 2 * (kp & 3)]) = pr;
+      }
     }
   };
 
-  const float scale = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
-  float m2[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};
+  const float c2 = 0.125f * 1.4426950408889634f;  // scores -> log2 units: 1/sqrt(64) * log2(e)
+  float mref[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};  // running max (score units) and sum per lane
   f32x4 o[2][4];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gload(j0);
+  gload_k(j0);
+  gload_v(j0);
   sstore(0);
   __syncthreads();
   for (int j = j0; j <= j1; ++j) {
     const int buf = (j - j0) & 1;
-    if (j < j1) gload(j + 1);
+    if (j < j1) gload_k(j + 1);
     const int kstart = j * BKV;
     const bf16* kt = sk[buf];
-    const bf16* vt = sv[buf];
-    // S^T = K Q^T for 4 key blocks x 2 query blocks
-    f32x4 s[2][4];
+    const f16* vt = sv[buf];
+    // S^T = K Q^T
+    f32x4 s[2][KB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      bf16x8 kf[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) kf[kk] = *reinterpret_cast<const bf16x8*>(&kt[tswz(16 * kb + (lane & 15), 4 * kk + grp)]);
+    for (int kb = 0; kb < KB; ++kb) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&kt[kswz(16 * kb + (lane & 15), grp)]);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&kt[kswz(16 * kb + (lane & 15), 4 + grp)]);
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-        a = mfma16x16x32(kf[0], qf[qb][0], a);
-        a = mfma16x16x32(kf[1], qf[qb][1], a);
-        s[qb][kb] = a;
+        a = mfma16x16x32(k0, qf[qb][0], a);
+        s[qb][kb] = mfma16x16x32(k1, qf[qb][1], a);
       }
     }
-    // mask (only blocks touching the causal edge or the window edge need it), online softmax
+    // mask (only blocks touching the causal edge or the window edge), lazy-max online softmax
     const bool full = kstart + BKV - 1 <= q0 && q0 + BQ - 1 - kstart <= g.window;
-    bf16x8 pf[2][2], pl[2][2];
+    f16x8 pf[2][KC];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
       float mx = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = s[qb][kb][e] * scale;
           if (!full) {
             const int key = kstart + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
-            if (key > q || q - key > g.window) v = -INFINITY;
+            if (key > q || q - key > g.window) s[qb][kb][e] = -INFINITY;
           }
-          s[qb][kb][e] = v;
-          mx = fmaxf(mx, v);
+          mx = fmaxf(mx, s[qb][kb][e]);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m2[qb], mx);
-      const float alpha = exp2f(m2[qb] - mnew);
-      m2[qb] = mnew;
-      float ps = 0.f;
-      float pv[4][4];
+      const bool move = mx * c2 > mref[qb] * c2 + LAZY;
+      if (__any(move)) {
+        const float mnew = move ? mx : mref[qb];
+        const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
+        mref[qb] = mnew;
+        lsum[qb] *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pv[kb][e] = exp2f(s[qb][kb][e] - mnew);
-          ps += pv[kb][e];
-        }
-      lsum[qb] = lsum[qb] * alpha + ps;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16 h0 = to_bf16(pv[2 * c][e]), h1 = to_bf16(pv[2 * c + 1][e]);
-          pf[qb][c][e] = h0;
-          pf[qb][c][4 + e] = h1;
-          pl[qb][c][e] = to_bf16(pv[2 * c][e] - (float)h0);
-          pl[qb][c][4 + e] = to_bf16(pv[2 * c + 1][e] - (float)h1);
-        }
+        for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
       }
+      const float mc = mref[qb] * c2;
+      float ps = 0.f;
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pv = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
+            ps += pv;
+            pf[qb][c][4 * hlf + e] = (f16)pv;
+          }
+      lsum[qb] += ps;
     }
+    // V of the next block is fetched once the scores are dead (register pressure)
+    if (j < j1) gload_v(j + 1);
     // O^T += V^T P^T
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&vt[tswz(16 * db + (lane & 15), 4 * c + grp)]);
+        const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[vswz(16 * db + (lane & 15), 4 * c + grp)]);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          o[qb][db] = mfma16x16x32(vf, pf[qb][c], o[qb][db]);
-          o[qb][db] = mfma16x16x32(vf, pl[qb][c], o[qb][db]);
-        }
+        for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma16x16x32_f16(vf, pf[qb][c], o[qb][db]);
       }
     if (j < j1) {
-      __syncthreads();  // everyone is done with buf ^ 1 (read two blocks ago)
+      // buf ^ 1 was last read in the previous iteration, which every wave finished before the barrier
+      // that closed it
       sstore(buf ^ 1);
       __syncthreads();
     }
@@ -274,8 +292,8 @@ __global__ void moments_reduce_kernel(const float* part, float* out, int nqb, in
 long attention_moment_partials(int members, int T, int H) { return (long)members * H * (T / BQ) * 2 * HD; }
 
 int attention_launch(const AttnArgs& g, hipStream_t s) {
-  if (!g.qkv || !g.y || g.members <= 0 || g.T <= 0 || g.T % BQ || g.H <= 0 || g.window < 0 || g.ldq % 8 ||
-      g.ldy % 8 || g.koff % 8 || g.voff % 8 || ((uintptr_t)g.qkv & 15) || ((uintptr_t)g.y & 15))
+  if (!g.qkv || !g.y || g.members <= 0 || g.T <= 0 || g.T % BQ || g.T % BKV || g.H <= 0 || g.window < 0 ||
+      g.ldq % 8 || g.ldy % 8 || g.koff % 8 || g.voff % 8 || ((uintptr_t)g.qkv & 15) || ((uintptr_t)g.y & 15))
     return NOISE_EINVAL;
   if (g.upart && (!g.b_proj || g.upart_ld < g.H || g.b_ld < g.H * HD)) return NOISE_EINVAL;
   if (g.mom && !g.mom_out) return NOISE_EINVAL;

@@ -46,7 +46,9 @@ struct NormDotArgs {
 };
 
 struct HeadNormArgs {
-  const float* x;
+  const void* x;         // [M, 512] fp32, or bf16 when x_bf16
+  int x_bf16;
+  const float* gain;     // [512] or null
   __bf16* h;             // fp32 head: [M, 1536] = [hi | hi | lo]; bf16 head: [M, 512]
   const float* b;        // [dirs, 512]
   float* u;              // [M]

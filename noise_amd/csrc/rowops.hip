@@ -150,8 +150,20 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
   const int p = (int)(row / g.T), dir = p >> g.pair_shift;
-  Row8 x = load8(g.x + row * D + lane * 8);
+  Row8 x;
+  if (g.x_bf16) {
+    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(g.x) + row * D + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x.v[e] = (float)xv[e];
+  } else {
+    x = load8(static_cast<const float*>(g.x) + row * D + lane * 8);
+  }
   rms_norm_row(x);
+  if (g.gain) {
+    const Row8 gv = load8(g.gain + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x.v[e] *= gv.v[e];
+  }
   if (g.fp32_head) {
     Row8 lo;
 #pragma unroll

@@ -212,7 +212,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     ah, bh = noise['lm_head.weight']
     Vh = W.head_w.shape[0]
     t0 = tm.mark('head')
-    _lib.call('noise_head_ce', _p(buf.x), _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
+    _lib.call('noise_head_ce', _p(buf.x), 0, 0, _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
               _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), s)
     tm.close(t0)
 

@@ -3,7 +3,7 @@ ONLY). Follows `train/val/eggroll.py:106-168` and `:205`, `:208-212`.
 
 Parity pins (tests/test_oracle.py, tests/test_golden.py): offsets / gathered noise against golden streams
 written by importing the reference in the build container; fitness against a hand-computed closed form
-(unbiased std, no centering); update against the explicit sum_j w_j a_j b_j^T; Adam against
+(unbiased std, no centering); rank_fitness (no reference function) against hand-ranked vectors with ties; update against the explicit sum_j w_j a_j b_j^T; Adam against
 torch.optim.AdamW (library routine); a whole reference step (losses, new weights) against the golden
 fixture of `Eggroll.step` with CHUNK and NOISE reduced.
 """
@@ -49,6 +49,20 @@ def fitness(losses, pairs):
     f = losses[1::2] - losses[0::2]
     f = f / (f.std() + 1e-8)
     weight = torch.zeros(pairs).index_add_(0, torch.arange(len(f)) % pairs, f)
+    return f, weight
+
+
+def rank_fitness(losses, pairs):
+    """Config-4 option: pair fitness f_j = L[2j+1] - L[2j] replaced by centred ranks
+    rank_j / (n - 1) - 0.5 (ties broken by index), folded onto directions like `fitness`. No reference
+    function: the reference z-scores (train/val/eggroll.py:151-152)."""
+    f = losses[1::2] - losses[0::2]
+    n = len(f)
+    order = torch.argsort(f, stable=True)
+    ranks = torch.empty(n, dtype=torch.float32)
+    ranks[order] = torch.arange(n, dtype=torch.float32)
+    f = ranks / (n - 1) - 0.5 if n > 1 else torch.zeros(n)
+    weight = torch.zeros(pairs).index_add_(0, torch.arange(n) % pairs, f)
     return f, weight
 
 

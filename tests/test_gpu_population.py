@@ -177,7 +177,7 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
         loss = torch.empty(m, device=DEV)
         ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV,
                          dtype=torch.uint8)
-        _lib.call('noise_head_ce', xd.data_ptr(), wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
+        _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
                   sd.data_ptr(), td.data_ptr(), m, T, 0, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
         torch.cuda.synchronize()
         if fp32:
@@ -186,6 +186,31 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
         else:
             ref = om.head_loss(h, W, a, b, sign, targets, 'bf16', 'bf16')
             assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
+
+
+def test_head_ce_config3_bf16_input_with_gain():
+    """Config 3: bf16 hidden states, RMSNorm gain ~ U(0.9, 1.1), fp32 head with rank-1 perturbation."""
+    g = torch.Generator().manual_seed(12)
+    m, T, V = 4, 256, 4096
+    h = torch.randn(m, T, 512, generator=g).bfloat16()
+    gain = 0.9 + 0.2 * torch.rand(512, generator=g)
+    W = torch.randn(V, 512, generator=g) * 512 ** -0.5
+    a, b = torch.randn(m // 2, V, generator=g), torch.randn(m // 2, 512, generator=g)
+    sign = antithetic_signs(m, 1e-3)
+    _, targets = zipf_tokens(T, seed=13)
+    s = torch.cuda.current_stream().cuda_stream
+    hd, gd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (h, gain, W, a, b, sign, targets))
+    log_case(f'head_ce config3 m={m} T={T}')
+    wd = torch.empty(V, 1536, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512, s)
+    loss = torch.empty(m, device=DEV)
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, 1), device=DEV, dtype=torch.uint8)
+    _lib.call('noise_head_ce', hd.data_ptr(), 1, gd.data_ptr(), wd.data_ptr(), V, 1, ad.data_ptr(), bd.data_ptr(),
+              sd.data_ptr(), td.data_ptr(), m, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
+    torch.cuda.synchronize()
+    rep = lambda t: t.repeat_interleave(2, 0)  # noqa: E731
+    ref = om.norm_head_ce(h.float(), gain, W, rep(a), rep(b), sign, targets)
+    assert (loss.cpu() - ref).abs().max() < 1e-4, (loss.cpu(), ref)
 
 
 # ---------------------------------------------------------------- whole population forward
@@ -331,8 +356,9 @@ def test_fitness_update_adam_match_oracle():
     # rank mode: a permutation of centred ranks
     _lib.call('noise_fitness', ld.data_ptr(), nl, pairs, 1, fit.data_ptr(), w.data_ptr(), s)
     torch.cuda.synchronize()
-    ranks = torch.argsort(torch.argsort(losses[1::2] - losses[0::2], stable=True), stable=True).float()
-    assert torch.allclose(fit.cpu(), ranks / (nl // 2 - 1) - 0.5, atol=1e-6)
+    fr, wr = oe.rank_fitness(losses, pairs)
+    assert torch.allclose(fit.cpu(), fr, atol=1e-6)
+    assert torch.allclose(w.cpu(), wr, atol=1e-6)
 
     log_case('outer_update')
     out_d, in_d = 70, 130

@@ -222,3 +222,50 @@ def test_member_directions():
     d = oe.member_directions(0, 4, 4)
     assert d.tolist() == [0, 1, 2, 3]
     assert oe.member_directions(8, 4, 4).tolist() == [0, 1, 2, 3]
+
+
+def test_rank_fitness_hand_ranked_with_ties():
+    # pair differences: [2, -1, 2, 0.5] -> ranks with ties by index: -1 -> 0, 0.5 -> 1, 2 (j=0) -> 2, 2 (j=2) -> 3
+    losses = torch.tensor([1.0, 3.0, 2.0, 1.0, 0.0, 2.0, 4.0, 4.5])
+    f, w = oe.rank_fitness(losses, 4)
+    assert torch.allclose(f, torch.tensor([2 / 3, 0.0, 1.0, 1 / 3]) - 0.5)
+    assert torch.allclose(w, f)
+    _, w2 = oe.rank_fitness(losses, 2)
+    assert torch.allclose(w2, torch.tensor([f[0] + f[2], f[1] + f[3]]))
+
+
+def test_mlp_population_equals_materialised_weights():
+    g = torch.Generator().manual_seed(10)
+    m, T, d, f = 2, 5, 16, 24
+    x = torch.randn(m, T, d, generator=g)
+    w1, w2 = torch.randn(f, d, generator=g), torch.randn(d, f, generator=g)
+    a1, b1 = torch.randn(m, f, generator=g), torch.randn(m, d, generator=g)
+    a2, b2 = torch.randn(m, d, generator=g), torch.randn(m, f, generator=g)
+    sign = torch.tensor([0.1, -0.1])
+    y = om.mlp_population(x, w1, w2, a1, b1, a2, b2, sign, 'fp32')
+    for p in range(m):
+        W1 = w1 + sign[p] * torch.outer(a1[p], b1[p])
+        W2 = w2 + sign[p] * torch.outer(a2[p], b2[p])
+        ref = torch.relu(x[p].double() @ W1.double().t()) ** 2 @ W2.double().t()
+        assert torch.allclose(y[p].double(), ref, rtol=1e-5, atol=1e-4)
+
+
+def test_norm_head_ce_with_gain_is_capped_cross_entropy():
+    g = torch.Generator().manual_seed(11)
+    m, T, D, V = 2, 4, 8, om.VOCAB
+    h = torch.randn(m, T, D, generator=g)
+    gain = 0.9 + 0.2 * torch.rand(D, generator=g)
+    W = torch.randn(V, D, generator=g)
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, D, generator=g)
+    sign = torch.tensor([0.05, -0.05])
+    tgt = torch.tensor([3, 0, V - 1, 17])
+    out = om.norm_head_ce(h, gain, W, a, b, sign, tgt)
+    for p in range(m):
+        hn = h[p].double() * torch.rsqrt(h[p].double().pow(2).mean(-1, keepdim=True) + 2 ** -23) * gain.double()
+        z = hn @ (W.double() + float(sign[p]) * torch.outer(a[p].double(), b[p].double())).t()
+        z = 15 * torch.tanh(z / 15)
+        ce = torch.logsumexp(z, -1) - z.gather(-1, tgt[:, None])[:, 0]
+        assert abs(float(out[p]) - float(ce.mean())) < 1e-4
+    # gain = 1 reproduces the reference head path
+    ones = om.norm_head_ce(h, torch.ones(D), W, a, b, sign, tgt)
+    assert torch.allclose(ones, om.head_loss(om.norm(h), W, a, b, sign, tgt), atol=1e-6)
