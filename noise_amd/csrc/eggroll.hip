@@ -64,46 +64,60 @@ __global__ void __launch_bounds__(1024) fitness_kernel(const float* __restrict__
   }
 }
 
-// G[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions (a null: a_j[o] = 1, out = 1).
-// 64 x 64 output tile per workgroup, 16 directions per LDS step, 4 x 4 outputs per thread.
+// G[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions (a null: a_j[o] = 1, out = 1),
+// on the fp32 MFMA (v_mfma_f32_16x16x4_f32): a 64 x 64 output tile per workgroup of 4 waves (32 x 32
+// each), directions staged through LDS 32 at a time with w_j folded into the a rows.
 __global__ void __launch_bounds__(256) outer_update_kernel(OuterUpdateArgs g) {
-  __shared__ float sa[16][64];
-  __shared__ float sb[16][64];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  constexpr int TK = 32;
+  __shared__ float sa[TK][64 + 4];
+  __shared__ float sb[TK][64 + 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
   const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int j0 = 0; j0 < g.ndir; j0 += 16) {
-    for (int e = tid; e < 16 * 64; e += 256) {
-      const int jj = e >> 6, c = e & 63, j = j0 + jj;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < g.ndir; j0 += TK) {
+#pragma unroll
+    for (int s = 0; s < TK * 64 / 256; ++s) {
+      const int e = tid + s * 256, jj = e >> 6, c = e & 63, j = j0 + jj;
       float av = 0.f, bv = 0.f;
       if (j < g.ndir) {
-        const float w = g.w[j];
-        av = (o0 + c < g.out) ? w * (g.a ? g.a[(long)j * g.a_ld + o0 + c] : 1.f) : 0.f;
-        bv = (i0 + c < g.in) ? g.b[(long)j * g.b_ld + i0 + c] : 0.f;
+        if (o0 + c < g.out) av = g.w[j] * (g.a ? g.a[(long)j * g.a_ld + o0 + c] : 1.f);
+        if (i0 + c < g.in) bv = g.b[(long)j * g.b_ld + i0 + c];
       }
       sa[jj][c] = av;
       sb[jj][c] = bv;
     }
     __syncthreads();
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      float ar[4], br[4];
+    for (int ks = 0; ks < TK / 4; ++ks) {
+      const int jj = 4 * ks + (lane >> 4);
+      float af[2], bf[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ar[r] = sa[jj][ty * 4 + r], br[r] = sb[jj][tx * 4 + r];
+      for (int f = 0; f < 2; ++f) {
+        af[f] = sa[jj][wm * 32 + 16 * f + (lane & 15)];
+        bf[f] = sb[jj][wn * 32 + 16 * f + (lane & 15)];
+      }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] += ar[r] * br[c];
+        for (int b = 0; b < 2; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
     }
     __syncthreads();
   }
+  // lane holds C[row = 4 (lane / 16) + e][col = lane % 16] of each 16 x 16 block
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int o = o0 + ty * 4 + r, i = i0 + tx * 4 + c;
-      if (o < g.out && i < g.in) g.grad[(long)o * g.in + i] = g.scale * acc[r][c];
-    }
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int o = o0 + wm * 32 + 16 * a + 4 * (lane >> 4) + e, i = i0 + wn * 32 + 16 * b + (lane & 15);
+        if (o < g.out && i < g.in) g.grad[(long)o * g.in + i] = g.scale * acc[a][b][e];
+      }
 }
 
 // torch.optim.AdamW (single-tensor path) with weight_decay = 0:

@@ -102,8 +102,8 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   return *reinterpret_cast<unsigned*>(&p);
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI>
-__global__ void __launch_bounds__(WGM * WGN * 64, 1)
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC, int EPI>
+__global__ void __launch_bounds__(WGM * WGN * 64, WGM * WGN * OCC / 4)
 lowrank_gemm_kernel(const LowrankGemmArgs g) {
   using C = Cfg<BM, BN, BK, STAGES, WGM, WGN>;
   constexpr int FM = C::FM, FN = C::FN, WM = C::WM, WN = C::WN, CW = C::CW;
@@ -438,18 +438,28 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
 #ifndef NOISE_GEMM_CFG
 #define NOISE_GEMM_CFG 0
 #endif
+// <BM, BN, BK, STAGES, WGM, WGN, OCC>: OCC workgroups of WGM x WGN waves share a CU.
 #if NOISE_GEMM_CFG == 0
-#define CFG_BIG 256, 256, 32, 4, 2, 4
-#define CFG_SMALL 256, 128, 32, 4, 4, 2
+#define CFG_BIG 256, 256, 32, 4, 2, 4, 1
+#define CFG_SMALL 256, 128, 32, 4, 4, 2, 1
 #elif NOISE_GEMM_CFG == 1
-#define CFG_BIG 256, 256, 64, 2, 2, 4
-#define CFG_SMALL 256, 128, 64, 2, 4, 2
+#define CFG_BIG 256, 256, 64, 2, 2, 4, 1
+#define CFG_SMALL 256, 128, 64, 2, 4, 2, 1
 #elif NOISE_GEMM_CFG == 3
-#define CFG_BIG 256, 256, 32, 3, 2, 4
-#define CFG_SMALL 256, 128, 32, 3, 4, 2
+#define CFG_BIG 256, 256, 32, 3, 2, 4, 1
+#define CFG_SMALL 256, 128, 32, 3, 4, 2, 1
+#elif NOISE_GEMM_CFG == 5
+#define CFG_BIG 256, 128, 32, 3, 2, 2, 2
+#define CFG_SMALL 256, 128, 32, 3, 2, 2, 2
+#elif NOISE_GEMM_CFG == 6
+#define CFG_BIG 256, 128, 32, 2, 2, 2, 2
+#define CFG_SMALL 256, 128, 32, 2, 2, 2, 2
+#elif NOISE_GEMM_CFG == 7
+#define CFG_BIG 128, 256, 32, 3, 2, 2, 2
+#define CFG_SMALL 128, 128, 32, 4, 2, 2, 2
 #endif
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC>
 constexpr int cfg_wave_n() { return BN / WGN; }
 
 int num_cus() {
@@ -463,15 +473,15 @@ int num_cus() {
   return cus;
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC, int EPI>
 int launch_cfg(const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.N % BN || g.K % 64) return NOISE_ENOTSUP;
   const long tiles = (long)((g.M + BM - 1) / BM) * (g.N / BN);
   if (tiles > 0x7fffffffL) return NOISE_ENOTSUP;
-  // one persistent workgroup per CU (LDS admits no second one), a multiple of 8 for the XCD split
-  long grid = std::min<long>(num_cus(), tiles);
+  // OCC persistent workgroups per CU, a multiple of 8 for the XCD split
+  long grid = std::min<long>((long)OCC * num_cus(), tiles);
   grid = (grid + 7) / 8 * 8;
-  hipLaunchKernelGGL((lowrank_gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, EPI>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((lowrank_gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, OCC, EPI>), dim3((unsigned)grid),
                      dim3(WGM * WGN * 64), 0, stream, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
