@@ -153,7 +153,7 @@ def run_step(args):
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
-                     'kernel': 'fused relu^2 MLP: lowrank_gemm<EPI_RELU2> (c_fc) + lowrank_gemm<EPI_RESID> (c_proj)',
+                     'kernel': 'fused relu^2 MLP: xs_relu2_kernel (c_fc, weight-resident) + lowrank_gemm<EPI_RESID> (c_proj)',
                      'flop_per_launch': mlp_flop, 'ms_per_launch': mlp_ms},
         'forward_tflops': flop_tok * P * T / (sum(v for k, v in stages.items()) / args.steps * 1e-3) / 1e12,
         'stage_ms_per_step': {k: v / args.steps for k, v in stages.items()},
@@ -207,7 +207,7 @@ def run_mlp(args):
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
-                     'kernel': 'noise_lowrank_mlp (rowdot + relu2 GEMM + proj GEMM)',
+                     'kernel': 'noise_lowrank_mlp (rowdot + xs_relu2_kernel + lowrank_gemm<EPI_STORE> proj)',
                      'flop_per_launch': flop, 'ms_per_launch': ms_launch},
     }
 

@@ -62,7 +62,7 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
  *   x       bf16 [members, T, d] (x_mstride as above)
  *   w_fc    bf16 [f, d];  a_fc [dirs, f], b_fc [dirs, d]
  *   w_proj  bf16 [d, f];  a_proj [dirs, d], b_proj [dirs, f]
- *   y_f32 / y_bf16 / accumulate as in noise_lowrank_linear; d % 128 == 0, f % 256 == 0.
+ *   y_f32 / y_bf16 / accumulate as in noise_lowrank_linear; d == 512, f % 256 == 0, T % 32 == 0.
  * Workspace: noise_lowrank_mlp_workspace_size(). */
 int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* bytes);
 int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc, const void* w_proj, int d, int f,
@@ -117,18 +117,22 @@ int noise_attention(const void* qkv, int members, int T, int window, const float
                     void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream);
 
-/* resid += lowrank(x, w) with the input-side dot given as u_parts partial sums per row (u [rows,
- * u_parts]): the attention c_proj (u from noise_attention) and the MLP c_proj.
- * Replaces `x = x + linear('attn.c_proj.weight', y)` (train/val/eggroll.py:92). */
+/* resid += lowrank(x, w) with the input-side dot of row r given as u_parts partial sums
+ * u[r * u_row_stride + q * u_part_stride]: the attention c_proj (u from noise_attention: row stride 8,
+ * part stride 1) and the MLP c_proj (u from noise_mlp_fc: row stride 1, part stride members*T).
+ * Replaces `x = x + linear('attn.c_proj.weight', y)` (train/val/eggroll.py:92) and the MLP's
+ * `x = x + linear('mlp.c_proj.weight', ...)` (:93). */
 int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,
-                        const float* sign, int members, int T, int pair_shift, float* resid, noise_stream_t stream);
+                        long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
+                        float* resid, noise_stream_t stream);
 
 /* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). */
 int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
                    int pair_shift, noise_stream_t stream);
 
-/* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] and its dot partials with b_proj
- * (upart [members*T, noise_mlp_fc_parts(f)]) for the following noise_lowrank_resid. */
+/* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] and its dot partials with bf16(b_proj),
+ * part-major: upart [noise_mlp_fc_parts(f), members*T] (one partial per 256 columns), for the
+ * following noise_lowrank_resid. d == 512, f % 256 == 0, T % 32 == 0 (NOISE_ENOTSUP otherwise). */
 int noise_mlp_fc_parts(int f);
 int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,

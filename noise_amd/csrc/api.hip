@@ -40,6 +40,7 @@ LowrankGemmArgs base_args(const void* x, long x_ld, long x_mstride, const void* 
   g.ra[0] = a;
   g.seg_n = out;
   g.ra_ld = out;
+  g.u_qstride = 1;
   g.round_bf16 = 1;
   return g;
 }
@@ -88,11 +89,11 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
 }
 
 int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* bytes) {
-  if (members <= 0 || T <= 0 || d <= 0 || f <= 0 || !bytes || !lowrank_gemm_parts(f)) return NOISE_EINVAL;
+  if (members <= 0 || T <= 0 || d <= 0 || f <= 0 || !bytes || !xs_relu2_parts(f)) return NOISE_EINVAL;
   const size_t M = (size_t)members * T;
   Carve c(nullptr);
   c.take<float>(M);                            // u_fc
-  c.take<float>(M * lowrank_gemm_parts(f));    // partial dots h.b_proj
+  c.take<float>(M * xs_relu2_parts(f));        // partial dots h.b_proj, part-major
   c.take<bf16>(M * f);                         // hidden h
   *bytes = c.used;
   return NOISE_OK;
@@ -111,7 +112,7 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   const size_t M = (size_t)members * T;
   Carve c(workspace);
   float* u_fc = c.take<float>(M);
-  const int parts = lowrank_gemm_parts(f);
+  const int parts = xs_relu2_parts(f);
   float* upart = c.take<float>(M * parts);
   bf16* hid = c.take<bf16>(M * f);
   if (int rc = rowdot_launch(static_cast<const bf16*>(x), x_ld, x_mstride, (int)M, d, T, pair_shift, b_fc, d, u_fc, s))
@@ -130,7 +131,8 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   LowrankGemmArgs g2 = base_args(hid, f, (long)T * f, w_proj, f, d, a_proj, sign, members, T, pair_shift);
   g2.u = upart;
   g2.u_parts = parts;
-  g2.u_ld = parts;
+  g2.u_ld = 1;
+  g2.u_qstride = (long)M;
   g2.out_f32 = y_f32;
   g2.out_bf16 = static_cast<bf16*>(y_bf16);
   g2.ldo = d;
@@ -243,12 +245,14 @@ int noise_attention(const void* qkv, int members, int T, int window, const float
 }
 
 int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,
-                        const float* sign, int members, int T, int pair_shift, float* resid, noise_stream_t stream) {
-  if (bad_members(members, T, pair_shift) || u_parts <= 0) return NOISE_EINVAL;
+                        long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
+                        float* resid, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift) || u_parts <= 0 || u_row_stride < 1 || u_part_stride < 1) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, a, sign, members, T, pair_shift);
   g.u = u;
   g.u_parts = u_parts;
-  g.u_ld = u_parts;
+  g.u_ld = (int)u_row_stride;
+  g.u_qstride = u_part_stride;
   g.out_f32 = resid;
   g.ldo = out;
   return lowrank_gemm_launch(EPI_RESID, g, static_cast<hipStream_t>(stream));
@@ -261,12 +265,12 @@ int noise_norm_dot(const float* x, void* h, const float* b, float* u, const floa
   return norm_dot_launch(g, static_cast<hipStream_t>(stream));
 }
 
-int noise_mlp_fc_parts(int f) { return lowrank_gemm_parts(f); }
+int noise_mlp_fc_parts(int f) { return xs_relu2_parts(f); }
 
 int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
                  float* upart, noise_stream_t stream) {
-  if (bad_members(members, T, pair_shift) || !lowrank_gemm_parts(f)) return NOISE_EINVAL;
+  if (bad_members(members, T, pair_shift) || !xs_relu2_parts(f)) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(h, d, (long)T * d, w_fc, d, f, a_fc, sign, members, T, pair_shift);
   g.u = u;
   g.u_parts = 1;
@@ -276,7 +280,7 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
   g.rb_next = b_proj;
   g.rb_next_ld = f;
   g.upart_out = upart;
-  g.upart_ld = lowrank_gemm_parts(f);
+  g.upart_ld = xs_relu2_parts(f);
   return lowrank_gemm_launch(EPI_RELU2, g, static_cast<hipStream_t>(stream));
 }
 

@@ -7,6 +7,7 @@
 enum : int {
   EPI_STORE = 0,  // out = lowrank(x)                       -> fp32 and/or bf16 store
   EPI_RELU2 = 1,  // h = bf16(relu(lowrank(x))^2)            -> bf16 store + partial dots h.b_next per row
+                  //                                         (weight-resident kernel of gemm_xs.hip, K = 512)
   EPI_RESID = 2,  // resid += lowrank(x)                     -> fp32 read-modify-write
   EPI_QKV = 3,    // q|k|v = lowrank(x) per 512-column segment; rotary + RMSNorm on q and k, gated value
                   // embedding added to v                   -> bf16 store
@@ -31,21 +32,24 @@ struct LowrankGemmArgs {
   const float* ra[3];
   int seg_n;
   long ra_ld;
-  // Input-side dots x.b, as u_parts partial sums: row r, segment s: sum_q u[r * u_ld + s * u_parts + q].
+  // Input-side dots x.b, as u_parts partial sums: row r, segment s: sum_q u[r * u_ld + (s * u_parts + q) * u_qstride]
+  // (u_qstride = 1: row-major partials; u_ld = 1, u_qstride = rows: part-major).
   const float* u;
   int u_parts;
   int u_ld;
+  long u_qstride;
   // 1: autocast rounding points (the dense product and the dot rounded to bf16); 0: fp32 throughout.
   int round_bf16;
   // outputs
   float* out_f32;     // EPI_STORE (optional) / EPI_RESID (accumulated in place)
   __bf16* out_bf16;   // EPI_STORE (optional) / EPI_RELU2 / EPI_QKV
   long ldo;
-  // EPI_RELU2: partial dots of the bf16 output with the next layer's input-side vector b_next
+  // EPI_RELU2: partial dots of the bf16 output with the next layer's input-side vector b_next, part-major
+  // [xs_relu2_parts(N), M]. EPI_CE: per-row partial sums, row-major [M, upart_ld].
   const float* rb_next;
   long rb_next_ld;
-  float* upart_out;   // [M, upart_ld]
-  int upart_ld;       // = lowrank_gemm_parts(N)
+  float* upart_out;
+  int upart_ld;       // EPI_CE: = lowrank_gemm_parts(N)
   // EPI_QKV: rotary tables (bf16 [>= T, 32]); optional gated value embedding for the v segment:
   // v += gate[r, head] * (ve_w[idx[t]] + s_p ve_a[dir, idx[t]] ve_b[dir]).
   const __bf16* rot_cos;
@@ -61,6 +65,12 @@ struct LowrankGemmArgs {
   float* ce_tgt;
 };
 
-// Number of per-row partials EPI_RELU2 / EPI_CE write for an N-column output (0: N unsupported).
+// Number of per-row partials EPI_CE writes for an N-column output (0: N unsupported).
 int lowrank_gemm_parts(int N);
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream);
+
+// The weight-resident K = 512 relu^2 GEMM (gemm_xs.hip): partials per row it writes for N columns (0: N
+// unsupported), whether it tiles the shape, and the launch.
+int xs_relu2_parts(int N);
+bool xs_relu2_supported(const LowrankGemmArgs& g);
+int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream);

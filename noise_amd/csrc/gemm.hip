@@ -110,7 +110,6 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   constexpr int SUB = BK / 32;
   __shared__ __attribute__((aligned(1024))) bf16 smem[STAGES * C::STAGE];
   __shared__ __attribute__((aligned(16))) float ep_a[BN];             // a_p over the tile's columns
-  __shared__ __attribute__((aligned(16))) float ep_b[BN];             // bf16(b_next) (EPI_RELU2)
   __shared__ float ep_u[C::UGROUPS][BM];                               // partial sums of x.b per row
   __shared__ float ep_sign;
 
@@ -166,26 +165,17 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto prefetch_ep = [&](int m0, int n0) {
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
     const int dir = pfirst >> g.pair_shift, seg = n0 / g.seg_n, ncol = n0 - seg * g.seg_n;
-    if (tid < BN / 4) {
-      pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
-    } else if (EPI == EPI_RELU2 && tid < BN / 2) {
-      pre_ab = *reinterpret_cast<const float4*>(g.rb_next + (long)dir * g.rb_next_ld + n0 + 4 * (tid - BN / 4));
-    }
+    if (tid < BN / 4) pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
     if (tid == 0) pre_sign = pfirst == plast ? g.sign[pfirst] : 0.f;
     const int row = min(m0 + tid % BM, g.M - 1), grp = tid / BM;
     const int q0 = grp * g.u_parts / C::UGROUPS, q1 = (grp + 1) * g.u_parts / C::UGROUPS;
-    const float* up = g.u + (long)row * g.u_ld + seg * g.u_parts;
+    const float* up = g.u + (long)row * g.u_ld + (long)seg * g.u_parts * g.u_qstride;
     float u = 0.f;
-    for (int q = q0; q < q1; ++q) u += up[q];
+    for (int q = q0; q < q1; ++q) u += up[q * g.u_qstride];
     pre_u = u;
   };
   auto stage_ep = [&]() {
-    if (tid < BN / 4) {
-      *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
-    } else if (EPI == EPI_RELU2 && tid < BN / 2) {
-      const float4 b = pre_ab;
-      *reinterpret_cast<float4*>(&ep_b[4 * (tid - BN / 4)]) = make_float4(bf16r(b.x), bf16r(b.y), bf16r(b.z), bf16r(b.w));
-    }
+    if (tid < BN / 4) *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
     if (tid == 0) ep_sign = pre_sign;
     ep_u[tid / BM][tid % BM] = pre_u;
   };
@@ -346,31 +336,6 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
             o[j] = r;
           }
         }
-      } else if constexpr (EPI == EPI_RELU2) {
-        float dot = 0.f;
-        unsigned hp[CW / 2];
-#pragma unroll
-        for (int e = 0; e < CW; e += 2) {
-          float b0, b1;
-          if (uniform) {
-            b0 = ep_b[lcol + e], b1 = ep_b[lcol + e + 1];
-          } else {
-            const float* brow = g.rb_next + (long)dir * g.rb_next_ld + cb;
-            b0 = bf16r(brow[e]), b1 = bf16r(brow[e + 1]);
-          }
-          const float r0v = fmaxf(v[e], 0.f), r1v = fmaxf(v[e + 1], 0.f);
-          const unsigned h2 = pack_bf16(r0v * r0v, r1v * r1v);
-          hp[e / 2] = h2;
-          dot += bf16_lo(h2) * b0 + bf16_hi(h2) * b1;
-        }
-        if (live) {
-          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
-#pragma unroll
-          for (int e = 0; e < CW / 2; e += 4) o[e / 4] = make_uint4(hp[e], hp[e + 1], hp[e + 2], hp[e + 3]);
-        }
-        dot += __shfl_xor(dot, 16, 64);
-        dot += __shfl_xor(dot, 32, 64);
-        if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = dot;
       } else if constexpr (EPI == EPI_QKV) {
         // the wave's WN = 64 columns are one head; lane group lane / 16 holds head dims 16 (lane / 16) ..
         const int t = rrow % g.T;
@@ -504,12 +469,12 @@ int lowrank_gemm_parts(int N) {
 
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
-      g.u_ld < g.u_parts || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
+      g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
-      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.N / g.seg_n > 3)
+      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.N / g.seg_n > 3 || g.u_qstride < 1)
     return NOISE_EINVAL;
   const int nseg = g.N / g.seg_n;
-  if (g.u_ld < nseg * g.u_parts) return NOISE_EINVAL;
+  if (g.u_qstride == 1 && g.u_ld < nseg * g.u_parts) return NOISE_EINVAL;
   for (int s = 0; s < nseg; ++s)
     if (!g.ra[s] || ((uintptr_t)g.ra[s] & 15)) return NOISE_EINVAL;
   if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return NOISE_EINVAL;
@@ -519,10 +484,8 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
       if (!g.out_f32 && !g.out_bf16) return NOISE_EINVAL;
       return launch_epi<EPI_STORE>(g, stream);
     case EPI_RELU2:
-      if (!g.out_bf16 || !g.rb_next || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N) ||
-          g.rb_next_ld % 4 || ((uintptr_t)g.rb_next & 15))
-        return NOISE_EINVAL;
-      return launch_epi<EPI_RELU2>(g, stream);
+      if (!xs_relu2_supported(g)) return NOISE_ENOTSUP;
+      return xs_relu2_launch(g, stream);
     case EPI_RESID:
       if (!g.out_f32) return NOISE_EINVAL;
       return launch_epi<EPI_RESID>(g, stream);

@@ -1,0 +1,305 @@
+// Weight-resident low-rank-perturbed GEMM for K = 512 on gfx950 bf16 MFMA, with the relu^2 epilogue of the
+// MLP c_fc: h = bf16(relu(bf16(x W^T) + s_p bf16(x.b_p) a_p)^2) and the partial dots h . bf16(b_next).
+//
+// Reference: `lowrank` (train/val/eggroll.py:56-58) feeding `F.relu(...).square()` of the MLP
+// (utils/model.py:106-107, train/val/eggroll.py:93) under bf16 autocast (:144); the dot with the c_proj
+// input-side vector is the `(x @ b)` of the following `lowrank`, computed here from the bf16 h the kernel
+// already holds.
+//
+// Why this shape. With 256 x 256 output tiles every tile re-reads both operands from L2: K = 512 GEMMs then
+// need (256 + 256) rows of K per 256^2 outputs, and the L2 -> CU path (about 17 TB/s measured on MI355X)
+// caps the c_fc GEMM near the MFMA time. Here a workgroup owns one 256-column slice of W for the whole
+// launch and keeps it in registers (wave w: columns 32 w .. 32 w + 31, all 512 K = 128 VGPRs as MFMA A
+// fragments), so only x streams: half the L2 traffic per FLOP.
+//
+// Schedule. 8 waves (2 per SIMD), one workgroup per CU. Workgroup b serves XCD b % 8; on each XCD the
+// N / 256 slices form groups that walk the same 32-row blocks of x in the same order (the XCD's contiguous
+// range of blocks, strided over the groups), so each x block is fetched from HBM once and served from that
+// XCD's L2 to every slice.
+//
+// x path. Blocks of 32 rows x 512 K (32 KiB) stream through a 4-deep LDS ring with direct global -> LDS
+// loads (global_load_lds_dwordx4). The LDS image of a block is fragment-major: fragment d (k step d / 2,
+// row half d % 2) is 1 KiB at byte d * 1024, in exactly the MFMA B-operand lane order, so every ds_read_b128
+// is lane-contiguous. The loads are issued from inline assembly: the compiler would otherwise make every
+// LDS read wait for every outstanding LDS-bound load (vmcnt(0)), which drains the ring. The kernel waits
+// for them itself: vector memory operations complete in issue order, so "block k landed" is
+// s_waitcnt vmcnt(n) with n = the operations issued after block k's loads, followed by s_barrier.
+//
+// Epilogue overlap. Iteration k runs the MFMAs of block k and, interleaved one stage per MFMA k step (a
+// scheduling barrier between steps keeps the interleave), the epilogue of block k - 1 from the other
+// accumulator set: the epilogue VALU work issues in the shadow of the MFMAs.
+//
+// h . b_next. Each lane holds 8 consecutive bf16 h of a row and the matching bf16(b_next) pairs: 4
+// v_dot2_f32_bf16 per row, two lane shuffles give the wave's 32-column partial, and the 8 wave partials of a
+// row are summed in LDS (fixed order) by wave 0, which stores one partial per (slice, row): upart_out is
+// part-major [N / 256][M], 128 contiguous bytes per block.
+#include <algorithm>
+
+#include "common.h"
+#include "gemm.h"
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int R = 32;                 // rows per block
+constexpr int NBUF = 4;               // LDS ring depth (blocks)
+constexpr int NW = 8;                 // waves per workgroup
+constexpr int BN = 256;               // columns per workgroup slice (32 per wave)
+constexpr int KD = 512;               // K
+constexpr int KS = KD / 32;           // MFMA k steps per block
+constexpr int XBYTES = R * KD * 2;    // 32 KiB of x per block
+constexpr int VEC = 512;              // per-wave vector area: a (128 B) | b_next (128 B) | u (128 B) | .. | sign
+constexpr int SIGN_OFF = VEC - 8;
+constexpr int DMA_PER_BLOCK = 6;      // per wave and block: 4 x fragments, a|b_next|u, sign
+constexpr int STORES_PER_EPI = 2;     // lower bound on an epilogue's store instructions (two h rows)
+
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N <= 63, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// global_load_lds_dword{x4}: each active lane's bytes land at lds + size * lane. M0 is saved and restored.
+__device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(src), "s"(off)
+               : "memory");
+}
+__device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(src), "s"(off)
+               : "memory");
+}
+
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+  bf16x2 p = {to_bf16(a), to_bf16(b)};
+  return *reinterpret_cast<unsigned*>(&p);
+}
+__device__ __forceinline__ bf16x2 as_bf16x2(unsigned v) { return *reinterpret_cast<bf16x2*>(&v); }
+
+__global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[NBUF * XBYTES];
+  __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
+  __shared__ __attribute__((aligned(16))) float red[2][R][NW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
+  const int nslices = g.N / BN;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int streams = (gridDim.x >> 3) / nslices;
+  const int nslice = slot % nslices, stream = slot / nslices;
+  const int nb_all = g.M / R;
+  const int lo = (int)((long)xcd * nb_all / 8), hi = (int)((long)(xcd + 1) * nb_all / 8);
+  // this workgroup's blocks: lo + stream + k * streams, k = 0 .. nb - 1 (the same for every wave)
+  const int nb = stream < streams && lo + stream < hi ? (hi - lo - stream + streams - 1) / streams : 0;
+  if (nb == 0) return;
+  const int fw = nslice * BN + wave * 32;  // first column of this wave
+
+  // ---- resident W: fragment [j][s] holds W row fw + 8 (r >> 2) + 4 j + (r & 3), r = lane & 15, k = 32 s + 8 grp.
+  // MFMA output element e of column block j in lane l is then column fw + 8 (l >> 4) + 4 j + e: the lane's 8
+  // columns are contiguous.
+  bf16x8 wr[2][KS];
+  {
+    const int r = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bf16* wp = g.W + (long)(fw + 8 * (r >> 2) + 4 * j + (r & 3)) * g.ldw + 8 * grp;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) wr[j][s] = *reinterpret_cast<const bf16x8*>(wp + 32 * s);
+    }
+  }
+  // the resident fragments have landed before any LDS-bound load is issued, so no wait below covers them
+  wait_vm_lgkm0<0>();
+
+  auto blk_of = [&](int k) { return lo + stream + k * streams; };
+
+  // ---- loads of block k into ring slot k % NBUF. Wave w fills x fragments d = 4 w + q: lane L loads row
+  // 16 (d & 1) + (L & 15), k 32 (d >> 1) + 8 (L >> 4). Lanes 0-7 load a_p, 8-15 b_next over the wave's 32
+  // columns, 16-23 the block's 32 input-side dots; lane 0 the member's sign.
+  auto issue = [&](int k) {
+    const int buf = k % NBUF, row0 = blk_of(k) * R;
+    const int p = row0 / g.T, t0 = row0 - p * g.T, dir = p >> g.pair_shift;
+    const bf16* abase = g.A + (long)p * g.a_mstride;
+    char* xsl = smem + buf * XBYTES;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int d = 4 * wave + q;
+      dma_x4(abase + (long)(t0 + 16 * (d & 1) + (lane & 15)) * g.lda + 32 * (d >> 1) + 8 * grp, xsl + d * 1024);
+    }
+    const float* vsrc = lane < 8 ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
+                        : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
+                                    : g.u + row0 + 4 * (lane - 16);
+    if (lane < 24) dma_x4(vsrc, &svec[buf][wave][0]);
+    if (lane == 0) dma_x1(g.sign + p, &svec[buf][wave][SIGN_OFF]);
+  };
+
+  // Block k has landed for this wave once at most nd * DMA_PER_BLOCK + ne * STORES_PER_EPI later operations
+  // are outstanding: the nd later load groups and the stores of the ne epilogues issued since.
+  auto wait_block = [&](int nd, int ne) {
+    constexpr int D = DMA_PER_BLOCK, S = STORES_PER_EPI;
+    switch (nd * 3 + ne) {
+      case 0: wait_vm_lgkm0<0>(); break;
+      case 1: wait_vm_lgkm0<S>(); break;
+      case 2: wait_vm_lgkm0<2 * S>(); break;
+      case 3: wait_vm_lgkm0<D>(); break;
+      case 4: wait_vm_lgkm0<D + S>(); break;
+      case 5: wait_vm_lgkm0<D + 2 * S>(); break;
+      case 6: wait_vm_lgkm0<2 * D>(); break;
+      case 7: wait_vm_lgkm0<2 * D + S>(); break;
+      default: wait_vm_lgkm0<2 * D + 2 * S>(); break;
+    }
+  };
+
+  f32x4 accA[2][2], accB[2][2];
+  float ev_a[8], ev_u[2], ev_dot[2];
+  unsigned ev_bp[4], ev_h[2][4];
+
+  // Stage st (0 .. 15) of the epilogue of block pk (ring slot pbuf) from acc:
+  //   0: vectors from LDS; 1-4 / 7-10: column pairs of row half 0 / 1; 5 / 11: h store and first shuffle;
+  //   6 / 12: second shuffle and the wave partial into LDS.
+  auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
+    const char* vw = &svec[pbuf][wave][0];
+    if (st == 0) {
+      const float4 a0 = *reinterpret_cast<const float4*>(vw + 32 * grp);
+      const float4 a1 = *reinterpret_cast<const float4*>(vw + 32 * grp + 16);
+      ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
+      ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
+      const float4 b0 = *reinterpret_cast<const float4*>(vw + 128 + 32 * grp);
+      const float4 b1 = *reinterpret_cast<const float4*>(vw + 128 + 32 * grp + 16);
+      ev_bp[0] = pack_bf16(b0.x, b0.y), ev_bp[1] = pack_bf16(b0.z, b0.w);
+      ev_bp[2] = pack_bf16(b1.x, b1.y), ev_bp[3] = pack_bf16(b1.z, b1.w);
+      const float sg = *reinterpret_cast<const float*>(vw + SIGN_OFF);
+      const float* uw = reinterpret_cast<const float*>(vw + 256);
+      ev_u[0] = sg * bf16r(uw[lane & 15]);
+      ev_u[1] = sg * bf16r(uw[16 + (lane & 15)]);
+      return;
+    }
+    if (st > 12) return;
+    const int i = st < 7 ? 0 : 1, sub = st - (i ? 7 : 1);
+    const int lr = 16 * i + (lane & 15);
+    if (sub < 4) {
+      // columns c, c + 1 of the lane's 8: dense part rounded to bf16 (autocast GEMM output), fp32
+      // rank-1 correction, relu^2, bf16
+      const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
+      const float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
+      const float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+      const float r0 = fmaxf(v0, 0.f), r1 = fmaxf(v1, 0.f);
+      const unsigned h2 = pack_bf16(r0 * r0, r1 * r1);
+      ev_h[i][sub] = h2;
+      ev_dot[i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(h2), as_bf16x2(ev_bp[sub]), sub == 0 ? 0.f : ev_dot[i], false);
+    } else if (sub == 4) {
+      const long row = (long)blk_of(pk) * R + lr;
+      *reinterpret_cast<uint4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) =
+          make_uint4(ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]);
+      ev_dot[i] += __shfl_xor(ev_dot[i], 16, 64);
+    } else {
+      ev_dot[i] += __shfl_xor(ev_dot[i], 32, 64);
+      red[pk & 1][lr][wave] = ev_dot[i];  // the row's four lanes write the same value
+    }
+  };
+  // wave 0: the 8 wave partials of block pk's rows (written before the last barrier) -> one partial per row
+  auto sum_partials = [&](int pk) {
+    if (wave == 0 && lane < R) {
+      const float4 p0 = *reinterpret_cast<const float4*>(&red[pk & 1][lane][0]);
+      const float4 p1 = *reinterpret_cast<const float4*>(&red[pk & 1][lane][4]);
+      const float s = ((((((p0.x + p0.y) + p0.z) + p0.w) + p1.x) + p1.y) + p1.z) + p1.w;
+      g.upart_out[(long)nslice * g.M + (long)blk_of(pk) * R + lane] = s;
+    }
+  };
+
+  // One iteration: wait for block k, MFMAs of block k into acc, interleaved step by step with the epilogue
+  // of block k - 1 (epi) and the partial sums of block k - 2 (sum); then the loads of block k + NBUF - 1
+  // into the slot block k - 1 used.
+  auto iter = [&](f32x4 (&acc)[2][2], const f32x4 (&prev)[2][2], int k, bool epi, bool sum) {
+    wait_block(min(NBUF - 2, nb - 1 - k), min(2, max(0, k - 1)));
+    __builtin_amdgcn_s_barrier();
+    const int pbuf = (k + NBUF - 1) % NBUF;
+    const bf16* xsb = reinterpret_cast<const bf16*>(smem + (k % NBUF) * XBYTES) + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 xa[2], xb[2];
+    xa[0] = *reinterpret_cast<const bf16x8*>(xsb);
+    xa[1] = *reinterpret_cast<const bf16x8*>(xsb + 512);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8(&xc)[2] = (s & 1) ? xb : xa;
+      bf16x8(&xn)[2] = (s & 1) ? xa : xb;
+      if (s + 1 < KS) {
+        xn[0] = *reinterpret_cast<const bf16x8*>(xsb + (2 * (s + 1)) * 512);
+        xn[1] = *reinterpret_cast<const bf16x8*>(xsb + (2 * (s + 1) + 1) * 512);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma16x16x32(wr[j][s], xc[i], acc[i][j]);
+      if (epi) epi_stage(prev, k - 1, pbuf, s);
+      if (s == 13 && sum) sum_partials(k - 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (k + NBUF - 1 < nb) issue(k + NBUF - 1);
+  };
+
+#pragma unroll
+  for (int k = 0; k < NBUF - 1; ++k)
+    if (k < nb) issue(k);
+
+  iter(accA, accB, 0, false, false);
+  int k = 1;
+  for (; k + 1 < nb; k += 2) {
+    iter(accB, accA, k, true, k >= 2);
+    iter(accA, accB, k + 1, true, true);
+  }
+  // tail: the last block's epilogue; partial sums of the last two blocks, each after a barrier
+  int last = k - 1;
+  if (k < nb) {
+    iter(accB, accA, k, true, k >= 2);
+    last = k;
+  }
+  wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  if (last >= 1) sum_partials(last - 1);
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    if (last == k) epi_stage(accB, last, last % NBUF, st);
+    else epi_stage(accA, last, last % NBUF, st);
+  }
+  wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  sum_partials(last);
+}
+
+}  // namespace
+
+int xs_relu2_parts(int N) { return (N > 0 && N % BN == 0) ? N / BN : 0; }
+
+bool xs_relu2_supported(const LowrankGemmArgs& g) {
+  return g.K == KD && g.N % BN == 0 && g.N > 0 && g.M % R == 0 && g.T % R == 0 && g.u_parts == 1 && g.u_ld == 1 &&
+         g.lda % 8 == 0 && g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.ra_ld % 4 == 0 &&
+         g.rb_next_ld % 4 == 0;
+}
+
+int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_relu2_supported(g) || !g.A || !g.W || !g.sign || !g.u || !g.ra[0] || !g.rb_next || !g.out_bf16 ||
+      !g.upart_out || g.pair_shift < 0 || g.pair_shift > 1 || g.lda < g.K || g.ldw < g.K || g.ldo < g.N)
+    return NOISE_EINVAL;
+  if (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16 | (uintptr_t)g.ra[0] | (uintptr_t)g.rb_next |
+       (uintptr_t)g.u) & 15)
+    return NOISE_EINVAL;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int nslices = g.N / BN, per_xcd = std::max(1, cus / 8);
+  const int streams = std::max(1, per_xcd / nslices);
+  hipLaunchKernelGGL(xs_relu2_kernel, dim3(8 * streams * nslices), dim3(512), 0, stream, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}

@@ -93,7 +93,7 @@ class Buffers:
         self.u_fc = torch.empty(M, device=device, dtype=f32)
         self.parts = _lib.value('noise_mlp_fc_parts', F)
         self.hidden = torch.empty(M, F, device=device, dtype=b16)
-        self.u_mlp = torch.empty(M, self.parts, device=device, dtype=f32)
+        self.u_mlp = torch.empty(self.parts, M, device=device, dtype=f32)  # part-major
         ws = _lib.size_query('noise_head_ce_workspace_size', members, T, vocab, int(head == 'fp32'))
         self.head_ws = torch.empty(ws, device=device, dtype=torch.uint8)
 
@@ -195,8 +195,8 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], _p(bp), ps, _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
-        _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, _p(sign), m, T,
-                  ps, _p(buf.x), s)
+        _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, H, 1, _p(sign),
+                  m, T, ps, _p(buf.x), s)
         tm.close(t0)
         af, bf_ = noise[pre + 'mlp.c_fc.weight']
         am, bm = noise[pre + 'mlp.c_proj.weight']
@@ -206,8 +206,9 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         t0 = tm.mark('mlp')
         _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
                   _p(buf.hidden), _p(buf.u_mlp), s)
-        _lib.call('noise_lowrank_resid', _p(buf.hidden), _p(W.mproj[i]), F, D, _p(am), _p(buf.u_mlp), buf.parts,
-                  _p(sign), m, T, ps, _p(buf.x), s)
+        # the fc partials are part-major with stride m * T (this chunk's rows)
+        _lib.call('noise_lowrank_resid', _p(buf.hidden), _p(W.mproj[i]), F, D, _p(am), _p(buf.u_mlp), buf.parts, 1,
+                  m * T, _p(sign), m, T, ps, _p(buf.x), s)
         tm.close(t0)
     ah, bh = noise['lm_head.weight']
     Vh = W.head_w.shape[0]

@@ -61,7 +61,7 @@ def test_version_and_size_queries_run_on_cpu():
         _lib.size_query('noise_lowrank_mlp_workspace_size', 0, 256, 512, 2048)
     assert _lib.size_query('noise_head_ce_workspace_size', 2, 256, 4096, 1) > _lib.size_query(
         'noise_head_ce_workspace_size', 2, 256, 4096, 0)
-    assert _lib.value('noise_mlp_fc_parts', 2048) == 32
+    assert _lib.value('noise_mlp_fc_parts', 2048) == 8
     assert _lib.value('noise_mlp_fc_parts', 100) == 0
 
 
