@@ -87,13 +87,13 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
 
   // global -> register staging of one key block: 4 K chunks and 2 V (key pair, dim chunk) items per
   // thread; K is fetched at the top of the previous block, V after its softmax
-  uint4 rk[4], rv[2][2];
+  u32x4 rk[4], rv[2][2];
   auto gload_k = [&](int j) {
     const long kr0 = rbase + (long)j * BKV;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      rk[s] = *reinterpret_cast<const uint4*>(qkv + (kr0 + k) * g.ldq + kcol + 8 * c);
+      rk[s] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + k) * g.ldq + kcol + 8 * c);
     }
   };
   auto gload_v = [&](int j) {
@@ -101,15 +101,15 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int item = tid + s * NTH, kp = item >> 3, c = item & 7;
-      rv[s][0] = *reinterpret_cast<const uint4*>(qkv + (kr0 + 2 * kp) * g.ldq + vcol + 8 * c);
-      rv[s][1] = *reinterpret_cast<const uint4*>(qkv + (kr0 + 2 * kp + 1) * g.ldq + vcol + 8 * c);
+      rv[s][0] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + 2 * kp) * g.ldq + vcol + 8 * c);
+      rv[s][1] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + 2 * kp + 1) * g.ldq + vcol + 8 * c);
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      *reinterpret_cast<uint4*>(&sk[buf][kswz(krow(k), c)]) = rk[s];
+      *reinterpret_cast<u32x4*>(&sk[buf][kswz(krow(k), c)]) = rk[s];
     }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -138,9 +138,78 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   gload_v(j0);
   sstore(0);
   __syncthreads();
+  // per-lane LDS offsets (elements) of the MFMA operand reads; the block index adds a constant
+  // K block kb, chunk grp / 4 + grp: row 16 kb + lane % 16 -> kswz = 1024 kb + (lane % 16) 64 + ((c ^ lane % 8) << 3)
+  const int kofs0 = kswz(lane & 15, grp), kofs1 = kswz(lane & 15, 4 + grp);
+  // V^T block db, contraction step c: row 16 db + lane % 16, chunk 4 c + grp
+  int vofs[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) vofs[c] = vswz(lane & 15, 4 * c + grp);
+  const f16x2 ones = {(f16)1.f, (f16)1.f};
+
+  // Scores of keys a query may not see (after it, or beyond the window) become -inf (branch-free).
+  auto apply_mask = [&](f32x4 (&s)[2][KB], int kstart) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = kstart + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
+          const bool out = key > q || q - key > g.window;
+          s[qb][kb][e] = out ? -INFINITY : s[qb][kb][e];
+        }
+    }
+  };
+  // Online softmax of one key block for query block qb of this wave.
+  auto softmax = [&](f32x4 (&s)[2][KB], f16x8 (&pf)[2][KC], int qb) {
+    float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < KB; kb += 2) {
+      m0 = fmaxf(m0, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
+      m1 = fmaxf(m1, fmaxf(fmaxf(s[qb][kb + 1][0], s[qb][kb + 1][1]), fmaxf(s[qb][kb + 1][2], s[qb][kb + 1][3])));
+    }
+    float mx = fmaxf(m0, m1);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const bool move = mx * c2 > mref[qb] * c2 + LAZY;
+    if (__any(move)) {
+      const float mnew = move ? mx : mref[qb];
+      const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
+      mref[qb] = mnew;
+      lsum[qb] *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+    }
+    const float mc = mref[qb] * c2;
+    float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int hlf = 0; hlf < 2; ++hlf) {
+        f16x2 pr[2];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e + 1], c2, -mc));
+          pr[e / 2] = f16x2{(f16)p0, (f16)p1};
+          pf[qb][c][4 * hlf + e] = pr[e / 2][0];
+          pf[qb][c][4 * hlf + e + 1] = pr[e / 2][1];
+        }
+        // row sum of the fp16 probabilities actually used in P V
+        ps0 = __builtin_amdgcn_fdot2(pr[0], ones, ps0, false);
+        ps1 = __builtin_amdgcn_fdot2(pr[1], ones, ps1, false);
+      }
+    lsum[qb] += ps0 + ps1;
+  };
+
   for (int j = j0; j <= j1; ++j) {
     const int buf = (j - j0) & 1;
-    if (j < j1) gload_k(j + 1);
+    // the next block's K and V (the last iteration fetches its own block again: no branch around the
+    // staging registers, which keeps them in VGPRs)
+    const int jn = min(j + 1, j1);
+    gload_k(jn);
     const int kstart = j * BKV;
     const bf16* kt = sk[buf];
     const f16* vt = sv[buf];
@@ -148,8 +217,8 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
     f32x4 s[2][KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&kt[kswz(16 * kb + (lane & 15), grp)]);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&kt[kswz(16 * kb + (lane & 15), 4 + grp)]);
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&kt[kofs0 + 1024 * kb]);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&kt[kofs1 + 1024 * kb]);
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -157,65 +226,27 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
         s[qb][kb] = mfma16x16x32(k1, qf[qb][1], a);
       }
     }
-    // mask (only blocks touching the causal edge or the window edge), lazy-max online softmax
+    // blocks away from the causal edge and the window edge need no mask
     const bool full = kstart + BKV - 1 <= q0 && q0 + BQ - 1 - kstart <= g.window;
+    if (!full) apply_mask(s, kstart);
     f16x8 pf[2][KC];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (!full) {
-            const int key = kstart + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
-            if (key > q || q - key > g.window) s[qb][kb][e] = -INFINITY;
-          }
-          mx = fmaxf(mx, s[qb][kb][e]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const bool move = mx * c2 > mref[qb] * c2 + LAZY;
-      if (__any(move)) {
-        const float mnew = move ? mx : mref[qb];
-        const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
-        mref[qb] = mnew;
-        lsum[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
-      }
-      const float mc = mref[qb] * c2;
-      float ps = 0.f;
-#pragma unroll
-      for (int c = 0; c < KC; ++c)
-#pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
-            ps += pv;
-            pf[qb][c][4 * hlf + e] = (f16)pv;
-          }
-      lsum[qb] += ps;
-    }
+    softmax(s, pf, 0);
+    softmax(s, pf, 1);
     // V of the next block is fetched once the scores are dead (register pressure)
-    if (j < j1) gload_v(j + 1);
+    gload_v(jn);
     // O^T += V^T P^T
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[vswz(16 * db + (lane & 15), 4 * c + grp)]);
+        const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[vofs[c] + 16 * BKV * db]);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma16x16x32_f16(vf, pf[qb][c], o[qb][db]);
       }
-    if (j < j1) {
-      // buf ^ 1 was last read in the previous iteration, which every wave finished before the barrier
-      // that closed it
-      sstore(buf ^ 1);
-      __syncthreads();
-    }
+    // buf ^ 1 was last read in the previous iteration, which every wave finished before the barrier
+    // that closed it
+    sstore(buf ^ 1);
+    __syncthreads();
   }
 
   // ---- epilogue: y = O / l, bf16; c_proj dot partial; optional moments
