@@ -240,7 +240,12 @@ def run_attention(args):
     torch.cuda.set_device(dev)
     P, window = 256, args.window
     g = torch.Generator(device=dev).manual_seed(0)
-    qkv = torch.randn(P * T, 3 * D, device=dev, generator=g).to(torch.bfloat16)
+    qkv = torch.randn(P * T, 3 * D, device=dev, generator=g)
+    if args.qk_norm:
+        # q and k rows RMS-normalised per head, as the model's QK-norm leaves them (utils/model.py:46-47)
+        qk = qkv[:, :2 * D].view(P * T, 16, 64)
+        qkv[:, :2 * D] = (qk * torch.rsqrt(qk.pow(2).mean(-1, keepdim=True) + 2 ** -23)).view(P * T, 2 * D)
+    qkv = qkv.to(torch.bfloat16)
     y = torch.empty(P * T, D, device=dev, dtype=torch.bfloat16)
     up = torch.empty(P * T, 8, device=dev)
     bp = torch.randn(P, D, device=dev, generator=g)
@@ -249,15 +254,16 @@ def run_attention(args):
     s = torch.cuda.current_stream().cuda_stream
 
     def step():
-        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, bp.data_ptr(), 0, y.data_ptr(), up.data_ptr(),
-                  mom.data_ptr(), ws.data_ptr(), ws.numel(), s)
+        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, int(args.qk_norm), bp.data_ptr(), 0, y.data_ptr(),
+                  up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), s)
     ms_step, ms_launch = _timed(step, args.steps, args.warmup)
     pairs = sum(min(q, window) + 1 for q in range(T))
     flop = 4 * 64 * 8 * P * pairs
     achieved = flop / (ms_launch * 1e-3) / 1e12
     return _common(args, P * T / (ms_step * 1e-3), ms_step,
                    {'workload': 'config2_attention_moments', 'members': P, 'heads': 8, 'tokens': T, 'head_dim': 64,
-                    'window': window, 'outputs': 'y bf16, c_proj dot partials, per-head mean of y and y^2',
+                    'window': window, 'q_k': 'RMS-normalised rows (QK-norm)' if args.qk_norm else 'N(0,1)',
+                    'outputs': 'y bf16, c_proj dot partials, per-head mean of y and y^2',
                     'parallelism': 'single GPU'},
                    {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None, 'kernel': 'attention_kernel + moments_reduce',
@@ -306,6 +312,7 @@ def main():
     ap.add_argument('--warmup', type=int, default=1)
     ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head'), default='step')
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
+    ap.add_argument('--qk-norm', action='store_true', help='config 2 with RMS-normalised q, k rows (the model case)')
     ap.add_argument('--pairs', type=int, default=1536)
     ap.add_argument('--chunk', type=int, default=1024, help='members per kernel pass')
     ap.add_argument('--no-cpu-baseline', action='store_true')

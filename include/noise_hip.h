@@ -111,10 +111,13 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
  * sees keys s - window .. s (utils/model.py:14-31). When b_proj is not null, writes the c_proj
  * input-side dot partials upart [members*T, 8]. When mom is not null, writes per-(member, head)
  * means over tokens of y and y^2, mom [members, 8, 2, 64] ("credit moments"; no reference
- * function), using mom_work (noise_attention_workspace_size bytes). T % 128 == 0. */
+ * function), using mom_work (noise_attention_workspace_size bytes). T % 128 == 0.
+ * qk_norm != 0 declares that q and k rows are RMS-normalised (norm(q), norm(k) at train/val/eggroll.py:90,
+ * as noise_qkv writes them): every score is then bounded by 8.03 and the softmax runs without a running
+ * maximum; qk_norm == 0 accepts any q, k. */
 int noise_attention_workspace_size(int members, int T, size_t* bytes);
-int noise_attention(const void* qkv, int members, int T, int window, const float* b_proj, int pair_shift,
-                    void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
+int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, const float* b_proj,
+                    int pair_shift, void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream);
 
 /* resid += lowrank(x, w) with the input-side dot of row r given as u_parts partial sums

@@ -9,6 +9,7 @@ struct AttnArgs {
   __bf16* y;          // [members * T, ldy], head h at columns h*64 .. h*64+63
   long ldy;
   int members, T, H, window;
+  int qk_norm;        // q and k rows are RMS-normalised (scores bounded by 8.03): no running maximum
   // c_proj input-side dot partials: upart[row * upart_ld + h] = sum_d y[row, h*64+d] bf16(b_proj[dir, h*64+d])
   const float* b_proj;
   long b_ld;

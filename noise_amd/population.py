@@ -150,6 +150,10 @@ class _NoTimer:
 TIMER = _NoTimer()
 
 
+# q and k reach attention RMS-normalised (noise_qkv applies the QK-norm), so its bounded-score softmax applies
+QK_NORM = True
+
+
 def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, windows):
     """Losses of members 0..m-1 of `sign` (m = len(sign)) into out[0:m]; noise rows are indexed by
     p >> pair_shift. Follows train/val/eggroll.py:72-103 op for op."""
@@ -192,7 +196,9 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         tm.close(t0)
         ap, bp = noise[pre + 'attn.c_proj.weight']
         t0 = tm.mark('attention')
-        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], _p(bp), ps, _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
+        # q and k come out of noise_qkv RMS-normalised
+        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], int(QK_NORM), _p(bp), ps, _p(buf.y), _p(buf.u_attn),
+                  0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
         _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, H, 1, _p(sign),

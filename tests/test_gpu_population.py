@@ -130,12 +130,19 @@ def test_block_entry_and_qkv_match_oracle():
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
 
 
-def test_attention_matches_oracle_and_moments():
+@pytest.mark.parametrize('qk_norm', [0, 1])
+def test_attention_matches_oracle_and_moments(qk_norm):
+    """qk_norm = 0: any q, k (running-maximum softmax); qk_norm = 1: q, k RMS-normalised per head as the
+    model's QK-norm leaves them (bounded scores, no running maximum), including rows scaled to the bound."""
     g = torch.Generator().manual_seed(2)
     m, T = 2, 256
     for window in (T, 100):
-        log_case(f'attention m={m} T={T} window={window}')
+        log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm}')
         q, k, v = (torch.randn(m, T, 8, 64, generator=g).bfloat16() for _ in range(3))
+        if qk_norm:
+            q, k = om.norm(q.float()).bfloat16(), om.norm(k.float()).bfloat16()
+            # extreme case: every key of the first head equal to its query direction (scores at the bound)
+            k[:, :, 0] = q[:, :, 0]
         qkv = torch.cat([q.reshape(m * T, 512), k.reshape(m * T, 512), v.reshape(m * T, 512)], 1).to(DEV)
         y = torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
         bp = torch.randn(m, 512, generator=g)
@@ -143,7 +150,7 @@ def test_attention_matches_oracle_and_moments():
         up = torch.empty(m * T, 8, device=DEV)
         mom = torch.empty(m, 8, 2, 64, device=DEV)
         ws = torch.empty(_lib.size_query('noise_attention_workspace_size', m, T), device=DEV, dtype=torch.uint8)
-        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, bpd.data_ptr(), 0, y.data_ptr(),
+        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, bpd.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
@@ -229,9 +236,34 @@ def _population_case(model, params, P, T, sigma, seed, head='fp32'):
 
 
 def _oracle_with_floor(params, noise, sign, idx, tgt):
-    """bf16-mode oracle losses, and how far they move when every GEMM accumulates in fp64 instead of
-    fp32 (the summation-order sensitivity of the bf16 path at these weights)."""
+    """bf16-mode oracle losses, and how far they move under three equally valid changes of rounding: every
+    GEMM accumulating in fp64 instead of fp32, attention computed in fp64, and attention probabilities
+    rounded to fp16. The largest move (per loss and per antithetic difference) is the floor: at trained-scale
+    weights the bf16 path is chaotic, and one alternative alone under-samples how far valid roundings diverge
+    (the CPU oracle's own results also shift with the host's summation order)."""
     ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    orig_attn = om.attention
+
+    def attention_p16(q, k, v, window, dtype=torch.float32):
+        # probabilities rounded to fp16 before P V (11-bit significand, the precision class of the
+        # reference's TF32 flex attention); normalised by the sum of the rounded probabilities
+        B, T, H, D = q.shape
+        qh, kh, vh = (t.transpose(1, 2).float() for t in (q, k, v))
+        scores = qh @ kh.transpose(-1, -2) / math.sqrt(D)
+        pos = torch.arange(T)
+        mask = (pos[:, None] >= pos[None, :]) & (pos[:, None] - pos[None, :] <= window)
+        scores = scores.masked_fill(~mask, float('-inf'))
+        p = torch.exp(scores - scores.amax(-1, keepdim=True)).half().float()
+        return ((p @ vh) / p.sum(-1, keepdim=True)).transpose(1, 2).to(q.dtype)
+
+    alts = []
+    for variant in (lambda q, k, v, window, dtype=torch.float32: orig_attn(q, k, v, window, torch.float64),
+                    attention_p16):
+        om.attention = variant
+        try:
+            alts.append(om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32'))
+        finally:
+            om.attention = orig_attn
     orig = om.lowrank
 
     def lowrank64(x, weight, a, b, s, mode='fp32'):
@@ -246,8 +278,8 @@ def _oracle_with_floor(params, noise, sign, idx, tgt):
         alt = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
     finally:
         om.lowrank = orig
-    floor = float((alt - ref).abs().max())
-    pair_floor = float(((alt[1::2] - alt[0::2]) - (ref[1::2] - ref[0::2])).abs().max())
+    floor = max(float((a - ref).abs().max()) for a in (alt, *alts))
+    pair_floor = max(float(((a[1::2] - a[0::2]) - (ref[1::2] - ref[0::2])).abs().max()) for a in (alt, *alts))
     return ref, floor, pair_floor
 
 
