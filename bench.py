@@ -245,7 +245,10 @@ def run_attention(args):
         # q and k rows RMS-normalised per head, as the model's QK-norm leaves them (utils/model.py:46-47)
         qk = qkv[:, :2 * D].view(P * T, 16, 64)
         qkv[:, :2 * D] = (qk * torch.rsqrt(qk.pow(2).mean(-1, keepdim=True) + 2 ** -23)).view(P * T, 2 * D)
-    qkv = qkv.to(torch.bfloat16)
+    qkv16 = qkv.to(torch.bfloat16)
+    # v as fp16 holding the bf16 value, the format noise_qkv writes
+    qkv16[:, 2 * D:] = qkv16[:, 2 * D:].half().view(torch.bfloat16)
+    qkv = qkv16
     y = torch.empty(P * T, D, device=dev, dtype=torch.bfloat16)
     up = torch.empty(P * T, 8, device=dev)
     bp = torch.randn(P, D, device=dev, generator=g)

@@ -98,8 +98,9 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
 
 /* q | k | v = lowrank(h, [W_q; W_k; W_v]) with per-segment a vectors and the u_qkv dots, then rotary +
  * QK RMSNorm on q and k (utils/model.py:55-58, :46-47; train/val/eggroll.py:90) and, when gate is not
- * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89). Output bf16
- * [members*T, 1536] (q | k | v, head h at columns h*64 of each segment).
+ * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89). Output
+ * [members*T, 1536] 16-bit (q | k | v, head h at columns h*64 of each segment): q and k bf16, v the
+ * bf16-rounded value stored as fp16 (exact), the operand format of noise_attention.
  *   w_qkv    bf16 [1536, 512] = c_q ; c_k ; c_v
  *   rot_cos / rot_sin  bf16 [>= T, 32] (utils/model.py:177-183) */
 int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
@@ -107,7 +108,8 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
               const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
               const float* ve_b, const int64_t* idx, void* qkv, noise_stream_t stream);
 
-/* Windowed causal attention on the q | k | v rows (8 heads x 64): y bf16 [members*T, 512]; a query at s
+/* Windowed causal attention on the q | k | v rows as noise_qkv writes them (q, k bf16; v fp16; 8 heads x 64):
+ * y bf16 [members*T, 512]; a query at s
  * sees keys s - window .. s (utils/model.py:14-31). When b_proj is not null, writes the c_proj
  * input-side dot partials upart [members*T, 8]. When mom is not null, writes per-(member, head)
  * means over tokens of y and y^2, mom [members, 8, 2, 64] ("credit moments"; no reference

@@ -3,24 +3,28 @@
 //
 // Reference: `attention` / `window_mask` (utils/model.py:14-31) called from population_loss
 // (train/val/eggroll.py:91): softmax(q k^T / sqrt(64)) v, a query at s seeing keys k with
-// s - window <= k <= s. q, k, v arrive bf16 (rotary and QK-norm already applied by the QKV GEMM).
+// s - window <= k <= s. q and k arrive bf16 (rotary and QK-norm already applied by the QKV GEMM), v arrives
+// as fp16 holding the bf16-rounded value exactly.
 //
 // One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; two workgroups per CU.
-// K/V blocks of 128 keys go through a double-buffered LDS ring with one barrier per block: K rows as
-// they are (bf16), V transposed to V^T and converted to fp16 while it is staged, so the key dimension
-// is the MFMA contraction dimension of both products. Per wave and key block:
-//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 32 scores of query l % 16;
-//   online softmax in fp32 with a lazy maximum: the running max moves only when a block's maximum
-//   exceeds it by more than 2^8 in probability, so P <= 256 and the rescale of O is skipped unless
-//   some lane of the wave moved; exp2 on the FMA-folded argument (s - m) * log2(e) / 8;
-//   O^T += V^T P^T (fp16 MFMA, A = V^T rows, B = P): the scores' register layout IS the B operand
-//   once the K rows of each 16-row MFMA block are interleaved (block kb, row r <-> key
-//   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so P never leaves registers. P is rounded to
-//   fp16 (11-bit significand, the precision class of the reference's TF32 attention); V is bf16 and
-//   converts to fp16 exactly.
-// V^T rows are interleaved the same way (block db, row r <-> dim 16 (r / 4) + 4 db + r % 4), so each
-// lane ends with 16 contiguous output dims of one query: 16-byte stores, and the c_proj dot
-// y . b_proj over the head's 64 dims is a 4-lane reduction.
+// K/V blocks of 128 keys go through a double-buffered LDS ring filled by direct global -> LDS loads
+// (global_load_lds_dwordx4, issued from inline assembly so the compiler adds no LDS-wide waits): while block j
+// is computed, block j + 1 lands; one s_waitcnt vmcnt(0) + s_barrier per block (the loads are the only
+// vector memory operations in the loop). Nothing passes through registers on the way in.
+//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 32 scores of query l % 16. The K rows
+//   of each 16-row MFMA block are interleaved at load time (block kb, row r <-> key
+//   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so the scores' register layout IS the B operand of P V;
+//   P never leaves registers.
+//   Softmax in fp32: exp2 on the FMA-folded argument; P rounded to fp16 (11-bit significand, the precision
+//   class of the reference's TF32 attention). With RMS-normalised q, k (QKN) the scores are bounded and no
+//   running maximum is kept; otherwise a lazy running maximum (moves only beyond 2^8 of headroom).
+//   O^T += V^T P^T (fp16 MFMA): V stays row-major [key][dim] in LDS and its A fragments (8 consecutive keys
+//   of one dim per lane) come from ds_read_b64_tr_b16, which transposes 16-bit elements across each group
+//   of 16 lanes: with source lane 4 t + a of group g pointing at key 32 c + 8 g + 4 h + t, dims
+//   16 a + 4 db .. + 3, output lane 16 g + 4 a + b receives keys 32 c + 8 g + 4 h + (0..3) of dim
+//   16 a + 4 db + b. The A-row <-> dim order (row 4 a + b of block db is dim 16 a + 4 db + b) leaves each
+//   lane with 16 contiguous output dims of one query: 16-byte stores, and the c_proj dot y . b_proj over
+//   the head's 64 dims is a 4-lane reduction.
 #include "attention.h"
 #include "common.h"
 
@@ -33,27 +37,36 @@ constexpr float LAZY = 8.f;        // max moves only beyond 2^8 of headroom
 
 typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
 __device__ __forceinline__ f32x4 mfma16x16x32_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// K tile [BKV keys][64 dims] bf16, rows of 128 B, 16-byte chunks XOR-swizzled by row.
-__device__ __forceinline__ int kswz(int r, int c) { return r * HD + ((c ^ (r & 7)) << 3); }
-// V^T tile [64 dims][BKV keys] fp16, rows of 256 B (16 chunks), chunk XOR-swizzled by row.
-__device__ __forceinline__ int vswz(int r, int c) { return r * BKV + ((c ^ (r & 7)) << 3); }
+// global_load_lds_dwordx4: each lane's 16 bytes land at lds + 16 * lane. M0 is saved and restored.
+__device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(src), "s"(off)
+               : "memory");
+}
 
-// LDS row of key k (0..BKV-1) in the interleaved K tile, and of dim d in the interleaved V^T tile.
-__device__ __forceinline__ int krow(int k) {
-  const int grp = k >> 5, w = k & 31;
-  const int kb = 2 * grp + ((w & 7) >> 2), r = 4 * (w >> 3) + (w & 3);
-  return 16 * kb + r;
+// K tile [BKV keys][64 dims] bf16, 128-byte rows, 16-byte chunks XOR-swizzled by row.
+__device__ __forceinline__ int kswz(int r, int c) { return r * HD + ((c ^ (r & 7)) << 3); }
+// key held by LDS row R of the interleaved K tile (inverse of the row interleave above)
+__device__ __forceinline__ int key_of_krow(int R) {
+  const int kb = R >> 4, r = R & 15;
+  return 32 * (kb >> 1) + 8 * (r >> 2) + 4 * (kb & 1) + (r & 3);
 }
-__device__ __forceinline__ int drow(int d) {
-  const int db = (d & 15) >> 2, r = 4 * (d >> 4) + (d & 3);
-  return 16 * db + r;
-}
+// V tile [BKV keys][64 dims] fp16, 128-byte rows in key order; chunk c of row R sits at chunk c ^ vsw(R),
+// which spreads the transposing reads of 16 rows over the banks.
+__device__ __forceinline__ int vsw(int R) { return (R >> 1) & 7; }
 
 __device__ __forceinline__ unsigned pack2(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
@@ -66,8 +79,8 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
 // cross-lane shuffles and the rescaling from the loop. Softmax is shift-invariant, so the result is the same.
 template <bool QKN>
 __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][BKV * HD];
-  __shared__ __attribute__((aligned(16))) f16 sv[2][HD * BKV];
+  __shared__ __attribute__((aligned(1024))) bf16 sk[2][BKV * HD];
+  __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
   __shared__ float smom[NWAVE][2][HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
@@ -90,44 +103,21 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   const int k_lo = max(0, q0 - g.window), k_hi = min(g.T - 1, q0 + BQ - 1);
   const int j0 = k_lo / BKV, j1 = k_hi / BKV;
 
-  // global -> register staging of one key block: 4 K chunks and 2 V (key pair, dim chunk) items per
-  // thread; K is fetched at the top of the previous block, V after its softmax
-  u32x4 rk[4], rv[2][2];
-  auto gload_k = [&](int j) {
+  // ---- loads of key block j into ring slot buf: 16 K and 16 V instructions of 1 KiB, 4 + 4 per wave.
+  // Instruction d fills LDS rows 8 d .. 8 d + 7; lane L -> row R = 8 d + L / 8, physical chunk L % 8.
+  const int lrow = lane >> 3, lchunk = lane & 7;
+  auto issue = [&](int j, int buf) {
     const long kr0 = rbase + (long)j * BKV;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      rk[s] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + k) * g.ldq + kcol + 8 * c);
-    }
-  };
-  auto gload_v = [&](int j) {
-    const long kr0 = rbase + (long)j * BKV;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int item = tid + s * NTH, kp = item >> 3, c = item & 7;
-      rv[s][0] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + 2 * kp) * g.ldq + vcol + 8 * c);
-      rv[s][1] = *reinterpret_cast<const u32x4*>(qkv + (kr0 + 2 * kp + 1) * g.ldq + vcol + 8 * c);
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int item = tid + s * NTH, k = item >> 3, c = item & 7;
-      *reinterpret_cast<u32x4*>(&sk[buf][kswz(krow(k), c)]) = rk[s];
+    for (int q = 0; q < 4; ++q) {
+      const int d = 4 * wave + q, R = 8 * d + lrow;
+      dma_x4(qkv + (kr0 + key_of_krow(R)) * g.ldq + kcol + 8 * (lchunk ^ (R & 7)),
+             reinterpret_cast<const char*>(sk[buf]) + d * 1024);
     }
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int item = tid + s * NTH, kp = item >> 3, c = item & 7;
-      const bf16* v0 = reinterpret_cast<const bf16*>(&rv[s][0]);
-      const bf16* v1 = reinterpret_cast<const bf16*>(&rv[s][1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int R = drow(8 * c + e);
-        // keys 2 kp, 2 kp + 1 of V^T row R: chunk kp / 4, element 2 (kp % 4)
-        f16x2 pr = {(f16)(float)v0[e], (f16)(float)v1[e]};
-        *reinterpret_cast<f16x2*>(&sv[buf][vswz(R, kp >> 2) + 2 * (kp & 3)]) = pr;
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int d = 4 * wave + q, R = 8 * d + lrow;
+      dma_x4(qkv + (kr0 + R) * g.ldq + vcol + 8 * (lchunk ^ vsw(R)), reinterpret_cast<const char*>(sv[buf]) + d * 1024);
     }
   };
 
@@ -139,17 +129,22 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gload_k(j0);
-  gload_v(j0);
-  sstore(0);
-  __syncthreads();
-  // per-lane LDS offsets (elements) of the MFMA operand reads; the block index adds a constant
-  // K block kb, chunk grp / 4 + grp: row 16 kb + lane % 16 -> kswz = 1024 kb + (lane % 16) 64 + ((c ^ lane % 8) << 3)
+  // per-lane LDS offsets of the MFMA operand reads (the block / step index adds a constant)
+  // K block kb: row 16 kb + lane % 16, chunk grp and 4 + grp
   const int kofs0 = kswz(lane & 15, grp), kofs1 = kswz(lane & 15, 4 + grp);
-  // V^T block db, contraction step c: row 16 db + lane % 16, chunk 4 c + grp
-  int vofs[KC];
+  // V fragment (step c, dim block db, half hh): source row 32 c + 8 grp + 4 hh + t, dims 16 a + 4 db ..
+  // (t = (lane % 16) / 4, a = lane % 4); byte offset within the tile, without the 4096 c of the step
+  int vofs[2][4];
+  {
+    const int t = (lane & 15) >> 2, a = lane & 3;
 #pragma unroll
-  for (int c = 0; c < KC; ++c) vofs[c] = vswz(lane & 15, 4 * c + grp);
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int R = 8 * grp + 4 * hh + t;
+        vofs[hh][db] = R * 128 + 16 * ((2 * a + (db >> 1)) ^ vsw(R)) + 8 * (db & 1);
+      }
+  }
   const f16x2 ones = {(f16)1.f, (f16)1.f};
 
   // Scores of keys a query may not see (after it, or beyond the window) become -inf (branch-free).
@@ -171,25 +166,25 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   auto softmax = [&](f32x4 (&s)[2][KB], f16x8 (&pf)[2][KC], int qb) {
     float mc = 0.f;
     if constexpr (!QKN) {
-    float m0 = -INFINITY, m1 = -INFINITY;
+      float m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < KB; kb += 2) {
-      m0 = fmaxf(m0, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
-      m1 = fmaxf(m1, fmaxf(fmaxf(s[qb][kb + 1][0], s[qb][kb + 1][1]), fmaxf(s[qb][kb + 1][2], s[qb][kb + 1][3])));
-    }
-    float mx = fmaxf(m0, m1);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const bool move = mx * c2 > mref[qb] * c2 + LAZY;
-    if (__any(move)) {
-      const float mnew = move ? mx : mref[qb];
-      const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
-      mref[qb] = mnew;
-      lsum[qb] *= alpha;
+      for (int kb = 0; kb < KB; kb += 2) {
+        m0 = fmaxf(m0, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
+        m1 = fmaxf(m1, fmaxf(fmaxf(s[qb][kb + 1][0], s[qb][kb + 1][1]), fmaxf(s[qb][kb + 1][2], s[qb][kb + 1][3])));
+      }
+      float mx = fmaxf(m0, m1);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const bool move = mx * c2 > mref[qb] * c2 + LAZY;
+      if (__any(move)) {
+        const float mnew = move ? mx : mref[qb];
+        const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
+        mref[qb] = mnew;
+        lsum[qb] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
-    }
-    mc = mref[qb] * c2;
+        for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+      }
+      mc = mref[qb] * c2;
     }
     // row sum of the fp16 probabilities actually used in P V, in four independent chains
     float ps[4] = {0.f, 0.f, 0.f, 0.f};
@@ -210,15 +205,16 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
     lsum[qb] += (ps[0] + ps[1]) + (ps[2] + ps[3]);
   };
 
+  issue(j0, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __syncthreads();
   for (int j = j0; j <= j1; ++j) {
     const int buf = (j - j0) & 1;
-    // the next block's K and V (the last iteration fetches its own block again: no branch around the
-    // staging registers, which keeps them in VGPRs)
-    const int jn = min(j + 1, j1);
-    gload_k(jn);
+    // block j + 1 into the slot block j - 1 used (every wave finished it before the last barrier)
+    if (j < j1) issue(j + 1, buf ^ 1);
     const int kstart = j * BKV;
     const bf16* kt = sk[buf];
-    const f16* vt = sv[buf];
+    const char* vt = reinterpret_cast<const char*>(sv[buf]);
     // S^T = K Q^T
     f32x4 s[2][KB];
 #pragma unroll
@@ -238,20 +234,21 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
     f16x8 pf[2][KC];
     softmax(s, pf, 0);
     softmax(s, pf, 1);
-    // V of the next block is fetched once the scores are dead (register pressure)
-    gload_v(jn);
     // O^T += V^T P^T
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const f16x8 vf = *reinterpret_cast<const f16x8*>(&vt[vofs[c] + 16 * BKV * db]);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + 4096 * c + vofs[0][db]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + 4096 * c + vofs[1][db]));
+        const f16x4 lo16 = __builtin_bit_cast(f16x4, lo), hi16 = __builtin_bit_cast(f16x4, hi);
+        const f16x8 vf = {lo16[0], lo16[1], lo16[2], lo16[3], hi16[0], hi16[1], hi16[2], hi16[3]};
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma16x16x32_f16(vf, pf[qb][c], o[qb][db]);
       }
-    // buf ^ 1 was last read in the previous iteration, which every wave finished before the barrier
-    // that closed it
-    sstore(buf ^ 1);
+    // block j + 1 has landed for this wave (the only vector memory operations in flight are its loads);
+    // the barrier makes every wave's part visible and retires slot buf
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 

@@ -101,6 +101,12 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
   return *reinterpret_cast<unsigned*>(&p);
 }
+// fp16 pair of the bf16-rounded values (exact: |v| < 65504 and bf16's 8-bit significand fits fp16's 11 bits;
+// magnitudes below 2^-14 become fp16 subnormals)
+__device__ __forceinline__ unsigned pack_f16_of_bf16(float a, float b) {
+  _Float16 __attribute__((ext_vector_type(2))) p = {(_Float16)bf16r(a), (_Float16)bf16r(b)};
+  return *reinterpret_cast<unsigned*>(&p);
+}
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC, int EPI>
 __global__ void __launch_bounds__(WGM * WGN * 64, WGM * WGN * OCC / 4)
@@ -372,10 +378,19 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         }
         if (live) {
           uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+          if (seg < 2) {
 #pragma unroll
-          for (int e = 0; e < CW; e += 8)
-            o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
-                                  pack_bf16(v[e + 6], v[e + 7]));
+            for (int e = 0; e < CW; e += 8)
+              o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
+                                    pack_bf16(v[e + 4], v[e + 5]), pack_bf16(v[e + 6], v[e + 7]));
+          } else {
+            // v: the bf16-rounded value (the autocast rounding point) stored as fp16, which holds it exactly, so
+            // attention can feed it to fp16 MFMAs straight from memory
+#pragma unroll
+            for (int e = 0; e < CW; e += 8)
+              o[e / 8] = make_uint4(pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
+                                    pack_f16_of_bf16(v[e + 4], v[e + 5]), pack_f16_of_bf16(v[e + 6], v[e + 7]));
+          }
         }
       } else {  // EPI_CE
         // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,

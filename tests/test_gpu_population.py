@@ -125,6 +125,8 @@ def test_block_entry_and_qkv_match_oracle():
     qr = om.norm(om.apply_rotary(q.view(m, T, 8, 64), c, sn))
     kr = om.norm(om.apply_rotary(kk_.view(m, T, 8, 64), c, sn))
     got = qkv.cpu().float().view(m, T, 3, 8, 64)
+    # the v segment is written as fp16 (the bf16-rounded value, exactly)
+    got[:, :, 2] = qkv[:, 1024:].cpu().view(torch.float16).float().view(m, T, 8, 64)
     for k, ref in enumerate((qr, kr, vv)):
         assert rel_err(got[:, :, k], om.bf(ref)) < 5e-3, k
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
@@ -143,7 +145,9 @@ def test_attention_matches_oracle_and_moments(qk_norm):
             q, k = om.norm(q.float()).bfloat16(), om.norm(k.float()).bfloat16()
             # extreme case: every key of the first head equal to its query direction (scores at the bound)
             k[:, :, 0] = q[:, :, 0]
-        qkv = torch.cat([q.reshape(m * T, 512), k.reshape(m * T, 512), v.reshape(m * T, 512)], 1).to(DEV)
+        # v travels as fp16 holding the bf16 value (the format noise_qkv writes)
+        v16 = v.half().view(torch.bfloat16)
+        qkv = torch.cat([q.reshape(m * T, 512), k.reshape(m * T, 512), v16.reshape(m * T, 512)], 1).to(DEV)
         y = torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
         bp = torch.randn(m, 512, generator=g)
         bpd = bp.to(DEV)
