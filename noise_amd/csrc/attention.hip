@@ -122,8 +122,10 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   };
 
   const float c2 = 0.125f * 1.4426950408889634f;  // scores -> log2 units: 1/sqrt(64) * log2(e)
-  float mref[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};  // running max (score units) and sum per lane
-  f32x4 o[2][4];
+  float mref[2] = {-1e30f, -1e30f};  // running max (score units)
+  // O^T accumulators, and the row sums of the fp16 probabilities actually used in P V, accumulated on the
+  // MFMA pipe (an all-ones A operand: every element of osum[qb] in lane l is the sum for query l % 16)
+  f32x4 o[2][4], osum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -145,21 +147,30 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
         vofs[hh][db] = R * 128 + 16 * ((2 * a + (db >> 1)) ^ vsw(R)) + 8 * (db & 1);
       }
   }
-  const f16x2 ones = {(f16)1.f, (f16)1.f};
+  const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
 
-  // Scores of keys a query may not see (after it, or beyond the window) become -inf (branch-free).
-  auto apply_mask = [&](f32x4 (&s)[2][KB], int kstart) {
+  // Scores of keys a query may not see become -inf (branch-free): keys after it when the block touches the
+  // causal edge, keys more than `window` before it when the block touches the window edge. Key
+  // kstart + 8 grp + ko(kb, e) of a lane, ko = 32 (kb / 2) + 4 (kb % 2) + e a constant, is compared with
+  // dq = q - kstart - 8 grp.
+  auto apply_mask = [&](f32x4 (&s)[2][KB], int kstart, bool causal_edge, bool window_edge) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
+      const int dq = q0 + 32 * wave + 16 * qb + (lane & 15) - kstart - 8 * grp, dw = dq - g.window;
+      if (causal_edge) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = kstart + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
-          const bool out = key > q || q - key > g.window;
-          s[qb][kb][e] = out ? -INFINITY : s[qb][kb][e];
-        }
+          for (int e = 0; e < 4; ++e)
+            s[qb][kb][e] = 32 * (kb >> 1) + 4 * (kb & 1) + e > dq ? -INFINITY : s[qb][kb][e];
+      }
+      if (window_edge) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s[qb][kb][e] = 32 * (kb >> 1) + 4 * (kb & 1) + e < dw ? -INFINITY : s[qb][kb][e];
+      }
     }
   };
   // Online softmax of one key block for query block qb of this wave.
@@ -180,29 +191,19 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
         const float mnew = move ? mx : mref[qb];
         const float alpha = __builtin_amdgcn_exp2f((mref[qb] - mnew) * c2);
         mref[qb] = mnew;
-        lsum[qb] *= alpha;
+        osum[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
       }
       mc = mref[qb] * c2;
     }
-    // row sum of the fp16 probabilities actually used in P V, in four independent chains
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int hlf = 0; hlf < 2; ++hlf) {
+      for (int hlf = 0; hlf < 2; ++hlf)
 #pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e + 1], c2, -mc));
-          const f16x2 pr = {(f16)p0, (f16)p1};
-          pf[qb][c][4 * hlf + e] = pr[0];
-          pf[qb][c][4 * hlf + e + 1] = pr[1];
-          ps[hlf * 2 + e / 2] = __builtin_amdgcn_fdot2(pr, ones, ps[hlf * 2 + e / 2], false);
-        }
-      }
-    lsum[qb] += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        for (int e = 0; e < 4; ++e)
+          pf[qb][c][4 * hlf + e] = (f16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
   };
 
   issue(j0, 0);
@@ -229,8 +230,8 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
       }
     }
     // blocks away from the causal edge and the window edge need no mask
-    const bool full = kstart + BKV - 1 <= q0 && q0 + BQ - 1 - kstart <= g.window;
-    if (!full) apply_mask(s, kstart);
+    const bool causal_edge = kstart + BKV - 1 > q0, window_edge = q0 + BQ - 1 - kstart > g.window;
+    if (causal_edge || window_edge) apply_mask(s, kstart, causal_edge, window_edge);
     f16x8 pf[2][KC];
     softmax(s, pf, 0);
     softmax(s, pf, 1);
@@ -246,6 +247,10 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma16x16x32_f16(vf, pf[qb][c], o[qb][db]);
       }
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) osum[qb] = mfma16x16x32_f16(ones, pf[qb][c], osum[qb]);
     // block j + 1 has landed for this wave (the only vector memory operations in flight are its loads);
     // the barrier makes every wave's part visible and retires slot buf
     __builtin_amdgcn_s_waitcnt(0);
@@ -259,10 +264,7 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   for (int e = 0; e < 16; ++e) mom1[e] = mom2[e] = 0.f;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    float l = lsum[qb];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const float inv = 1.f / l;
+    const float inv = 1.f / osum[qb][0];
     const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
     const long row = rbase + q;
     float yv[16];
