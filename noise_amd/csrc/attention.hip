@@ -6,12 +6,13 @@
 // s - window <= k <= s. q and k arrive bf16 (rotary and QK-norm already applied by the QKV GEMM), v arrives
 // as fp16 holding the bf16-rounded value exactly.
 //
-// One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; two workgroups per CU.
-// K/V blocks of 128 keys go through a double-buffered LDS ring filled by direct global -> LDS loads
+// One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; four workgroups per CU (122
+// VGPRs, 34 KiB of LDS each: 4 waves per SIMD hide the LDS and transcendental latencies).
+// K/V blocks of 64 keys go through a double-buffered LDS ring filled by direct global -> LDS loads
 // (global_load_lds_dwordx4, issued from inline assembly so the compiler adds no LDS-wide waits): while block j
 // is computed, block j + 1 lands; one s_waitcnt vmcnt(0) + s_barrier per block (the loads are the only
 // vector memory operations in the loop). Nothing passes through registers on the way in.
-//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 32 scores of query l % 16. The K rows
+//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 16 scores of query l % 16. The K rows
 //   of each 16-row MFMA block are interleaved at load time (block kb, row r <-> key
 //   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so the scores' register layout IS the B operand of P V;
 //   P never leaves registers.
@@ -30,7 +31,8 @@
 
 namespace {
 
-constexpr int HD = 64, BQ = 128, BKV = 128, NWAVE = 4, NTH = NWAVE * 64;
+constexpr int HD = 64, BQ = 128, BKV = 64, NWAVE = 4, NTH = NWAVE * 64;
+constexpr int DH = BKV * HD * 2 / 1024 / NWAVE;  // K (and V) load instructions per wave and block
 constexpr int KB = BKV / 16;       // 16-key MFMA blocks per key block
 constexpr int KC = BKV / 32;       // 32-key contraction steps of P V
 constexpr float LAZY = 8.f;        // max moves only beyond 2^8 of headroom
@@ -78,7 +80,7 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
 // normal fp16 numbers and their sums stay far from fp32 overflow), which removes the max reduction, its
 // cross-lane shuffles and the rescaling from the loop. Softmax is shift-invariant, so the result is the same.
 template <bool QKN>
-__global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
+__global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   __shared__ __attribute__((aligned(1024))) bf16 sk[2][BKV * HD];
   __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
   __shared__ float smom[NWAVE][2][HD];
@@ -103,20 +105,20 @@ __global__ void __launch_bounds__(NTH, 2) attention_kernel(AttnArgs g) {
   const int k_lo = max(0, q0 - g.window), k_hi = min(g.T - 1, q0 + BQ - 1);
   const int j0 = k_lo / BKV, j1 = k_hi / BKV;
 
-  // ---- loads of key block j into ring slot buf: 16 K and 16 V instructions of 1 KiB, 4 + 4 per wave.
+  // ---- loads of key block j into ring slot buf: 8 K and 8 V instructions of 1 KiB, 2 + 2 per wave.
   // Instruction d fills LDS rows 8 d .. 8 d + 7; lane L -> row R = 8 d + L / 8, physical chunk L % 8.
   const int lrow = lane >> 3, lchunk = lane & 7;
   auto issue = [&](int j, int buf) {
     const long kr0 = rbase + (long)j * BKV;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int d = 4 * wave + q, R = 8 * d + lrow;
+    for (int q = 0; q < DH; ++q) {
+      const int d = DH * wave + q, R = 8 * d + lrow;
       dma_x4(qkv + (kr0 + key_of_krow(R)) * g.ldq + kcol + 8 * (lchunk ^ (R & 7)),
              reinterpret_cast<const char*>(sk[buf]) + d * 1024);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int d = 4 * wave + q, R = 8 * d + lrow;
+    for (int q = 0; q < DH; ++q) {
+      const int d = DH * wave + q, R = 8 * d + lrow;
       dma_x4(qkv + (kr0 + R) * g.ldq + vcol + 8 * (lchunk ^ vsw(R)), reinterpret_cast<const char*>(sv[buf]) + d * 1024);
     }
   };
