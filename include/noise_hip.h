@@ -35,6 +35,20 @@ extern "C" {
 
 typedef void* noise_stream_t; /* hipStream_t */
 
+/* A c_proj output not yet added to the residual stream (a deferred residual): row r of member p receives
+ *   y[r, c] + sign[p] * bf16(sum_{q < u_parts} u[r * u_row_stride + q * u_part_stride]) * a[dir * 512 + c]
+ * with y = bf16(x W^T) from noise_dense_bf16: `x = x + linear(name, x_in)` of train/val/eggroll.py:92-93 with
+ * the rank-1 term of `lowrank` (:56-58) applied where the residual stream is next read. y, a 16-byte
+ * aligned. */
+typedef struct noise_pending {
+  const void* y;            /* bf16 [members*T, 512] */
+  const float* u;           /* input-side dot partials of the c_proj input */
+  int u_parts;
+  long u_row_stride;
+  long u_part_stride;
+  const float* a;           /* [dirs, 512] output-side vectors of the c_proj weight */
+} noise_pending_t;
+
 /* Library version (major * 10000 + minor * 100 + patch). */
 int noise_version(void);
 
@@ -89,12 +103,14 @@ int noise_embed_norm(const float* w, long vocab, const float* a, const float* b,
  * u_qkv[row, 0..2] = bf16(h . bf16(b_{q,k,v}[dir])) (row stride 4); when gate_w is not null the value
  * gate gate[row, 0..7] = 2 sigmoid(lowrank(h[:32], gate_w, gate_a, gate_b)).
  * Replaces train/val/eggroll.py:76-84, :88. eps_r / eps_0 point at this block's column of the
- * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. */
+ * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. The npend (<= 2) deferred
+ * residuals in pend (the previous block's attention and MLP c_proj outputs) are added to x_in, in order,
+ * before the mix. */
 int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h, float* u_qkv, const float* b_q,
                       const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
                       const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
                       const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
-                      noise_stream_t stream);
+                      const noise_pending_t* pend, int npend, noise_stream_t stream);
 
 /* q | k | v = lowrank(h, [W_q; W_k; W_v]) with per-segment a vectors and the u_qkv dots, then rotary +
  * QK RMSNorm on q and k (utils/model.py:55-58, :46-47; train/val/eggroll.py:90) and, when gate is not
@@ -131,9 +147,16 @@ int noise_lowrank_resid(const void* x, const void* w, int in, int out, const flo
                         long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
                         float* resid, noise_stream_t stream);
 
-/* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). */
+/* y = bf16(x W^T) [members*T, out] for x bf16 [members*T, in], w bf16 [out, in]: the dense product of a
+ * c_proj `lowrank` whose rank-1 term and residual add are deferred to the row kernel that next reads the
+ * stream (noise_pending_t). in % 64 == 0, out % 128 == 0. */
+int noise_dense_bf16(const void* x, int in, int out, const void* w, int members, int T, void* y,
+                     noise_stream_t stream);
+
+/* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). The npend (<= 2)
+ * deferred residuals in pend are added to x, in order, before the norm; x itself is not written. */
 int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
-                   int pair_shift, noise_stream_t stream);
+                   int pair_shift, const noise_pending_t* pend, int npend, noise_stream_t stream);
 
 /* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] and its dot partials with bf16(b_proj),
  * part-major: upart [noise_mlp_fc_parts(f), members*T] (one partial per 256 columns), for the
@@ -151,11 +174,13 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
  *   fp32_head != 0: w_head is the [vocab, 1536] split operand from noise_cast_bf16(split_cols = 512)
  *                   and the head is fp32-accurate (~2^-16 relative); 0: w_head bf16 [vocab, 512]
  *                   with the reference's autocast rounding points.
- * vocab % 256 == 0. Workspace: noise_head_ce_workspace_size(). */
+ * vocab % 256 == 0. Workspace: noise_head_ce_workspace_size(). The npend (<= 2) deferred residuals in
+ * pend are added to an fp32 x, in order, before the norm (the last block's c_proj outputs). */
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes);
 int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
                   const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
-                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, noise_stream_t stream);
+                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, const noise_pending_t* pend,
+                  int npend, noise_stream_t stream);
 
 /* ---------------------------------------------------------------- EGGROLL update */
 

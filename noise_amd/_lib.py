@@ -28,20 +28,38 @@ SIGNATURES = {
     'noise_lowrank_mlp': [P, L, L, P, P, I, I, P, P, P, P, P, I, I, I, P, P, I, P, S, P],
     'noise_cast_bf16': [P, P, L, I, P],
     'noise_embed_norm': [P, L, P, P, P, P, I, I, I, P, P],
-    'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P],
+    'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P, I, P],
     'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, P, P],
     'noise_attention_workspace_size': [I, I, SP],
     'noise_attention': [P, I, I, I, I, P, I, P, P, P, P, S, P],
     'noise_lowrank_resid': [P, P, I, I, P, P, I, L, L, P, I, I, I, P, P],
-    'noise_norm_dot': [P, P, P, P, P, I, I, I, P],
+    'noise_norm_dot': [P, P, P, P, P, I, I, I, P, I, P],
+    'noise_dense_bf16': [P, I, I, P, I, I, P, P],
     'noise_mlp_fc_parts': [I],
     'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, P, P],
     'noise_head_ce_workspace_size': [I, I, I, I, SP],
-    'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P],
+    'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P, I, P],
     'noise_fitness': [P, I, I, I, P, P, P],
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
+
+
+
+class Pending(ctypes.Structure):
+    """noise_pending_t: a c_proj output not yet added to the residual stream (see include/noise_hip.h)."""
+    _fields_ = [('y', ctypes.c_void_p), ('u', ctypes.c_void_p), ('u_parts', ctypes.c_int),
+                ('u_row_stride', ctypes.c_long), ('u_part_stride', ctypes.c_long), ('a', ctypes.c_void_p)]
+
+
+def pending(*items):
+    """ctypes array of Pending from (y_ptr, u_ptr, u_parts, u_row_stride, u_part_stride, a_ptr) tuples, and
+    its length; (None, 0) when empty. Keep the returned array alive until the call is enqueued."""
+    if not items:
+        return None, 0
+    arr = (Pending * len(items))(*[Pending(*it) for it in items])
+    return ctypes.cast(arr, ctypes.c_void_p), len(items)
+
 
 # Entry points whose int result is a value, not a status.
 VALUE_RESULT = {'noise_version', 'noise_mlp_fc_parts'}

@@ -45,6 +45,15 @@ LowrankGemmArgs base_args(const void* x, long x_ld, long x_mstride, const void* 
   return g;
 }
 
+// Copies the C-ABI deferred residuals into the row kernels' descriptors (npend validated by the launch).
+int copy_pending(const noise_pending_t* src, int npend, Pending* dst) {
+  if (npend < 0 || npend > MAX_PENDING || (npend > 0 && !src)) return NOISE_EINVAL;
+  for (int k = 0; k < npend; ++k)
+    dst[k] = Pending{static_cast<const bf16*>(src[k].y), src[k].u, src[k].u_parts, src[k].u_row_stride,
+                     src[k].u_part_stride, src[k].a};
+  return NOISE_OK;
+}
+
 bool bad_members(int members, int T, int pair_shift) {
   return members <= 0 || T <= 0 || pair_shift < 0 || pair_shift > 1 || (long)members * T > 0x7fffffffL;
 }
@@ -154,9 +163,11 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
                       const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
                       const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
                       const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
-                      noise_stream_t stream) {
+                      const noise_pending_t* pend, int npend, noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
   BlockEntryArgs g{};
+  if (int rc = copy_pending(pend, npend, g.pend)) return rc;
+  g.npend = npend;
   g.x_in = x_in;
   g.x0 = x0;
   g.x_out = x_out;
@@ -260,10 +271,21 @@ int noise_lowrank_resid(const void* x, const void* w, int in, int out, const flo
 }
 
 int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
-                   int pair_shift, noise_stream_t stream) {
+                   int pair_shift, const noise_pending_t* pend, int npend, noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
   NormDotArgs g{x, static_cast<bf16*>(h), b, u, sign, members * T, T, pair_shift};
+  if (int rc = copy_pending(pend, npend, g.pend)) return rc;
+  g.npend = npend;
   return norm_dot_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_dense_bf16(const void* x, int in, int out, const void* w, int members, int T, void* y,
+                     noise_stream_t stream) {
+  if (members <= 0 || T <= 0 || (long)members * T > 0x7fffffffL || in <= 0 || out <= 0) return NOISE_EINVAL;
+  LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, nullptr, nullptr, members, T, 0);
+  g.out_bf16 = static_cast<bf16*>(y);
+  g.ldo = out;
+  return lowrank_gemm_launch(EPI_DENSE, g, static_cast<hipStream_t>(stream));
 }
 
 int noise_mlp_fc_parts(int f) { return xs_relu2_parts(f); }
@@ -299,7 +321,8 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
 
 int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
                   const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
-                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, noise_stream_t stream) {
+                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, const noise_pending_t* pend,
+                  int npend, noise_stream_t stream) {
   size_t need = 0;
   if (int rc = noise_head_ce_workspace_size(members, T, vocab, fp32_head, &need)) return rc;
   if (bad_members(members, T, pair_shift) || !x || !w_head || !loss) return NOISE_EINVAL;
@@ -313,6 +336,8 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
   HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
+  if (int rc = copy_pending(pend, npend, hn.pend)) return rc;
+  hn.npend = npend;
   if (int rc = head_norm_launch(hn, s)) return rc;
   LowrankGemmArgs g = base_args(hop, K, (long)T * K, w_head, K, vocab, a, sign, members, T, pair_shift);
   g.u = u;

@@ -13,6 +13,8 @@ enum : int {
                   // embedding added to v                   -> bf16 store
   EPI_CE = 4,     // z = 15 tanh(lowrank(x) / 15); per row partial sum of exp(z) over each wave's columns
                   // and z at the target column             -> fp32 partials
+  EPI_DENSE = 5,  // y = bf16(x W^T) only: the rank-1 term and the residual add are left to the row kernel
+                  // that consumes y (a deferred residual)  -> bf16 store
 };
 
 struct LowrankGemmArgs {

@@ -169,6 +169,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f);
   float pre_u = 0.f, pre_sign = 0.f;
   auto prefetch_ep = [&](int m0, int n0) {
+    if constexpr (EPI == EPI_DENSE) return;
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
     const int dir = pfirst >> g.pair_shift, seg = n0 / g.seg_n, ncol = n0 - seg * g.seg_n;
     if (tid < BN / 4) pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
@@ -181,6 +182,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     pre_u = u;
   };
   auto stage_ep = [&]() {
+    if constexpr (EPI == EPI_DENSE) return;
     if (tid < BN / 4) *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
     if (tid == 0) ep_sign = pre_sign;
     ep_u[tid / BM][tid % BM] = pre_u;
@@ -291,6 +293,17 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       const int lr = wm * WM + i * 16 + (lane & 15), row = m0 + lr;
       const bool live = row < g.M;
       const int rrow = live ? row : g.M - 1;
+      if constexpr (EPI == EPI_DENSE) {
+        if (live) {
+          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+#pragma unroll
+          for (int e = 0; e < CW; e += 8)
+            o[e / 8] = make_uint4(pack_bf16(acc[i][e / 4][0], acc[i][e / 4][1]), pack_bf16(acc[i][e / 4][2], acc[i][e / 4][3]),
+                                  pack_bf16(acc[i][e / 4 + 1][0], acc[i][e / 4 + 1][1]),
+                                  pack_bf16(acc[i][e / 4 + 1][2], acc[i][e / 4 + 1][3]));
+        }
+        continue;
+      }
       float u = 0.f;
 #pragma unroll
       for (int q = 0; q < C::UGROUPS; ++q) u += ep_u[q][lr];
@@ -483,6 +496,13 @@ int lowrank_gemm_parts(int N) {
 }
 
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
+  if (epi == EPI_DENSE) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.out_bf16 || g.lda % 8 || g.ldw % 8 ||
+        g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K || g.ldo % 8 || g.ldo < g.N || g.N % 128 || g.K % 64 ||
+        (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15))
+      return NOISE_EINVAL;
+    return launch_epi<EPI_DENSE>(g, stream);
+  }
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||

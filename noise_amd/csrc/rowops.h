@@ -4,6 +4,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// A c_proj output not yet added to the residual stream (deferred residual): row r receives
+// y[r, c] + s_p bf16(sum_q u[r * u_ld + q * u_qstride]) a[dir * 512 + c], with y = bf16(x W^T) from an
+// EPI_DENSE GEMM. y == null: nothing pending.
+struct Pending {
+  const __bf16* y;
+  const float* u;
+  int u_parts;
+  long u_ld, u_qstride;
+  const float* a;
+};
+constexpr int MAX_PENDING = 2;
+
 struct EmbedNormArgs {
   const float* w;        // [V, 512] embedding table
   const float* a;        // [dirs, V] output-side (row) vectors
@@ -34,6 +46,9 @@ struct BlockEntryArgs {
   const float* gate_a;   // [dirs, 8]
   const float* gate_b;   // [dirs, 32]
   float* gate;           // [M, 8] 2 sigmoid(...)
+  // deferred residuals added (in order) to x_in before the mix
+  Pending pend[MAX_PENDING];
+  int npend;
 };
 
 struct NormDotArgs {
@@ -43,6 +58,9 @@ struct NormDotArgs {
   float* u;              // [M]
   const float* sign;
   int M, T, pair_shift;
+  // deferred residuals added (in order) to x before the norm; x itself is not written back
+  Pending pend[MAX_PENDING];
+  int npend;
 };
 
 struct HeadNormArgs {
@@ -55,6 +73,9 @@ struct HeadNormArgs {
   const float* sign;
   int M, T, pair_shift;
   int fp32_head;
+  // deferred residuals added (in order) to x (fp32 only) before the norm
+  Pending pend[MAX_PENDING];
+  int npend;
 };
 
 struct CeFinalizeArgs {

@@ -52,6 +52,22 @@ __device__ __forceinline__ float dot_bf16(const Row8& h, const float* b) {
   return bf16r(group_sum<64>(acc));
 }
 
+// x += the deferred c_proj outputs (`x = x + lowrank(...)`, train/val/eggroll.py:92-93): the same fp32
+// operations the GEMM epilogue would have done, v = fma(s bf16(u), a, bf16 dense) then x + v, in order.
+__device__ __forceinline__ void add_pending(Row8& x, const Pending* pend, int npend, long row, int dir, float s,
+                                            int lane) {
+  for (int k = 0; k < npend; ++k) {
+    const Pending& pd = pend[k];
+    const bf16x8 yv = *reinterpret_cast<const bf16x8*>(pd.y + row * D + lane * 8);
+    float u = 0.f;
+    for (int q = 0; q < pd.u_parts; ++q) u += pd.u[row * pd.u_ld + q * pd.u_qstride];
+    const float su = s * bf16r(u);
+    const Row8 a = load8(pd.a + (long)dir * D + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x.v[e] = x.v[e] + fmaf(su, a.v[e], (float)yv[e]);
+  }
+}
+
 // x0 = norm(W[idx] + s a[:, idx] b) (train/val/eggroll.py:61-63, :74).
 __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
   const int lane = threadIdx.x & 63;
@@ -79,6 +95,7 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
   Row8 x = load8(g.x_in + row * D + lane * 8);
+  add_pending(x, g.pend, g.npend, row, dir, s, lane);
   const Row8 x0 = load8(g.x0 + row * D + lane * 8);
 #pragma unroll
   for (int e = 0; e < 8; ++e) x.v[e] = lr * x.v[e] + l0 * x0.v[e];
@@ -135,6 +152,7 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
   if (row >= g.M) return;
   const int p = (int)(row / g.T), dir = p >> g.pair_shift;
   Row8 x = load8(g.x + row * D + lane * 8);
+  if (g.npend) add_pending(x, g.pend, g.npend, row, dir, g.sign[p], lane);
   rms_norm_row(x);
   store8_bf16(g.h + row * D + lane * 8, x);
   const float u = dot_bf16(x, g.b + (long)dir * D + lane * 8);
@@ -157,6 +175,7 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     for (int e = 0; e < 8; ++e) x.v[e] = (float)xv[e];
   } else {
     x = load8(static_cast<const float*>(g.x) + row * D + lane * 8);
+    if (g.npend) add_pending(x, g.pend, g.npend, row, dir, g.sign[p], lane);
   }
   rms_norm_row(x);
   if (g.gain) {
@@ -228,6 +247,17 @@ __global__ void __launch_bounds__(256) cast_kernel(const float* __restrict__ in,
 
 int grid_rows(long M) { return (int)((M + 3) / 4); }
 
+bool bad_pending(const Pending* pend, int npend) {
+  if (npend < 0 || npend > MAX_PENDING) return true;
+  for (int k = 0; k < npend; ++k) {
+    const Pending& pd = pend[k];
+    if (!pd.y || !pd.u || !pd.a || pd.u_parts < 1 || pd.u_ld < 1 || pd.u_qstride < 1 ||
+        (((uintptr_t)pd.y | (uintptr_t)pd.a) & 15))
+      return true;
+  }
+  return false;
+}
+
 }  // namespace
 
 int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s) {
@@ -242,20 +272,24 @@ int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
       !g.lambda_r || !g.lambda_0 || !g.b_qkv[0] || !g.b_qkv[1] || !g.b_qkv[2])
     return NOISE_EINVAL;
   if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate)) return NOISE_EINVAL;
+  if (bad_pending(g.pend, g.npend)) return NOISE_EINVAL;
   hipLaunchKernelGGL(block_entry_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
 
 int norm_dot_launch(const NormDotArgs& g, hipStream_t s) {
-  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign) return NOISE_EINVAL;
+  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign || bad_pending(g.pend, g.npend))
+    return NOISE_EINVAL;
   hipLaunchKernelGGL(norm_dot_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
 
 int head_norm_launch(const HeadNormArgs& g, hipStream_t s) {
-  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign) return NOISE_EINVAL;
+  if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign || bad_pending(g.pend, g.npend) ||
+      (g.x_bf16 && g.npend))
+    return NOISE_EINVAL;
   hipLaunchKernelGGL(head_norm_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;

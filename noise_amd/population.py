@@ -90,6 +90,9 @@ class Buffers:
         self.qkv = torch.empty(M, 3 * D, device=device, dtype=b16)
         self.y = torch.empty(M, D, device=device, dtype=b16)
         self.u_attn = torch.empty(M, H, device=device, dtype=f32)
+        # dense products of the two c_proj GEMMs (their rank-1 terms and residual adds are deferred)
+        self.y_ap = torch.empty(M, D, device=device, dtype=b16)
+        self.y_mp = torch.empty(M, D, device=device, dtype=b16)
         self.u_fc = torch.empty(M, device=device, dtype=f32)
         self.parts = _lib.value('noise_mlp_fc_parts', F)
         self.hidden = torch.empty(M, F, device=device, dtype=b16)
@@ -171,6 +174,11 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     tm.close(t0)
     eps_r, eps_0 = noise['resid_lambdas'], noise['x0_lambdas']
     lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
+    # Deferred residuals. `x = x + lowrank(c_proj, ...)` (train/val/eggroll.py:92-93) is split: the c_proj GEMM
+    # writes only its bf16 dense product, and the next kernel that reads the residual stream adds the rank-1
+    # term and the residual with the same fp32 operations, in the same order (the MLP entry for the attention
+    # output; the next block entry, or the head, for both outputs of a block).
+    pend_prev = []
     for i in range(cfg.n_layer):
         pre = f'transformer.h.{i}.'
         aq, bq = noise[pre + 'attn.c_q.weight']
@@ -184,10 +192,11 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
             va, vb = noise[f'value_embeds.{i}.weight']
         x_in = buf.x0 if i == 0 else buf.x
         t0 = tm.mark('entry')
+        pend, npend = _lib.pending(*pend_prev)
         _lib.call('noise_block_entry', _p(x_in), _p(buf.x0), _p(buf.x), _p(buf.h), _p(buf.u_qkv), _p(bq), _p(bk),
                   _p(bv), lam_r.data_ptr() + 4 * i, lam_0.data_ptr() + 4 * i, eps_r.data_ptr() + 4 * i,
                   eps_0.data_ptr() + 4 * i, eps_r.stride(0), _p(gw) if ve else 0, _p(ga) if ve else 0,
-                  _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, s)
+                  _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, pend, npend, s)
         tm.close(t0)
         t0 = tm.mark('qkv')
         _lib.call('noise_qkv', _p(buf.h), _p(W.qkv[i]), _p(aq), _p(ak), _p(av), _p(buf.u_qkv), _p(sign), m, T, ps,
@@ -201,26 +210,29 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
                   0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
-        _lib.call('noise_lowrank_resid', _p(buf.y), _p(W.proj[i]), D, D, _p(ap), _p(buf.u_attn), H, H, 1, _p(sign),
-                  m, T, ps, _p(buf.x), s)
+        _lib.call('noise_dense_bf16', _p(buf.y), D, D, _p(W.proj[i]), m, T, _p(buf.y_ap), s)
         tm.close(t0)
+        attn_out = (_p(buf.y_ap), _p(buf.u_attn), H, H, 1, _p(ap))
         af, bf_ = noise[pre + 'mlp.c_fc.weight']
         am, bm = noise[pre + 'mlp.c_proj.weight']
         t0 = tm.mark('mlp_entry')
-        _lib.call('noise_norm_dot', _p(buf.x), _p(buf.h), _p(bf_), _p(buf.u_fc), _p(sign), m, T, ps, s)
+        pend, npend = _lib.pending(attn_out)
+        _lib.call('noise_norm_dot', _p(buf.x), _p(buf.h), _p(bf_), _p(buf.u_fc), _p(sign), m, T, ps, pend, npend, s)
         tm.close(t0)
         t0 = tm.mark('mlp')
         _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
                   _p(buf.hidden), _p(buf.u_mlp), s)
-        # the fc partials are part-major with stride m * T (this chunk's rows)
-        _lib.call('noise_lowrank_resid', _p(buf.hidden), _p(W.mproj[i]), F, D, _p(am), _p(buf.u_mlp), buf.parts, 1,
-                  m * T, _p(sign), m, T, ps, _p(buf.x), s)
+        _lib.call('noise_dense_bf16', _p(buf.hidden), F, D, _p(W.mproj[i]), m, T, _p(buf.y_mp), s)
         tm.close(t0)
+        # the fc partials are part-major with stride m * T (this chunk's rows)
+        mlp_out = (_p(buf.y_mp), _p(buf.u_mlp), buf.parts, 1, m * T, _p(am))
+        pend_prev = [attn_out, mlp_out]
     ah, bh = noise['lm_head.weight']
     Vh = W.head_w.shape[0]
     t0 = tm.mark('head')
+    pend, npend = _lib.pending(*pend_prev)
     _lib.call('noise_head_ce', _p(buf.x), 0, 0, _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
-              _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), s)
+              _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), pend, npend, s)
     tm.close(t0)
 
 

@@ -97,7 +97,7 @@ def test_block_entry_and_qkv_match_oracle():
     _lib.call('noise_block_entry', d['x'].data_ptr(), d['x0'].data_ptr(), xo.data_ptr(), h.data_ptr(), u.data_ptr(),
               d['bq'].data_ptr(), d['bk'].data_ptr(), d['bv'].data_ptr(), d['lr'].data_ptr(), d['l0'].data_ptr(),
               d['er'].data_ptr() + 4 * 3, d['e0'].data_ptr() + 4 * 3, 8, d['gw'].data_ptr(), d['ga'].data_ptr(),
-              d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, s)
+              d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, None, 0, s)
     _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
               u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), gate.data_ptr(),
               d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(), d['idx'].data_ptr(), qkv.data_ptr(), s)
@@ -131,6 +131,68 @@ def test_block_entry_and_qkv_match_oracle():
         assert rel_err(got[:, :, k], om.bf(ref)) < 5e-3, k
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
 
+
+
+def test_deferred_residuals_match_eager_lowrank():
+    """Two c_proj outputs deferred into the block entry and one into the MLP entry equal the eager
+    `x = x + lowrank(...)` of train/val/eggroll.py:92-93: dense bf16 product plus s bf16(sum of the input-side
+    partials) a, added in order in fp32 (partials row-major for the attention, part-major for the MLP)."""
+    g = torch.Generator().manual_seed(12)
+    m, T, D = 4, 64, 512
+    M = m * T
+    x, x0 = torch.randn(M, D, generator=g) * 3, torch.randn(M, D, generator=g)
+    y1, y2 = (torch.randn(M, D, generator=g).bfloat16() for _ in range(2))
+    u1 = torch.randn(M, 8, generator=g)           # row-major partials [rows, 8]
+    u2 = torch.randn(8, M, generator=g)           # part-major partials [8, rows]
+    a1, a2 = torch.randn(m // 2, D, generator=g), torch.randn(m // 2, D, generator=g)
+    sign = torch.tensor([0.05, -0.05, 0.02, -0.02])
+    lr, l0 = torch.tensor([0.9]), torch.tensor([0.3])
+    er, e0 = torch.randn(m // 2, 8, generator=g), torch.randn(m // 2, 8, generator=g)
+    bq, bk, bv = (torch.randn(m // 2, D, generator=g) for _ in range(3))
+    dev = {k: v.to(DEV) for k, v in dict(x=x, x0=x0, y1=y1, y2=y2, u1=u1, u2=u2, a1=a1, a2=a2, sign=sign, lr=lr, l0=l0,
+                                          er=er, e0=e0, bq=bq, bk=bk, bv=bv).items()}
+    log_case(f'deferred residuals m={m} T={T}')
+    s = torch.cuda.current_stream().cuda_stream
+    p1 = (dev['y1'].data_ptr(), dev['u1'].data_ptr(), 8, 8, 1, dev['a1'].data_ptr())
+    p2 = (dev['y2'].data_ptr(), dev['u2'].data_ptr(), 8, 1, M, dev['a2'].data_ptr())
+    xo = torch.empty(M, D, device=DEV)
+    h = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+    u = torch.empty(M, 4, device=DEV)
+    pend, npend = _lib.pending(p1, p2)
+    _lib.call('noise_block_entry', dev['x'].data_ptr(), dev['x0'].data_ptr(), xo.data_ptr(), h.data_ptr(), u.data_ptr(),
+              dev['bq'].data_ptr(), dev['bk'].data_ptr(), dev['bv'].data_ptr(), dev['lr'].data_ptr(), dev['l0'].data_ptr(),
+              dev['er'].data_ptr() + 4 * 3, dev['e0'].data_ptr() + 4 * 3, 8, 0, 0, 0, 0, dev['sign'].data_ptr(), m, T, 1,
+              pend, npend, s)
+    hn = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+    un = torch.empty(M, device=DEV)
+    pend1, n1 = _lib.pending(p1)
+    _lib.call('noise_norm_dot', dev['x'].data_ptr(), hn.data_ptr(), dev['bq'].data_ptr(), un.data_ptr(),
+              dev['sign'].data_ptr(), m, T, 1, pend1, n1, s)
+    torch.cuda.synchronize()
+    rows = torch.arange(M)
+    member = rows // T
+    srow = sign[member][:, None]
+    dirs = member // 2
+
+    def lowrank_out(y, usum, a):
+        return y.float() + (srow * om.bf(usum)[:, None]) * a[dirs]
+    def seqsum(parts):  # q = 0, 1, ... in fp32, the kernel's order (bf16 rounding of the sum is order-sensitive)
+        acc = parts[0].clone()
+        for q in range(1, parts.shape[0]):
+            acc = acc + parts[q]
+        return acc
+    v1 = lowrank_out(y1, seqsum(u1.t()), a1)
+    v2 = lowrank_out(y2, seqsum(u2), a2)
+    mixed = ((x + v1) + v2)
+    lam_r = lr + srow * er[dirs][:, 3:4]
+    lam_0 = l0 + srow * e0[dirs][:, 3:4]
+    ref_x = lam_r * mixed + lam_0 * x0
+    assert torch.allclose(xo.cpu(), ref_x, rtol=1e-5, atol=1e-5)
+    assert rel_err(h.cpu().float(), om.bf(om.norm(ref_x))) < 5e-3
+    ref_h1 = om.norm(x + v1)
+    assert rel_err(hn.cpu().float(), om.bf(ref_h1)) < 5e-3
+    # x itself is not written by the MLP entry
+    assert torch.equal(dev['x'].cpu(), x)
 
 @pytest.mark.parametrize('qk_norm', [0, 1])
 def test_attention_matches_oracle_and_moments(qk_norm):
@@ -189,7 +251,7 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
         ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV,
                          dtype=torch.uint8)
         _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
-                  sd.data_ptr(), td.data_ptr(), m, T, 0, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
+                  sd.data_ptr(), td.data_ptr(), m, T, 0, loss.data_ptr(), ws.data_ptr(), ws.numel(), None, 0, s)
         torch.cuda.synchronize()
         if fp32:
             ref = om.head_loss(h, W, a, b, sign, targets, 'fp32', 'fp32')
@@ -217,7 +279,7 @@ def test_head_ce_config3_bf16_input_with_gain():
     loss = torch.empty(m, device=DEV)
     ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, 1), device=DEV, dtype=torch.uint8)
     _lib.call('noise_head_ce', hd.data_ptr(), 1, gd.data_ptr(), wd.data_ptr(), V, 1, ad.data_ptr(), bd.data_ptr(),
-              sd.data_ptr(), td.data_ptr(), m, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(), s)
+              sd.data_ptr(), td.data_ptr(), m, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(), None, 0, s)
     torch.cuda.synchronize()
     rep = lambda t: t.repeat_interleave(2, 0)  # noqa: E731
     ref = om.norm_head_ce(h.float(), gain, W, rep(a), rep(b), sign, targets)
