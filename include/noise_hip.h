@@ -39,7 +39,7 @@ typedef void* noise_stream_t; /* hipStream_t */
  *   y[r, c] + sign[p] * bf16(sum_{q < u_parts} u[r * u_row_stride + q * u_part_stride]) * a[dir * 512 + c]
  * with y = bf16(x W^T) from noise_dense_bf16: `x = x + linear(name, x_in)` of train/val/eggroll.py:92-93 with
  * the rank-1 term of `lowrank` (:56-58) applied where the residual stream is next read. y, a 16-byte
- * aligned. */
+ * aligned; 1 <= u_parts <= 64. */
 typedef struct noise_pending {
   const void* y;            /* bf16 [members*T, 512] */
   const float* u;           /* input-side dot partials of the c_proj input */

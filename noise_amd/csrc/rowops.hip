@@ -59,8 +59,10 @@ __device__ __forceinline__ void add_pending(Row8& x, const Pending* pend, int np
   for (int k = 0; k < npend; ++k) {
     const Pending& pd = pend[k];
     const bf16x8 yv = *reinterpret_cast<const bf16x8*>(pd.y + row * D + lane * 8);
+    // lane q loads partial q; the sum runs q = 0, 1, ... on the broadcast values (a fixed order)
+    const float uq = lane < pd.u_parts ? pd.u[row * pd.u_ld + lane * pd.u_qstride] : 0.f;
     float u = 0.f;
-    for (int q = 0; q < pd.u_parts; ++q) u += pd.u[row * pd.u_ld + q * pd.u_qstride];
+    for (int q = 0; q < pd.u_parts; ++q) u += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uq), q));
     const float su = s * bf16r(u);
     const Row8 a = load8(pd.a + (long)dir * D + lane * 8);
 #pragma unroll
@@ -251,7 +253,7 @@ bool bad_pending(const Pending* pend, int npend) {
   if (npend < 0 || npend > MAX_PENDING) return true;
   for (int k = 0; k < npend; ++k) {
     const Pending& pd = pend[k];
-    if (!pd.y || !pd.u || !pd.a || pd.u_parts < 1 || pd.u_ld < 1 || pd.u_qstride < 1 ||
+    if (!pd.y || !pd.u || !pd.a || pd.u_parts < 1 || pd.u_parts > 64 || pd.u_ld < 1 || pd.u_qstride < 1 ||
         (((uintptr_t)pd.y | (uintptr_t)pd.a) & 15))
       return true;
   }
