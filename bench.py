@@ -153,7 +153,7 @@ def run_step(args):
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
-                     'kernel': 'fused relu^2 MLP: xs_relu2_kernel (c_fc, weight-resident) + lowrank_gemm<EPI_RESID> (c_proj)',
+                     'kernel': 'fused relu^2 MLP: xs_relu2_kernel (c_fc, weight-resident) + lowrank_gemm<EPI_DENSE> (c_proj)',
                      'flop_per_launch': mlp_flop, 'ms_per_launch': mlp_ms},
         'forward_tflops': flop_tok * P * T / (sum(v for k, v in stages.items()) / args.steps * 1e-3) / 1e12,
         'stage_ms_per_step': {k: v / args.steps for k, v in stages.items()},
@@ -309,12 +309,31 @@ def run_head(args):
                     'ms_per_launch': ms_launch})
 
 
+def run_copy(args):
+    """A plain 1 GiB device-to-device copy: the known-size kernel that calibrates the FETCH_SIZE and
+    WRITE_SIZE counters (read 1 GiB, write 1 GiB per launch) and a check of the HBM roofline."""
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    n = 1 << 29
+    src = torch.ones(n, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    ms_step, ms_launch = _timed(lambda: dst.copy_(src), args.steps, args.warmup)
+    nbytes = 2 * 2 * n
+    achieved = nbytes / (ms_launch * 1e-3) / 1e9
+    return {'metric': 'device copy bandwidth (counter calibration)', 'value': achieved, 'unit': 'GB/s', 'n_gpus': 1,
+            'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': ms_step, 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+            'config': {'workload': 'copy_1GiB', 'bytes_read': 2 * n, 'bytes_written': 2 * n},
+            'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': 8000.0, 'unit': 'GB/s',
+                         'frac': achieved / 8000.0, 'traffic': nbytes, 'kernel': 'torch copy_'}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=3)
     ap.add_argument('--warmup', type=int, default=1)
-    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head'), default='step')
+    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy'), default='step')
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
     ap.add_argument('--qk-norm', action='store_true', help='config 2 with RMS-normalised q, k rows (the model case)')
     ap.add_argument('--pairs', type=int, default=1536)
@@ -328,8 +347,9 @@ def main():
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
         sys.exit(2)
-    result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head}[args.workload](args)
-    if not args.no_cpu_baseline:
+    result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head,
+              'copy': run_copy}[args.workload](args)
+    if not args.no_cpu_baseline and args.workload != 'copy':
         result['cpu_baseline'] = cpu_baseline_mlp() if args.workload == 'mlp' else cpu_baseline_step()
     print(json.dumps(result), flush=True)
 

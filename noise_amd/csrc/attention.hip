@@ -86,8 +86,13 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   __shared__ float smom[NWAVE][2][HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
-  // heavier (later) query blocks first
-  const int qblk = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, p = blockIdx.z;
+  // XCD-aware order. Workgroups reach the 8 XCDs round-robin (workgroup b runs on XCD b % 8), so XCD x takes
+  // a contiguous range of logical indices n: the query blocks of one (member, head) run together on one XCD
+  // and read its K/V through that XCD's L2 once from HBM. Heavier (later) query blocks first.
+  const int nq = g.T / BQ;
+  const unsigned G = gridDim.x, b = blockIdx.x, x = b & 7, qg = G >> 3, rg = G & 7;
+  const unsigned n = x * qg + min(x, rg) + (b >> 3);
+  const int ph = (int)(n / nq), qblk = nq - 1 - (int)(n % nq), h = ph % g.H, p = ph / g.H;
   const int q0 = qblk * BQ;
   const long rbase = (long)p * g.T;
   const bf16* qkv = g.qkv;
@@ -310,7 +315,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     if (tid < 2 * HD) {
       const int k = tid / HD, d = tid % HD;
       const float v = smom[0][k][d] + smom[1][k][d] + smom[2][k][d] + smom[3][k][d];
-      g.mom[((((long)p * gridDim.y + h) * gridDim.x + qblk) * 2 + k) * HD + d] = v;
+      g.mom[((((long)p * g.H + h) * nq + qblk) * 2 + k) * HD + d] = v;
     }
   }
 }
@@ -335,11 +340,12 @@ int attention_launch(const AttnArgs& g, hipStream_t s) {
     return NOISE_EINVAL;
   if (g.upart && (!g.b_proj || g.upart_ld < g.H || g.b_ld < g.H * HD)) return NOISE_EINVAL;
   if (g.mom && !g.mom_out) return NOISE_EINVAL;
-  if ((long)g.members > 65535 || g.H > 65535) return NOISE_ENOTSUP;
+  const long grid = (long)(g.T / BQ) * g.H * g.members;
+  if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   if (g.qk_norm)
-    hipLaunchKernelGGL(attention_kernel<true>, dim3(g.T / BQ, g.H, g.members), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL(attention_kernel<true>, dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else
-    hipLaunchKernelGGL(attention_kernel<false>, dim3(g.T / BQ, g.H, g.members), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)grid), dim3(NTH), 0, s, g);
   NOISE_CHECK_LAUNCH();
   if (g.mom) {
     const long n = (long)g.members * g.H * 2 * HD;
