@@ -18,12 +18,16 @@
 // XCD's L2 to every slice.
 //
 // x path. Blocks of 32 rows x 512 K (32 KiB) stream through a 4-deep LDS ring with direct global -> LDS
-// loads (global_load_lds_dwordx4). The LDS image of a block is fragment-major: fragment d (k step d / 2,
-// row half d % 2) is 1 KiB at byte d * 1024, in exactly the MFMA B-operand lane order, so every ds_read_b128
-// is lane-contiguous. The loads are issued from inline assembly: the compiler would otherwise make every
-// LDS read wait for every outstanding LDS-bound load (vmcnt(0)), which drains the ring. The kernel waits
-// for them itself: vector memory operations complete in issue order, so "block k landed" is
-// s_waitcnt vmcnt(n) with n = the operations issued after block k's loads, followed by s_barrier.
+// loads (global_load_lds_dwordx4), one whole 1 KiB row per instruction: every request is a full 128-byte
+// line (a 16 rows x 64 bytes pattern, half lines, measured 8.9 TB/s from L2 into LDS against 15.9 TB/s for
+// whole rows). LDS rows are 1040 bytes apart, so the 16 rows of an MFMA fragment fall in 16 different bank
+// groups. The contraction order inside K is permuted to make the fragment reads affine: MFMA k step s,
+// lane group g (lanes 16 g .. 16 g + 15) contracts k = 128 g + 8 s .. + 7, i.e. LDS chunk 16 g + s of the
+// lane's row, and the resident W fragments use the same k. The loads are issued from inline assembly: the
+// compiler would otherwise make every LDS read wait for every outstanding LDS-bound load (vmcnt(0)), which
+// drains the ring. The kernel waits for them itself: vector memory operations complete in issue order, so
+// "block k landed" is s_waitcnt vmcnt(n) with n = the operations issued after block k's loads, followed by
+// s_barrier.
 //
 // Epilogue overlap. Iteration k runs the MFMAs of block k and, interleaved one stage per MFMA k step (a
 // scheduling barrier between steps keeps the interleave), the epilogue of block k - 1 from the other
@@ -48,7 +52,8 @@ constexpr int NW = 8;                 // waves per workgroup
 constexpr int BN = 256;               // columns per workgroup slice (32 per wave)
 constexpr int KD = 512;               // K
 constexpr int KS = KD / 32;           // MFMA k steps per block
-constexpr int XBYTES = R * KD * 2;    // 32 KiB of x per block
+constexpr int XROW = KD * 2 + 16;     // LDS bytes per x row (1 KiB + 16: bank-group skew between rows)
+constexpr int XBYTES = R * XROW;      // LDS bytes of one x block
 constexpr int VEC = 512;              // per-wave vector area: a (128 B) | b_next (128 B) | u (128 B) | .. | sign
 constexpr int SIGN_OFF = VEC - 8;
 constexpr int DMA_PER_BLOCK = 6;      // per wave and block: 4 x fragments, a|b_next|u, sign
@@ -85,7 +90,7 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned v) { return *reinterpret_cast<bf16x2*>(&v); }
 
 __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[NBUF * XBYTES];
+  __shared__ __attribute__((aligned(16))) char smem[NBUF * XBYTES];
   __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
   __shared__ __attribute__((aligned(16))) float red[2][R][NW];
 
@@ -101,17 +106,17 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
   if (nb == 0) return;
   const int fw = nslice * BN + wave * 32;  // first column of this wave
 
-  // ---- resident W: fragment [j][s] holds W row fw + 8 (r >> 2) + 4 j + (r & 3), r = lane & 15, k = 32 s + 8 grp.
-  // MFMA output element e of column block j in lane l is then column fw + 8 (l >> 4) + 4 j + e: the lane's 8
-  // columns are contiguous.
+  // ---- resident W: fragment [j][s] holds W row fw + 8 (r >> 2) + 4 j + (r & 3), r = lane & 15,
+  // k = 128 grp + 8 s. MFMA output element e of column block j in lane l is then column
+  // fw + 8 (l >> 4) + 4 j + e: the lane's 8 columns are contiguous.
   bf16x8 wr[2][KS];
   {
     const int r = lane & 15;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const bf16* wp = g.W + (long)(fw + 8 * (r >> 2) + 4 * j + (r & 3)) * g.ldw + 8 * grp;
+      const bf16* wp = g.W + (long)(fw + 8 * (r >> 2) + 4 * j + (r & 3)) * g.ldw + 128 * grp;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) wr[j][s] = *reinterpret_cast<const bf16x8*>(wp + 32 * s);
+      for (int s = 0; s < KS; ++s) wr[j][s] = *reinterpret_cast<const bf16x8*>(wp + 8 * s);
     }
   }
   // the resident fragments have landed before any LDS-bound load is issued, so no wait below covers them
@@ -119,19 +124,16 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
 
   auto blk_of = [&](int k) { return lo + stream + k * streams; };
 
-  // ---- loads of block k into ring slot k % NBUF. Wave w fills x fragments d = 4 w + q: lane L loads row
-  // 16 (d & 1) + (L & 15), k 32 (d >> 1) + 8 (L >> 4). Lanes 0-7 load a_p, 8-15 b_next over the wave's 32
-  // columns, 16-23 the block's 32 input-side dots; lane 0 the member's sign.
+  // ---- loads of block k into ring slot k % NBUF. Wave w fills x rows 4 w + q: lane L loads k 8 L .. 8 L + 7.
+  // Lanes 0-7 load a_p, 8-15 b_next over the wave's 32 columns, 16-23 the block's 32 input-side dots; lane 0
+  // the member's sign.
   auto issue = [&](int k) {
     const int buf = k % NBUF, row0 = blk_of(k) * R;
     const int p = row0 / g.T, t0 = row0 - p * g.T, dir = p >> g.pair_shift;
-    const bf16* abase = g.A + (long)p * g.a_mstride;
-    char* xsl = smem + buf * XBYTES;
+    const bf16* abase = g.A + (long)p * g.a_mstride + (long)(t0 + 4 * wave) * g.lda + 8 * lane;
+    char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int d = 4 * wave + q;
-      dma_x4(abase + (long)(t0 + 16 * (d & 1) + (lane & 15)) * g.lda + 32 * (d >> 1) + 8 * grp, xsl + d * 1024);
-    }
+    for (int q = 0; q < 4; ++q) dma_x4(abase + q * g.lda, xsl + q * XROW);
     const float* vsrc = lane < 8 ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
                         : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
                                     : g.u + row0 + 4 * (lane - 16);
@@ -220,21 +222,22 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
     wait_block(min(NBUF - 2, nb - 1 - k), min(2, max(0, k - 1)));
     __builtin_amdgcn_s_barrier();
     const int pbuf = (k + NBUF - 1) % NBUF;
-    const bf16* xsb = reinterpret_cast<const bf16*>(smem + (k % NBUF) * XBYTES) + lane * 8;
+    // lane (row r = lane & 15, group grp): row-half i at LDS row 16 i + r, step s at chunk 16 grp + s
+    const char* xsb = smem + (k % NBUF) * XBYTES + (lane & 15) * XROW + 256 * grp;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     bf16x8 xa[2], xb[2];
     xa[0] = *reinterpret_cast<const bf16x8*>(xsb);
-    xa[1] = *reinterpret_cast<const bf16x8*>(xsb + 512);
+    xa[1] = *reinterpret_cast<const bf16x8*>(xsb + 16 * XROW);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       bf16x8(&xc)[2] = (s & 1) ? xb : xa;
       bf16x8(&xn)[2] = (s & 1) ? xa : xb;
       if (s + 1 < KS) {
-        xn[0] = *reinterpret_cast<const bf16x8*>(xsb + (2 * (s + 1)) * 512);
-        xn[1] = *reinterpret_cast<const bf16x8*>(xsb + (2 * (s + 1) + 1) * 512);
+        xn[0] = *reinterpret_cast<const bf16x8*>(xsb + 16 * (s + 1));
+        xn[1] = *reinterpret_cast<const bf16x8*>(xsb + 16 * XROW + 16 * (s + 1));
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
