@@ -35,6 +35,13 @@ extern "C" {
 
 typedef void* noise_stream_t; /* hipStream_t */
 
+/* Layouts of a bf16 activation [rows, cols] exchanged between entry points. */
+#define NOISE_LAYOUT_ROWS 0   /* row-major, cols contiguous (the reference's tensor layout) */
+#define NOISE_LAYOUT_TILE16 1 /* 1 KiB tiles of 16 rows x 32 cols (rows % 16 == 0, cols % 32 == 0): element
+                               * (r, c) at (r/16)*16*cols + (c/32)*512 + 8*p + c%8 with
+                               * p = 4*(r%16) + (((c%32)/8) ^ (((r%16)/2) % 4)). Same footprint as ROWS; a
+                               * producer writes and the GEMM loads it as whole 128-byte lines. */
+
 /* A c_proj output not yet added to the residual stream (a deferred residual): row r of member p receives
  *   y[r, c] + sign[p] * bf16(sum_{q < u_parts} u[r * u_row_stride + q * u_part_stride]) * a[dir * 512 + c]
  * with y = bf16(x W^T) from noise_dense_bf16: `x = x + linear(name, x_in)` of train/val/eggroll.py:92-93 with
@@ -147,10 +154,11 @@ int noise_lowrank_resid(const void* x, const void* w, int in, int out, const flo
                         long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
                         float* resid, noise_stream_t stream);
 
-/* y = bf16(x W^T) [members*T, out] for x bf16 [members*T, in], w bf16 [out, in]: the dense product of a
- * c_proj `lowrank` whose rank-1 term and residual add are deferred to the row kernel that next reads the
- * stream (noise_pending_t). in % 64 == 0, out % 128 == 0. */
-int noise_dense_bf16(const void* x, int in, int out, const void* w, int members, int T, void* y,
+/* y = bf16(x W^T) [members*T, out] for x bf16 [members*T, in] (x_layout NOISE_LAYOUT_ROWS or
+ * NOISE_LAYOUT_TILE16), w bf16 [out, in]: the dense product of a c_proj `lowrank` whose rank-1 term and
+ * residual add are deferred to the row kernel that next reads the stream (noise_pending_t). in % 64 == 0,
+ * out % 128 == 0; TILE16 also T % 16 == 0. */
+int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int members, int T, void* y,
                      noise_stream_t stream);
 
 /* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). The npend (<= 2)
@@ -158,13 +166,15 @@ int noise_dense_bf16(const void* x, int in, int out, const void* w, int members,
 int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,
                    int pair_shift, const noise_pending_t* pend, int npend, noise_stream_t stream);
 
-/* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] and its dot partials with bf16(b_proj),
+/* hidden = bf16(relu(lowrank(h, w_fc))^2) [members*T, f] in hidden_layout (NOISE_LAYOUT_ROWS or
+ * NOISE_LAYOUT_TILE16, the layout noise_dense_bf16 loads fastest) and its dot partials with bf16(b_proj),
  * part-major: upart [noise_mlp_fc_parts(f), members*T] (one partial per 256 columns), for the
- * following noise_lowrank_resid. d == 512, f % 256 == 0, T % 32 == 0 (NOISE_ENOTSUP otherwise). */
+ * following noise_lowrank_resid or deferred residual. d == 512, f % 256 == 0, T % 32 == 0 (NOISE_ENOTSUP
+ * otherwise). */
 int noise_mlp_fc_parts(int f);
 int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
-                 float* upart, noise_stream_t stream);
+                 int hidden_layout, float* upart, noise_stream_t stream);
 
 /* Per-member mean soft-capped cross-entropy (train/val/eggroll.py:94-103): h = norm(x) (times gain
  * when gain is not null: the config-3 extension; null reproduces utils/model.py:46-47);

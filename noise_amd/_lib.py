@@ -17,6 +17,7 @@ ERRORS = {-1: 'NOISE_EINVAL (rejected argument)', -2: 'NOISE_ENOSPC (workspace t
           -3: 'NOISE_ENOTSUP (shape outside the kernel tiling)'}
 
 FITNESS_ZSCORE, FITNESS_RANK = 0, 1
+LAYOUT_ROWS, LAYOUT_TILE16 = 0, 1
 
 # name -> argtypes in declaration order; every entry point returns int. Pointers (device buffers,
 # the stream) are c_void_p.
@@ -34,9 +35,9 @@ SIGNATURES = {
     'noise_attention': [P, I, I, I, I, P, I, P, P, P, P, S, P],
     'noise_lowrank_resid': [P, P, I, I, P, P, I, L, L, P, I, I, I, P, P],
     'noise_norm_dot': [P, P, P, P, P, I, I, I, P, I, P],
-    'noise_dense_bf16': [P, I, I, P, I, I, P, P],
+    'noise_dense_bf16': [P, I, I, I, P, I, I, P, P],
     'noise_mlp_fc_parts': [I],
-    'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, P, P],
+    'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, I, P, P],
     'noise_head_ce_workspace_size': [I, I, I, I, SP],
     'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P, I, P],
     'noise_fitness': [P, I, I, I, P, P, P],

@@ -132,12 +132,14 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   g1.u_ld = 1;
   g1.out_bf16 = hid;
   g1.ldo = f;
+  g1.out_tiled = 1;  // the hidden never leaves the library: TILE16, whole-line stores and loads
   g1.rb_next = b_proj;
   g1.rb_next_ld = f;
   g1.upart_out = upart;
   g1.upart_ld = parts;
   if (int rc = lowrank_gemm_launch(EPI_RELU2, g1, s)) return rc;
   LowrankGemmArgs g2 = base_args(hid, f, (long)T * f, w_proj, f, d, a_proj, sign, members, T, pair_shift);
+  g2.a_tiled = 1;
   g2.u = upart;
   g2.u_parts = parts;
   g2.u_ld = 1;
@@ -279,10 +281,12 @@ int noise_norm_dot(const float* x, void* h, const float* b, float* u, const floa
   return norm_dot_launch(g, static_cast<hipStream_t>(stream));
 }
 
-int noise_dense_bf16(const void* x, int in, int out, const void* w, int members, int T, void* y,
+int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int members, int T, void* y,
                      noise_stream_t stream) {
   if (members <= 0 || T <= 0 || (long)members * T > 0x7fffffffL || in <= 0 || out <= 0) return NOISE_EINVAL;
+  if (x_layout != NOISE_LAYOUT_ROWS && x_layout != NOISE_LAYOUT_TILE16) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, nullptr, nullptr, members, T, 0);
+  g.a_tiled = x_layout == NOISE_LAYOUT_TILE16;
   g.out_bf16 = static_cast<bf16*>(y);
   g.ldo = out;
   return lowrank_gemm_launch(EPI_DENSE, g, static_cast<hipStream_t>(stream));
@@ -292,14 +296,16 @@ int noise_mlp_fc_parts(int f) { return xs_relu2_parts(f); }
 
 int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_fc, const float* u,
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
-                 float* upart, noise_stream_t stream) {
+                 int hidden_layout, float* upart, noise_stream_t stream) {
   if (bad_members(members, T, pair_shift) || !xs_relu2_parts(f)) return NOISE_EINVAL;
+  if (hidden_layout != NOISE_LAYOUT_ROWS && hidden_layout != NOISE_LAYOUT_TILE16) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(h, d, (long)T * d, w_fc, d, f, a_fc, sign, members, T, pair_shift);
   g.u = u;
   g.u_parts = 1;
   g.u_ld = 1;
   g.out_bf16 = static_cast<bf16*>(hidden);
   g.ldo = f;
+  g.out_tiled = hidden_layout == NOISE_LAYOUT_TILE16;
   g.rb_next = b_proj;
   g.rb_next_ld = f;
   g.upart_out = upart;

@@ -17,12 +17,24 @@ enum : int {
                   // that consumes y (a deferred residual)  -> bf16 store
 };
 
+// TILE16 layout of a bf16 matrix [rows, cols] with leading dimension ld (rows % 16 == 0, ld % 32 == 0):
+// element (r, c) lives at (r / 16) * 16 * ld + (c / 32) * 512 + 8 * p + c % 8, with
+// p = 4 (r % 16) + (((c % 32) / 8) ^ (((r % 16) >> 1) & 3)). Each 1 KiB tile (16 rows x 32 columns) is
+// contiguous and already in the order of the GEMM's swizzled 32-deep LDS stage, so one wave-wide LDS-DMA
+// instruction moves one tile as eight whole 128-byte lines.
+__host__ __device__ inline long tile16_offset(long r, long c, long ld) {
+  const long rr = r & 15, p = 4 * rr + (((c & 31) >> 3) ^ ((rr >> 1) & 3));
+  return (r >> 4) * 16 * ld + (c >> 5) * 512 + 8 * p + (c & 7);
+}
+
 struct LowrankGemmArgs {
   // A operand: row r (member p = r / T, token t = r % T) starts at A + p * a_mstride + t * lda.
   // a_mstride = T * lda for per-member activations, 0 for one activation broadcast to all members.
+  // a_tiled: A is TILE16 with leading dimension lda over all M rows (requires a_mstride = T * lda).
   const __bf16* A;
   long lda;
   long a_mstride;
+  int a_tiled;
   const __bf16* W;  // [N, K], K contiguous (nn.Linear orientation)
   long ldw;
   int M, N, K;
@@ -46,6 +58,7 @@ struct LowrankGemmArgs {
   float* out_f32;     // EPI_STORE (optional) / EPI_RESID (accumulated in place)
   __bf16* out_bf16;   // EPI_STORE (optional) / EPI_RELU2 / EPI_QKV
   long ldo;
+  int out_tiled;      // EPI_RELU2: out_bf16 is TILE16 with leading dimension ldo
   // EPI_RELU2: partial dots of the bf16 output with the next layer's input-side vector b_next, part-major
   // [xs_relu2_parts(N), M]. EPI_CE: per-row partial sums, row-major [M, upart_ld].
   const float* rb_next;

@@ -135,10 +135,16 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto set_sources = [&](int m0, int n0) {
 #pragma unroll
     for (int d = 0; d < C::LA; ++d) {
-      const int r = (wave * C::LA + d) * C::ROWS_PER_DMA + lrow;
-      const int c = (lane % C::CPR) ^ ((r / C::RPL) % C::CPR);
-      const int row = min(m0 + r, g.M - 1);
-      a_src[d] = (long)(row / g.T) * g.a_mstride + (long)(row % g.T) * g.lda + c * 8;
+      if (g.a_tiled) {
+        // the 16 rows of this instruction are one 1 KiB TILE16 tile per 32-deep stage
+        const int G = min(m0 + (wave * C::LA + d) * C::ROWS_PER_DMA, g.M - 16) >> 4;
+        a_src[d] = (long)G * 16 * g.lda + 8 * lane;
+      } else {
+        const int r = (wave * C::LA + d) * C::ROWS_PER_DMA + lrow;
+        const int c = (lane % C::CPR) ^ ((r / C::RPL) % C::CPR);
+        const int row = min(m0 + r, g.M - 1);
+        a_src[d] = (long)(row / g.T) * g.a_mstride + (long)(row % g.T) * g.lda + c * 8;
+      }
     }
 #pragma unroll
     for (int d = 0; d < C::LB; ++d) {
@@ -152,10 +158,10 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto issue = [&](int kt, int buf) {
     bf16* sx = smem + buf * C::STAGE;
     bf16* sw = sx + BM * BK;
-    const int k0 = kt * BK;
+    const int k0 = kt * BK, ka = g.a_tiled ? kt * 512 : k0;
 #pragma unroll
     for (int d = 0; d < C::LA; ++d)
-      __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
                                        (lds_void_t*)(sx + (wave * C::LA + d) * 512), 16, 0, 0);
 #pragma unroll
     for (int d = 0; d < C::LB; ++d)
@@ -469,6 +475,8 @@ int num_cus() {
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC, int EPI>
 int launch_cfg(const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.N % BN || g.K % 64) return NOISE_ENOTSUP;
+  // a TILE16 A operand is one tile per 16-row DMA instruction and 32-deep stage
+  if (g.a_tiled && (BK != 32 || Cfg<BM, BN, BK, STAGES, WGM, WGN>::ROWS_PER_DMA != 16)) return NOISE_ENOTSUP;
   const long tiles = (long)((g.M + BM - 1) / BM) * (g.N / BN);
   if (tiles > 0x7fffffffL) return NOISE_ENOTSUP;
   // OCC persistent workgroups per CU, a multiple of 8 for the XCD split
@@ -496,6 +504,9 @@ int lowrank_gemm_parts(int N) {
 }
 
 int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
+  if (g.a_tiled && (epi == EPI_RELU2 || g.M % 16 || g.T % 16 || g.lda % 32 || g.a_mstride != (long)g.T * g.lda))
+    return NOISE_EINVAL;
+  if (g.out_tiled && (epi != EPI_RELU2 || g.M % 16 || g.ldo % 32)) return NOISE_EINVAL;
   if (epi == EPI_DENSE) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.out_bf16 || g.lda % 8 || g.ldw % 8 ||
         g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K || g.ldo % 8 || g.ldo < g.N || g.N % 128 || g.K % 64 ||

@@ -196,9 +196,13 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
       ev_h[i][sub] = h2;
       ev_dot[i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(h2), as_bf16x2(ev_bp[sub]), sub == 0 ? 0.f : ev_dot[i], false);
     } else if (sub == 4) {
+      // row-major: 16 rows x 64 bytes per instruction; TILE16: one contiguous 1 KiB tile (16 rows, the
+      // wave's 32 columns), eight whole 128-byte lines
       const long row = (long)blk_of(pk) * R + lr;
-      *reinterpret_cast<uint4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) =
-          make_uint4(ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]);
+      const int r = lane & 15;
+      bf16* dst = g.out_tiled ? g.out_bf16 + (row - r) * g.ldo + (fw >> 5) * 512 + 8 * (4 * r + (grp ^ ((r >> 1) & 3)))
+                              : g.out_bf16 + row * g.ldo + fw + 8 * grp;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]);
       ev_dot[i] += __shfl_xor(ev_dot[i], 16, 64);
     } else {
       ev_dot[i] += __shfl_xor(ev_dot[i], 32, 64);
@@ -285,6 +289,7 @@ int xs_relu2_parts(int N) { return (N > 0 && N % BN == 0) ? N / BN : 0; }
 
 bool xs_relu2_supported(const LowrankGemmArgs& g) {
   return g.K == KD && g.N % BN == 0 && g.N > 0 && g.M % R == 0 && g.T % R == 0 && g.u_parts == 1 && g.u_ld == 1 &&
+         !g.a_tiled && (!g.out_tiled || g.ldo % 32 == 0) &&
          g.lda % 8 == 0 && g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.ra_ld % 4 == 0 &&
          g.rb_next_ld % 4 == 0;
 }

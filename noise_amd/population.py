@@ -210,7 +210,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
                   0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
-        _lib.call('noise_dense_bf16', _p(buf.y), D, D, _p(W.proj[i]), m, T, _p(buf.y_ap), s)
+        _lib.call('noise_dense_bf16', _p(buf.y), _lib.LAYOUT_ROWS, D, D, _p(W.proj[i]), m, T, _p(buf.y_ap), s)
         tm.close(t0)
         attn_out = (_p(buf.y_ap), _p(buf.u_attn), H, H, 1, _p(ap))
         af, bf_ = noise[pre + 'mlp.c_fc.weight']
@@ -220,9 +220,10 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         _lib.call('noise_norm_dot', _p(buf.x), _p(buf.h), _p(bf_), _p(buf.u_fc), _p(sign), m, T, ps, pend, npend, s)
         tm.close(t0)
         t0 = tm.mark('mlp')
+        # the hidden stays in the library's TILE16 layout between the two MLP GEMMs
         _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
-                  _p(buf.hidden), _p(buf.u_mlp), s)
-        _lib.call('noise_dense_bf16', _p(buf.hidden), F, D, _p(W.mproj[i]), m, T, _p(buf.y_mp), s)
+                  _p(buf.hidden), _lib.LAYOUT_TILE16, _p(buf.u_mlp), s)
+        _lib.call('noise_dense_bf16', _p(buf.hidden), _lib.LAYOUT_TILE16, F, D, _p(W.mproj[i]), m, T, _p(buf.y_mp), s)
         tm.close(t0)
         # the fc partials are part-major with stride m * T (this chunk's rows)
         mlp_out = (_p(buf.y_mp), _p(buf.u_mlp), buf.parts, 1, m * T, _p(am))

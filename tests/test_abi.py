@@ -87,3 +87,22 @@ def test_ops_refuse_cpu_tensors():
     a = torch.zeros(2, 512)
     with pytest.raises(ValueError, match='CUDA'):
         ops.lowrank_linear(x, w, a, a, torch.zeros(2))
+
+
+def test_tile16_layout_is_a_permutation_of_whole_tiles():
+    """The TILE16 offsets are a bijection onto [0, rows * cols) and every 16 x 32 tile fills one contiguous
+    KiB, so a producer's tile store and the GEMM's tile load are each eight whole 128-byte lines."""
+    import torch
+    from tests._util import tile16_index
+    rows, cols = 64, 128
+    idx = tile16_index(rows, cols)
+    assert torch.equal(idx.flatten().sort().values, torch.arange(rows * cols))
+    for g in range(rows // 16):
+        for c in range(cols // 32):
+            t = idx[16 * g:16 * g + 16, 32 * c:32 * c + 32].flatten()
+            assert int(t.min()) % 512 == 0 and int(t.max() - t.min()) == 511
+    # a tile's unit p holds row p // 4 and logical 8-column chunk (p % 4) ^ ((p // 8) % 4): the order of the
+    # GEMM's XOR-swizzled 32-deep LDS stage
+    for p in range(64):
+        r, ch = p // 4, (p % 4) ^ ((p // 8) % 4)
+        assert int(idx[r, 8 * ch]) == 8 * p

@@ -19,7 +19,7 @@ from noise_amd.model import make_model
 from noise_amd.synthetic import antithetic_signs, population_noise, trained_like, zipf_tokens
 from oracle import eggroll as oe
 from oracle import model as om
-from tests._util import log_case, rel_err
+from tests._util import log_case, rel_err, tile16_index
 
 pytestmark = pytest.mark.gpu
 DEV = 'cuda'
@@ -193,6 +193,42 @@ def test_deferred_residuals_match_eager_lowrank():
     assert rel_err(hn.cpu().float(), om.bf(ref_h1)) < 5e-3
     # x itself is not written by the MLP entry
     assert torch.equal(dev['x'].cpu(), x)
+
+def test_mlp_hidden_tile16_matches_rows():
+    """noise_mlp_fc writes the same hidden (bit for bit, up to the layout) and the same partials in TILE16 as in
+    ROWS, and noise_dense_bf16 on the TILE16 hidden returns exactly its result on the row-major one."""
+    g = torch.Generator().manual_seed(13)
+    m, T, D, F = 4, 64, 512, 2048
+    M = m * T
+    h = torch.randn(M, D, generator=g).bfloat16()
+    wfc = (torch.randn(F, D, generator=g) * D ** -0.5).bfloat16()
+    wpj = (torch.randn(D, F, generator=g) * F ** -0.5).bfloat16()
+    afc, bpj = torch.randn(m // 2, F, generator=g), torch.randn(m // 2, F, generator=g)
+    u = torch.randn(M, generator=g)
+    sign = torch.tensor([0.05, -0.05, 0.02, -0.02])
+    d = {k: v.to(DEV) for k, v in dict(h=h, wfc=wfc, wpj=wpj, afc=afc, bpj=bpj, u=u, sign=sign).items()}
+    log_case(f'mlp hidden TILE16 vs ROWS m={m} T={T}')
+    s = torch.cuda.current_stream().cuda_stream
+    parts = _lib.value('noise_mlp_fc_parts', F)
+    out = {}
+    for layout in (_lib.LAYOUT_ROWS, _lib.LAYOUT_TILE16):
+        hid = torch.empty(M, F, device=DEV, dtype=torch.bfloat16)
+        up = torch.empty(parts, M, device=DEV)
+        _lib.call('noise_mlp_fc', d['h'].data_ptr(), d['wfc'].data_ptr(), D, F, d['afc'].data_ptr(), d['u'].data_ptr(),
+                  d['bpj'].data_ptr(), d['sign'].data_ptr(), m, T, 1, hid.data_ptr(), layout, up.data_ptr(), s)
+        y = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_dense_bf16', hid.data_ptr(), layout, F, D, d['wpj'].data_ptr(), m, T, y.data_ptr(), s)
+        torch.cuda.synchronize()
+        out[layout] = (hid.cpu(), up.cpu(), y.cpu())
+    rows_h, rows_u, rows_y = out[_lib.LAYOUT_ROWS]
+    tile_h, tile_u, tile_y = out[_lib.LAYOUT_TILE16]
+    assert torch.equal(tile_h.flatten()[tile16_index(M, F)], rows_h)
+    assert torch.equal(tile_u, rows_u)
+    assert torch.equal(tile_y, rows_y)
+    # and the dense product itself: bf16(hidden W^T) with fp32 accumulation
+    ref = (rows_h.float() @ wpj.float().t()).bfloat16().float()
+    assert rel_err(rows_y.float(), ref) < 5e-3
+
 
 @pytest.mark.parametrize('qk_norm', [0, 1])
 def test_attention_matches_oracle_and_moments(qk_norm):
