@@ -56,3 +56,12 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   if (nblocks % XCDS != 0) return bid;
   return (bid % XCDS) * (nblocks / XCDS) + bid / XCDS;
 }
+
+// 16-byte vector store that streams to memory (non-temporal, system scope: nt sc0 sc1). The line is not kept
+// dirty in L2, so later L2 fills of the same kernel do not wait on its write-back: measured on MI355X, a
+// kernel that streams its operand from HBM while writing 4x as many bytes runs about 10% faster with these
+// stores. Issued from inline assembly; a vmcnt wait the compiler places for its own loads only becomes
+// stricter for it (vector memory operations complete in issue order).
+__device__ __forceinline__ void store_stream_x4(void* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" : : "v"(p), "v"(v) : "memory");
+}

@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
       const int r = lane & 15;
       bf16* dst = g.out_tiled ? g.out_bf16 + (row - r) * g.ldo + (fw >> 5) * 512 + 8 * (4 * r + (grp ^ ((r >> 1) & 3)))
                               : g.out_bf16 + row * g.ldo + fw + 8 * grp;
-      *reinterpret_cast<uint4*>(dst) = make_uint4(ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]);
+      store_stream_x4(dst, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       ev_dot[i] += __shfl_xor(ev_dot[i], 16, 64);
     } else {
       ev_dot[i] += __shfl_xor(ev_dot[i], 32, 64);
