@@ -57,11 +57,20 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return (bid % XCDS) * (nblocks / XCDS) + bid / XCDS;
 }
 
-// 16-byte vector store that streams to memory (non-temporal, system scope: nt sc0 sc1). The line is not kept
-// dirty in L2, so later L2 fills of the same kernel do not wait on its write-back: measured on MI355X, a
-// kernel that streams its operand from HBM while writing 4x as many bytes runs about 10% faster with these
-// stores. Issued from inline assembly; a vmcnt wait the compiler places for its own loads only becomes
-// stricter for it (vector memory operations complete in issue order).
+// 16-byte non-temporal vector store (global_store_dwordx4 ... nt, the encoding the compiler gives
+// __builtin_nontemporal_store on gfx950): the line is marked for early eviction instead of staying dirty in
+// L2, so later L2 fills of the same kernel wait less on write-backs. Measured on MI355X: a kernel that
+// streams its operand from HBM while writing 4x as many bytes runs about 10% faster with these stores.
+// Issued from inline assembly so a 16-byte vector keeps one instruction; a vmcnt wait the compiler places
+// for its own loads only becomes stricter for it (vector memory operations complete in issue order). The
+// trailing s_nop 1 is the hazard wait the compiler would insert itself: a VALU write to the data VGPRs of a
+// preceding store wider than 8 bytes needs 2 wait states on gfx940+, or the store may pick up the new value.
 __device__ __forceinline__ void store_stream_x4(void* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" : : "v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_stream_x4(void* p, unsigned a, unsigned b, unsigned c, unsigned d) {
+  store_stream_x4(p, u32x4{a, b, c, d});
+}
+__device__ __forceinline__ void store_stream_f4(void* p, float a, float b, float c, float d) {
+  store_stream_x4(p, u32x4{__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)});
 }

@@ -301,12 +301,12 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       const int rrow = live ? row : g.M - 1;
       if constexpr (EPI == EPI_DENSE) {
         if (live) {
-          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+          bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
           for (int e = 0; e < CW; e += 8)
-            o[e / 8] = make_uint4(pack_bf16(acc[i][e / 4][0], acc[i][e / 4][1]), pack_bf16(acc[i][e / 4][2], acc[i][e / 4][3]),
-                                  pack_bf16(acc[i][e / 4 + 1][0], acc[i][e / 4 + 1][1]),
-                                  pack_bf16(acc[i][e / 4 + 1][2], acc[i][e / 4 + 1][3]));
+            store_stream_x4(o + e, pack_bf16(acc[i][e / 4][0], acc[i][e / 4][1]), pack_bf16(acc[i][e / 4][2], acc[i][e / 4][3]),
+                            pack_bf16(acc[i][e / 4 + 1][0], acc[i][e / 4 + 1][1]),
+                            pack_bf16(acc[i][e / 4 + 1][2], acc[i][e / 4 + 1][3]));
         }
         continue;
       }
@@ -336,16 +336,16 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       if constexpr (EPI == EPI_STORE) {
         if (live) {
           if (g.out_f32) {
-            float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb);
+            float* o = g.out_f32 + (long)row * g.ldo + cb;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) o[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            for (int j = 0; j < FN; ++j) store_stream_f4(o + 4 * j, v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
           }
           if (g.out_bf16) {
-            uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+            bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
-                                    pack_bf16(v[e + 6], v[e + 7]));
+              store_stream_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
+                              pack_bf16(v[e + 6], v[e + 7]));
           }
         }
       } else if constexpr (EPI == EPI_RESID) {
@@ -396,19 +396,19 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           for (int e = 0; e < CW; ++e) v[e] += gt * (wr[e] + sa * br[e]);
         }
         if (live) {
-          uint4* o = reinterpret_cast<uint4*>(g.out_bf16 + (long)row * g.ldo + cb);
+          bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
           if (seg < 2) {
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              o[e / 8] = make_uint4(pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
-                                    pack_bf16(v[e + 4], v[e + 5]), pack_bf16(v[e + 6], v[e + 7]));
+              store_stream_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
+                              pack_bf16(v[e + 4], v[e + 5]), pack_bf16(v[e + 6], v[e + 7]));
           } else {
             // v: the bf16-rounded value (the autocast rounding point) stored as fp16, which holds it exactly, so
             // attention can feed it to fp16 MFMAs straight from memory
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              o[e / 8] = make_uint4(pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
-                                    pack_f16_of_bf16(v[e + 4], v[e + 5]), pack_f16_of_bf16(v[e + 6], v[e + 7]));
+              store_stream_x4(o + e, pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
+                              pack_f16_of_bf16(v[e + 4], v[e + 5]), pack_f16_of_bf16(v[e + 6], v[e + 7]));
           }
         }
       } else {  // EPI_CE

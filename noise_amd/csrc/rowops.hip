@@ -24,14 +24,14 @@ __device__ __forceinline__ Row8 load8(const float* p) {
   return Row8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
 }
 __device__ __forceinline__ void store8(float* p, const Row8& r) {
-  *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
-  *reinterpret_cast<float4*>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
+  store_stream_f4(p, r.v[0], r.v[1], r.v[2], r.v[3]);
+  store_stream_f4(p + 4, r.v[4], r.v[5], r.v[6], r.v[7]);
 }
 __device__ __forceinline__ void store8_bf16(bf16* p, const Row8& r) {
   bf16x8 o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = to_bf16(r.v[e]);
-  *reinterpret_cast<bf16x8*>(p) = o;
+  store_stream_x4(p, __builtin_bit_cast(u32x4, o));
 }
 // RMSNorm of a 512-wide row spread 8 per lane over one wave: x * rsqrt(mean(x^2) + eps), fp32.
 __device__ __forceinline__ void rms_norm_row(Row8& r) {
