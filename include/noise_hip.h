@@ -206,6 +206,21 @@ int noise_fitness(const float* losses, int n, int pairs, int mode, float* fitnes
 int noise_outer_update(const float* a, long a_ld, const float* b, long b_ld, const float* w, int ndir, int out,
                        int in, float scale, float* grad, noise_stream_t stream);
 
+/* noise_outer_update for n matrices in one launch (every perturbed parameter of the model shares the
+ * direction weights w and ndir): mats is a host array, read before the call returns. Same arithmetic per
+ * matrix; replaces the per-parameter loop of train/val/eggroll.py:155-166. */
+typedef struct noise_outer_mat {
+  const float* a; /* [ndir, a_ld] or null (out == 1) */
+  long a_ld;
+  const float* b; /* [ndir, b_ld] */
+  long b_ld;
+  int out;
+  int in;
+  float* grad; /* [out, in] */
+} noise_outer_mat_t;
+int noise_outer_update_batch(const noise_outer_mat_t* mats, int n, const float* w, int ndir, float scale,
+                             noise_stream_t stream);
+
 /* One torch.optim.AdamW step with weight_decay 0 on n fp32 values (train/val/eggroll.py:205, :167):
  * step_size = lr / (1 - beta1^t), bc2_sqrt = sqrt(1 - beta2^t). */
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,

@@ -42,9 +42,21 @@ SIGNATURES = {
     'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P, I, P],
     'noise_fitness': [P, I, I, I, P, P, P],
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
+    'noise_outer_update_batch': [P, I, P, I, F, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
 
+
+
+class OuterMat(ctypes.Structure):
+    """noise_outer_mat_t of include/noise_hip.h (one matrix of a batched EGGROLL update)."""
+    _fields_ = [('a', P), ('a_ld', L), ('b', P), ('b_ld', L), ('out', I), ('in_', I), ('grad', P)]
+
+
+def outer_mats(items):
+    """(a ptr or 0, a_ld, b ptr, b_ld, out, in, grad ptr) tuples -> (pointer to a host array, count)."""
+    arr = (OuterMat * len(items))(*[OuterMat(*it) for it in items])
+    return ctypes.cast(arr, P), len(items), arr
 
 
 class Pending(ctypes.Structure):

@@ -1,4 +1,6 @@
 // extern "C" entry points of libnoise_hip.so (declared in include/noise_hip.h).
+#include <vector>
+
 #include "../../include/noise_hip.h"
 #include "attention.h"
 #include "common.h"
@@ -367,8 +369,16 @@ int noise_fitness(const float* losses, int n, int pairs, int mode, float* fitnes
 
 int noise_outer_update(const float* a, long a_ld, const float* b, long b_ld, const float* w, int ndir, int out,
                        int in, float scale, float* grad, noise_stream_t stream) {
-  OuterUpdateArgs g{a, a_ld, b, b_ld, w, ndir, out, in, scale, grad};
-  return outer_update_launch(g, static_cast<hipStream_t>(stream));
+  const OuterUpdateArgs u{a, a_ld, b, b_ld, out, in, grad};
+  return outer_update_launch(&u, 1, w, ndir, scale, static_cast<hipStream_t>(stream));
+}
+
+int noise_outer_update_batch(const noise_outer_mat_t* mats, int n, const float* w, int ndir, float scale,
+                             noise_stream_t stream) {
+  if (n <= 0 || !mats) return NOISE_EINVAL;
+  std::vector<OuterUpdateArgs> u(n);
+  for (int k = 0; k < n; ++k) u[k] = OuterUpdateArgs{mats[k].a, mats[k].a_ld, mats[k].b, mats[k].b_ld, mats[k].out, mats[k].in, mats[k].grad};
+  return outer_update_launch(u.data(), n, w, ndir, scale, static_cast<hipStream_t>(stream));
 }
 
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,

@@ -5,15 +5,32 @@
 #define NOISE_FITNESS_ZSCORE 0
 #define NOISE_FITNESS_RANK 1
 
+// One matrix of an update: grad [out, in] = scale * sum_j (w_j a_j[o]) b_j[i].
 struct OuterUpdateArgs {
   const float* a;  // [ndir, a_ld] output-side vectors (null: scalar 1, out must be 1)
   long a_ld;
   const float* b;  // [ndir, b_ld] input-side vectors
   long b_ld;
-  const float* w;  // [ndir] direction weights
-  int ndir, out, in;
-  float scale;
+  int out, in;
   float* grad;     // [out, in]
+};
+
+// Kernel-side form: up to OUTER_MAX matrices per launch, passed by value (under the 4 KiB argument limit),
+// with the running total of 64 x 64 tiles.
+constexpr int OUTER_MAX = 56;
+struct OuterMat {
+  const float* a;
+  const float* b;
+  float* grad;
+  long a_ld, b_ld;
+  int out, in, tiles_i, tile_end;
+};
+struct OuterBatchArgs {
+  OuterMat m[OUTER_MAX];
+  int n;
+  const float* w;  // [ndir] direction weights, shared by every matrix
+  int ndir;
+  float scale;
 };
 
 struct AdamArgs {
@@ -28,5 +45,5 @@ struct AdamArgs {
 };
 
 int fitness_launch(const float* losses, int n, int pairs, int mode, float* fit, float* weight, hipStream_t s);
-int outer_update_launch(const OuterUpdateArgs& g, hipStream_t s);
+int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int ndir, float scale, hipStream_t s);
 int adam_launch(const AdamArgs& g, hipStream_t s);

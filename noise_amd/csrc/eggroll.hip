@@ -3,6 +3,8 @@
 //
 // Reference: Eggroll.step (train/val/eggroll.py:151-167) and torch.optim.AdamW(lr, betas=(0.5, 0.95),
 // eps=1e-8, weight_decay=0) (:205). All fp32.
+#include <algorithm>
+
 #include "common.h"
 #include "eggroll.h"
 
@@ -64,49 +66,91 @@ __global__ void __launch_bounds__(1024) fitness_kernel(const float* __restrict__
   }
 }
 
-// G[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions (a null: a_j[o] = 1, out = 1),
-// on the fp32 MFMA (v_mfma_f32_16x16x4_f32): a 64 x 64 output tile per workgroup of 4 waves (32 x 32
-// each), directions staged through LDS 32 at a time with w_j folded into the a rows.
-__global__ void __launch_bounds__(256) outer_update_kernel(OuterUpdateArgs g) {
-  constexpr int TK = 32;
-  __shared__ float sa[TK][64 + 4];
-  __shared__ float sb[TK][64 + 4];
+// G[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions (a null: a_j[o] = 1, out = 1), for up
+// to OUTER_MAX matrices in one launch (every perturbed parameter of the model: ~9k 64 x 64 tiles fill the
+// GPU, where one 512 x 512 matrix alone is 64 workgroups). On the fp32 MFMA (v_mfma_f32_16x16x4_f32): a
+// 64 x 64 output tile per workgroup of 4 waves (32 x 32 each); directions pass through a double-buffered
+// LDS stage 32 at a time with w_j folded into the a rows, the next 32 loaded into registers while the
+// current ones feed the MFMAs.
+__global__ void __launch_bounds__(256) outer_update_kernel(const OuterBatchArgs g) {
+  constexpr int TK = 32, LD = 64 + 4;
+  __shared__ __attribute__((aligned(16))) float sa[2][TK][LD];
+  __shared__ __attribute__((aligned(16))) float sb[2][TK][LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
+  // this workgroup's matrix and tile (uniform scan over the prefix sums of tile counts)
+  const int t = blockIdx.x;
+  int mi = 0;
+  while (mi + 1 < g.n && t >= g.m[mi].tile_end) ++mi;
+  const OuterMat& M = g.m[mi];
+  const int lt = t - (mi ? g.m[mi - 1].tile_end : 0);
+  const int o0 = (lt / M.tiles_i) * 64, i0 = (lt % M.tiles_i) * 64;
+  // loader: thread tid fills direction jj = tid / 8 (of 32), columns 8 (tid % 8) .. + 7 of a and of b
+  const int ljj = tid >> 3, lc = 8 * (tid & 7);
+  const bool a_full = M.a && o0 + 64 <= M.out && M.a_ld % 4 == 0, b_full = i0 + 64 <= M.in && M.b_ld % 4 == 0;
+  float ra[8], rb[8];
+  auto load = [&](int j0) {
+    const int j = j0 + ljj;
+    const bool live = j < g.ndir;
+    const float wj = live ? g.w[j] : 0.f;
+    if (live && a_full) {
+      const float4 x0 = *reinterpret_cast<const float4*>(M.a + (long)j * M.a_ld + o0 + lc);
+      const float4 x1 = *reinterpret_cast<const float4*>(M.a + (long)j * M.a_ld + o0 + lc + 4);
+      ra[0] = x0.x, ra[1] = x0.y, ra[2] = x0.z, ra[3] = x0.w, ra[4] = x1.x, ra[5] = x1.y, ra[6] = x1.z, ra[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        ra[e] = live && o0 + lc + e < M.out ? (M.a ? M.a[(long)j * M.a_ld + o0 + lc + e] : 1.f) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ra[e] *= wj;
+    if (live && b_full) {
+      const float4 x0 = *reinterpret_cast<const float4*>(M.b + (long)j * M.b_ld + i0 + lc);
+      const float4 x1 = *reinterpret_cast<const float4*>(M.b + (long)j * M.b_ld + i0 + lc + 4);
+      rb[0] = x0.x, rb[1] = x0.y, rb[2] = x0.z, rb[3] = x0.w, rb[4] = x1.x, rb[5] = x1.y, rb[6] = x1.z, rb[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rb[e] = live && i0 + lc + e < M.in ? M.b[(long)j * M.b_ld + i0 + lc + e] : 0.f;
+    }
+  };
+  auto stage = [&](int buf) {
+    *reinterpret_cast<float4*>(&sa[buf][ljj][lc]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
+    *reinterpret_cast<float4*>(&sa[buf][ljj][lc + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
+    *reinterpret_cast<float4*>(&sb[buf][ljj][lc]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
+    *reinterpret_cast<float4*>(&sb[buf][ljj][lc + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
+  };
   f32x4 acc[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  stage(0);
+  __syncthreads();
+  int buf = 0;
   for (int j0 = 0; j0 < g.ndir; j0 += TK) {
-#pragma unroll
-    for (int s = 0; s < TK * 64 / 256; ++s) {
-      const int e = tid + s * 256, jj = e >> 6, c = e & 63, j = j0 + jj;
-      float av = 0.f, bv = 0.f;
-      if (j < g.ndir) {
-        if (o0 + c < g.out) av = g.w[j] * (g.a ? g.a[(long)j * g.a_ld + o0 + c] : 1.f);
-        if (i0 + c < g.in) bv = g.b[(long)j * g.b_ld + i0 + c];
-      }
-      sa[jj][c] = av;
-      sb[jj][c] = bv;
-    }
-    __syncthreads();
+    const bool more = j0 + TK < g.ndir;
+    if (more) load(j0 + TK);  // in flight during this chunk's MFMAs
 #pragma unroll
     for (int ks = 0; ks < TK / 4; ++ks) {
       const int jj = 4 * ks + (lane >> 4);
       float af[2], bf[2];
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        af[f] = sa[jj][wm * 32 + 16 * f + (lane & 15)];
-        bf[f] = sb[jj][wn * 32 + 16 * f + (lane & 15)];
+        af[f] = sa[buf][jj][wm * 32 + 16 * f + (lane & 15)];
+        bf[f] = sb[buf][jj][wn * 32 + 16 * f + (lane & 15)];
       }
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
     }
-    __syncthreads();
+    if (more) {
+      // the other buffer was last read in the previous chunk, before the barrier that ended it
+      stage(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
   }
   // lane holds C[row = 4 (lane / 16) + e][col = lane % 16] of each 16 x 16 block
 #pragma unroll
@@ -116,7 +160,7 @@ __global__ void __launch_bounds__(256) outer_update_kernel(OuterUpdateArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int o = o0 + wm * 32 + 16 * a + 4 * (lane >> 4) + e, i = i0 + wn * 32 + 16 * b + (lane & 15);
-        if (o < g.out && i < g.in) g.grad[(long)o * g.in + i] = g.scale * acc[a][b][e];
+        if (o < M.out && i < M.in) M.grad[(long)o * M.in + i] = g.scale * acc[a][b][e];
       }
 }
 
@@ -147,12 +191,30 @@ int fitness_launch(const float* losses, int n, int pairs, int mode, float* fit, 
   return NOISE_OK;
 }
 
-int outer_update_launch(const OuterUpdateArgs& g, hipStream_t s) {
-  if (!g.b || !g.w || !g.grad || g.ndir <= 0 || g.out <= 0 || g.in <= 0 || (!g.a && g.out != 1) ||
-      g.b_ld < g.in || (g.a && g.a_ld < g.out))
-    return NOISE_EINVAL;
-  hipLaunchKernelGGL(outer_update_kernel, dim3((g.in + 63) / 64, (g.out + 63) / 64), dim3(256), 0, s, g);
-  NOISE_CHECK_LAUNCH();
+int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int ndir, float scale, hipStream_t s) {
+  if (n <= 0 || !mats || !w || ndir <= 0) return NOISE_EINVAL;
+  for (int base = 0; base < n; base += OUTER_MAX) {
+    OuterBatchArgs g{};
+    g.n = std::min(OUTER_MAX, n - base);
+    g.w = w;
+    g.ndir = ndir;
+    g.scale = scale;
+    long tiles = 0;
+    for (int k = 0; k < g.n; ++k) {
+      const OuterUpdateArgs& u = mats[base + k];
+      if (!u.b || !u.grad || u.out <= 0 || u.in <= 0 || (!u.a && u.out != 1) || u.b_ld < u.in ||
+          (u.a && u.a_ld < u.out))
+        return NOISE_EINVAL;
+      OuterMat& m = g.m[k];
+      m.a = u.a, m.b = u.b, m.grad = u.grad, m.a_ld = u.a_ld, m.b_ld = u.b_ld, m.out = u.out, m.in = u.in;
+      m.tiles_i = (u.in + 63) / 64;
+      tiles += (long)((u.out + 63) / 64) * m.tiles_i;
+      if (tiles > 0x7fffffffL) return NOISE_ENOTSUP;
+      m.tile_end = (int)tiles;
+    }
+    hipLaunchKernelGGL(outer_update_kernel, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+  }
   return NOISE_OK;
 }
 

@@ -98,17 +98,22 @@ class Eggroll:
             d1 = min(pairs, d0 + (CHUNK if pairs > 8 * CHUNK else pairs))
             dirs = torch.arange(d0, d1, device=self.device)
             w = weight[d0:d1].contiguous()
-            for name, n in self.noise(offsets, dirs).items():
+            noise = self.noise(offsets, dirs)
+            tmps, mats = {}, []
+            for name, n in noise.items():
                 p = self.params[name]
-                tmp = grads[name] if d0 == 0 else torch.empty_like(p)
+                tmps[name] = tmp = grads[name] if d0 == 0 else torch.empty_like(p)
                 if isinstance(n, tuple):
                     a, b = n
-                    _lib.call('noise_outer_update', a.data_ptr(), a.shape[1], b.data_ptr(), b.shape[1], w.data_ptr(),
-                              d1 - d0, p.shape[0], p.shape[1], -1.0 / nfit, tmp.data_ptr(), s)
+                    mats.append((a.data_ptr(), a.shape[1], b.data_ptr(), b.shape[1], p.shape[0], p.shape[1],
+                                 tmp.data_ptr()))
                 else:
-                    _lib.call('noise_outer_update', 0, 0, n.data_ptr(), n.shape[1], w.data_ptr(), d1 - d0, 1,
-                              p.shape[0], -1.0 / nfit, tmp.data_ptr(), s)
-                if d0 != 0:
+                    mats.append((0, 0, n.data_ptr(), n.shape[1], 1, p.shape[0], tmp.data_ptr()))
+            # every parameter's outer-product sum in one launch
+            ptr, count, _keep = _lib.outer_mats(mats)
+            _lib.call('noise_outer_update_batch', ptr, count, w.data_ptr(), d1 - d0, -1.0 / nfit, s)
+            if d0 != 0:
+                for name, tmp in tmps.items():
                     grads[name] += tmp
         optimizer.zero_grad(set_to_none=True)
         for name, p in self.params.items():

@@ -510,6 +510,36 @@ def test_fitness_update_adam_match_oracle():
     assert torch.allclose(grad.cpu(), ref['m'], atol=1e-5)
     assert torch.allclose(gl.cpu()[0], ref['l'], atol=1e-6)
 
+    log_case('outer_update_batch')
+    # several matrices in one launch, including partial 64 x 64 tiles, a multi-chunk direction count and the
+    # scalar (a null) form: each equals the single-matrix result bit for bit and the oracle's update
+    nd = 75
+    wb = torch.randn(nd, generator=g)
+    shapes = [(70, 130), (64, 64), (1, 8), (200, 33), (512, 512)]
+    host = {}
+    for k, (o, i) in enumerate(shapes):
+        host[k] = (None if o == 1 else torch.randn(nd, o, generator=g), torch.randn(nd, i, generator=g))
+    dev_ = {k: (None if a_ is None else a_.to(DEV), b_.to(DEV)) for k, (a_, b_) in host.items()}
+    wbd = wb.to(DEV)
+    grads_b = {k: torch.empty(o, i, device=DEV) for k, (o, i) in enumerate(shapes)}
+    grads_s = {k: torch.empty(o, i, device=DEV) for k, (o, i) in enumerate(shapes)}
+    mats = []
+    for k, (o, i) in enumerate(shapes):
+        a_, b_ = dev_[k]
+        mats.append((0 if a_ is None else a_.data_ptr(), 0 if a_ is None else o, b_.data_ptr(), i, o, i,
+                     grads_b[k].data_ptr()))
+        _lib.call('noise_outer_update', 0 if a_ is None else a_.data_ptr(), 0 if a_ is None else o, b_.data_ptr(), i,
+                  wbd.data_ptr(), nd, o, i, -0.5, grads_s[k].data_ptr(), s)
+    ptr, count, _keep = _lib.outer_mats(mats)
+    _lib.call('noise_outer_update_batch', ptr, count, wbd.data_ptr(), nd, -0.5, s)
+    torch.cuda.synchronize()
+    for k, (o, i) in enumerate(shapes):
+        assert torch.equal(grads_b[k].cpu(), grads_s[k].cpu())
+        a_, b_ = host[k]
+        ref_k = oe.update(wb, {'m': (a_, b_) if a_ is not None else b_}, 2)['m']
+        ref_k = ref_k.reshape(o, i)
+        assert torch.allclose(grads_b[k].cpu(), ref_k, atol=1e-4, rtol=1e-5), k
+
     log_case('adam')
     p0 = torch.randn(1000, generator=g)
     param, m_, v_ = p0.clone().to(DEV), torch.zeros(1000, device=DEV), torch.zeros(1000, device=DEV)
