@@ -89,3 +89,6 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream);
 int xs_relu2_parts(int N);
 bool xs_relu2_supported(const LowrankGemmArgs& g);
 int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream);
+// The same weight-resident kernel for the dense c_proj product y = bf16(x W^T) at K = 512 (row-major A and y).
+bool xs_dense_supported(const LowrankGemmArgs& g);
+int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream);

@@ -512,6 +512,8 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
         g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K || g.ldo % 8 || g.ldo < g.N || g.N % 128 || g.K % 64 ||
         (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15))
       return NOISE_EINVAL;
+    // K = 512 (the attention c_proj): the weight-resident kernel streams x once per 256 output columns
+    if (xs_dense_supported(g)) return xs_dense_launch(g, stream);
     return launch_epi<EPI_DENSE>(g, stream);
   }
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||

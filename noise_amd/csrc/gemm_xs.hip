@@ -56,7 +56,9 @@ constexpr int XROW = KD * 2 + 16;     // LDS bytes per x row (1 KiB + 16: bank-g
 constexpr int XBYTES = R * XROW;      // LDS bytes of one x block
 constexpr int VEC = 512;              // per-wave vector area: a (128 B) | b_next (128 B) | u (128 B) | .. | sign
 constexpr int SIGN_OFF = VEC - 8;
-constexpr int DMA_PER_BLOCK = 6;      // per wave and block: 4 x fragments, a|b_next|u, sign
+// per wave and block: 4 x rows, then (relu^2 mode) a|b_next|u and the sign
+template <bool DENSE>
+constexpr int DMA_PER_BLOCK = DENSE ? 4 : 6;
 constexpr int STORES_PER_EPI = 2;     // lower bound on an epilogue's store instructions (two h rows)
 
 template <int N>
@@ -89,7 +91,9 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
 }
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned v) { return *reinterpret_cast<bf16x2*>(&v); }
 
-__global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs g) {
+// DENSE: the c_proj dense product y = bf16(x W^T) only (no rank-1 term, no vectors, no partial dots), row-major.
+template <bool DENSE>
+__global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   __shared__ __attribute__((aligned(16))) char smem[NBUF * XBYTES];
   __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
   __shared__ __attribute__((aligned(16))) float red[2][R][NW];
@@ -137,14 +141,16 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
     const float* vsrc = lane < 8 ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
                         : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
                                     : g.u + row0 + 4 * (lane - 16);
-    if (lane < 24) dma_x4(vsrc, &svec[buf][wave][0]);
-    if (lane == 0) dma_x1(g.sign + p, &svec[buf][wave][SIGN_OFF]);
+    if constexpr (!DENSE) {
+      if (lane < 24) dma_x4(vsrc, &svec[buf][wave][0]);
+      if (lane == 0) dma_x1(g.sign + p, &svec[buf][wave][SIGN_OFF]);
+    }
   };
 
   // Block k has landed for this wave once at most nd * DMA_PER_BLOCK + ne * STORES_PER_EPI later operations
   // are outstanding: the nd later load groups and the stores of the ne epilogues issued since.
   auto wait_block = [&](int nd, int ne) {
-    constexpr int D = DMA_PER_BLOCK, S = STORES_PER_EPI;
+    constexpr int D = DMA_PER_BLOCK<DENSE>, S = STORES_PER_EPI;
     switch (nd * 3 + ne) {
       case 0: wait_vm_lgkm0<0>(); break;
       case 1: wait_vm_lgkm0<S>(); break;
@@ -167,6 +173,19 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
   //   6 / 12: second shuffle and the wave partial into LDS.
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
+    if constexpr (DENSE) {
+      // stages 1-4 / 7-10: bf16 pairs of row half 0 / 1; 5 / 11: the row half's store
+      if (st == 0 || st > 11 || st == 6) return;
+      const int i = st < 7 ? 0 : 1, sub = st - (i ? 7 : 1);
+      if (sub < 4) {
+        const int j = sub >> 1, e0 = (sub & 1) * 2;
+        ev_h[i][sub] = pack_bf16(acc[i][j][e0], acc[i][j][e0 + 1]);
+      } else {
+        const long row = (long)blk_of(pk) * R + 16 * i + (lane & 15);
+        store_stream_x4(g.out_bf16 + row * g.ldo + fw + 8 * grp, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+      }
+      return;
+    }
     if (st == 0) {
       const float4 a0 = *reinterpret_cast<const float4*>(vw + 32 * grp);
       const float4 a1 = *reinterpret_cast<const float4*>(vw + 32 * grp + 16);
@@ -248,7 +267,9 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma16x16x32(wr[j][s], xc[i], acc[i][j]);
       if (epi) epi_stage(prev, k - 1, pbuf, s);
-      if (s == 13 && sum) sum_partials(k - 2);
+      if constexpr (!DENSE) {
+        if (s == 13 && sum) sum_partials(k - 2);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (k + NBUF - 1 < nb) issue(k + NBUF - 1);
@@ -272,42 +293,61 @@ __global__ void __launch_bounds__(512, 2) xs_relu2_kernel(const LowrankGemmArgs 
   }
   wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
-  if (last >= 1) sum_partials(last - 1);
+  if constexpr (!DENSE) {
+    if (last >= 1) sum_partials(last - 1);
+  }
 #pragma unroll
   for (int st = 0; st < KS; ++st) {
     if (last == k) epi_stage(accB, last, last % NBUF, st);
     else epi_stage(accA, last, last % NBUF, st);
   }
-  wait_vm_lgkm0<0>();
-  __builtin_amdgcn_s_barrier();
-  sum_partials(last);
+  if constexpr (!DENSE) {
+    wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    sum_partials(last);
+  }
 }
 
 }  // namespace
 
 int xs_relu2_parts(int N) { return (N > 0 && N % BN == 0) ? N / BN : 0; }
 
-bool xs_relu2_supported(const LowrankGemmArgs& g) {
-  return g.K == KD && g.N % BN == 0 && g.N > 0 && g.M % R == 0 && g.T % R == 0 && g.u_parts == 1 && g.u_ld == 1 &&
-         !g.a_tiled && (!g.out_tiled || g.ldo % 32 == 0) &&
-         g.lda % 8 == 0 && g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.ra_ld % 4 == 0 &&
-         g.rb_next_ld % 4 == 0;
+namespace {
+bool xs_shape_ok(const LowrankGemmArgs& g) {
+  return g.K == KD && g.N % BN == 0 && g.N > 0 && g.M % R == 0 && g.T % R == 0 && !g.a_tiled && g.lda % 8 == 0 &&
+         g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.lda >= g.K && g.ldw >= g.K && g.ldo >= g.N &&
+         g.A && g.W && g.out_bf16 && !(((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15);
 }
-
-int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream) {
-  if (!xs_relu2_supported(g) || !g.A || !g.W || !g.sign || !g.u || !g.ra[0] || !g.rb_next || !g.out_bf16 ||
-      !g.upart_out || g.pair_shift < 0 || g.pair_shift > 1 || g.lda < g.K || g.ldw < g.K || g.ldo < g.N)
-    return NOISE_EINVAL;
-  if (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16 | (uintptr_t)g.ra[0] | (uintptr_t)g.rb_next |
-       (uintptr_t)g.u) & 15)
-    return NOISE_EINVAL;
+template <bool DENSE>
+int xs_launch(const LowrankGemmArgs& g, hipStream_t stream) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
     cus = 256;
   const int nslices = g.N / BN, per_xcd = std::max(1, cus / 8);
   const int streams = std::max(1, per_xcd / nslices);
-  hipLaunchKernelGGL(xs_relu2_kernel, dim3(8 * streams * nslices), dim3(512), 0, stream, g);
+  hipLaunchKernelGGL((xs_kernel<DENSE>), dim3(8 * streams * nslices), dim3(512), 0, stream, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
+}
+}  // namespace
+
+bool xs_relu2_supported(const LowrankGemmArgs& g) {
+  return xs_shape_ok(g) && g.u_parts == 1 && g.u_ld == 1 && (!g.out_tiled || g.ldo % 32 == 0) && g.ra_ld % 4 == 0 &&
+         g.rb_next_ld % 4 == 0;
+}
+
+int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_relu2_supported(g) || !g.sign || !g.u || !g.ra[0] || !g.rb_next || !g.upart_out || g.pair_shift < 0 ||
+      g.pair_shift > 1)
+    return NOISE_EINVAL;
+  if (((uintptr_t)g.ra[0] | (uintptr_t)g.rb_next | (uintptr_t)g.u) & 15) return NOISE_EINVAL;
+  return xs_launch<false>(g, stream);
+}
+
+bool xs_dense_supported(const LowrankGemmArgs& g) { return xs_shape_ok(g) && !g.out_tiled; }
+
+int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_dense_supported(g)) return NOISE_EINVAL;
+  return xs_launch<true>(g, stream);
 }

@@ -228,6 +228,17 @@ def test_mlp_hidden_tile16_matches_rows():
     # and the dense product itself: bf16(hidden W^T) with fp32 accumulation
     ref = (rows_h.float() @ wpj.float().t()).bfloat16().float()
     assert rel_err(rows_y.float(), ref) < 5e-3
+    # K = 512 (the attention c_proj shape: the weight-resident kernel) against the same reference
+    log_case(f'dense K=512 m={m} T={T}')
+    wap = (torch.randn(D, D, generator=g) * D ** -0.5).bfloat16()
+    ya = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_dense_bf16', d['h'].data_ptr(), _lib.LAYOUT_ROWS, D, D, wap.to(DEV).data_ptr(), m, T,
+              ya.data_ptr(), s)
+    torch.cuda.synchronize()
+    refa = (h.float() @ wap.float().t()).bfloat16().float()
+    assert rel_err(ya.cpu().float(), refa) < 5e-3
+    # one bf16 ulp at most: only the fp32 summation order differs
+    assert ((ya.cpu().float() - refa).abs() <= refa.abs() * 2 ** -7 + 1e-6).all()
 
 
 @pytest.mark.parametrize('qk_norm', [0, 1])
