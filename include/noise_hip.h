@@ -107,7 +107,8 @@ int noise_embed_norm(const float* w, long vocab, const float* a, const float* b,
 
 /* Block entry: x_out = (lambda_r + s eps_r[dir]) x_in + (lambda_0 + s eps_0[dir]) x0; h = bf16(norm(x_out));
  * lambda_r / lambda_0 point at this block's entries of resid_lambdas / x0_lambdas (device memory);
- * u_qkv[row, 0..2] = bf16(h . bf16(b_{q,k,v}[dir])) (row stride 4); when gate_w is not null the value
+ * u_qkv[row, 0..2] = bf16(h . bf16(b_{q,k,v}[dir])), u_qkv[row, 3] = sign[member] (row stride 4: the row
+ * noise_qkv reads); when gate_w is not null the value
  * gate gate[row, 0..7] = 2 sigmoid(lowrank(h[:32], gate_w, gate_a, gate_b)).
  * Replaces train/val/eggroll.py:76-84, :88. eps_r / eps_0 point at this block's column of the
  * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. The npend (<= 2) deferred
@@ -126,6 +127,7 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
  * bf16-rounded value stored as fp16 (exact), the operand format of noise_attention.
  *   w_qkv    bf16 [1536, 512] = c_q ; c_k ; c_v
  *   rot_cos / rot_sin  bf16 [>= T, 32] (utils/model.py:177-183) */
+/*   u_qkv    [members*T, 4] as noise_block_entry writes it (dots with b_q, b_k, b_v; the member's sign) */
 int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
               const float* u_qkv, const float* sign, int members, int T, int pair_shift, const void* rot_cos,
               const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,

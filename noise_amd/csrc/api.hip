@@ -219,7 +219,21 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
   g.ve_b = ve_b;
   g.ve_v = vocab;
   g.idx = idx;
-  return lowrank_gemm_launch(EPI_QKV, g, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // q | k on the weight-resident kernel (rotary and the head RMSNorm in its epilogue), v (with the value
+  // embedding) on the tile GEMM; both read the same h
+  LowrankGemmArgs gqk = g;
+  gqk.N = 2 * DM;
+  if (xs_qk_supported(gqk)) {
+    if (int rc = xs_qk_launch(gqk, s)) return rc;
+    LowrankGemmArgs gv = g;
+    gv.N = DM;
+    gv.seg0 = 2;
+    gv.W = g.W + (long)2 * DM * DM;
+    gv.out_bf16 = g.out_bf16 + 2 * DM;
+    return lowrank_gemm_launch(EPI_QKV, gv, s);
+  }
+  return lowrank_gemm_launch(EPI_QKV, g, s);
 }
 
 int noise_attention_workspace_size(int members, int T, size_t* bytes) {

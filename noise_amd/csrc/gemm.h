@@ -45,6 +45,7 @@ struct LowrankGemmArgs {
   // ra[n / seg_n][dir(p) * ra_ld + n % seg_n]. One segment unless EPI_QKV.
   const float* ra[3];
   int seg_n;
+  int seg0;           // EPI_QKV: index of the first segment this launch covers (2: v only)
   long ra_ld;
   // Input-side dots x.b, as u_parts partial sums: row r, segment s: sum_q u[r * u_ld + (s * u_parts + q) * u_qstride]
   // (u_qstride = 1: row-major partials; u_ld = 1, u_qstride = rows: part-major).
@@ -92,3 +93,7 @@ int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream);
 // The same weight-resident kernel for the dense c_proj product y = bf16(x W^T) at K = 512 (row-major A and y).
 bool xs_dense_supported(const LowrankGemmArgs& g);
 int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream);
+// ... and for q | k (N = 1024 = c_q ; c_k): rank-1 term, rotary and the per-head RMSNorm in the epilogue.
+// u rows [M, 4] = the bf16 dots with b_q, b_k, b_v and the member's sign; ra[0] / ra[1] = a_q / a_k.
+bool xs_qk_supported(const LowrankGemmArgs& g);
+int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream);

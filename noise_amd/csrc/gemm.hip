@@ -177,7 +177,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto prefetch_ep = [&](int m0, int n0) {
     if constexpr (EPI == EPI_DENSE) return;
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
-    const int dir = pfirst >> g.pair_shift, seg = n0 / g.seg_n, ncol = n0 - seg * g.seg_n;
+    const int dir = pfirst >> g.pair_shift, sl = n0 / g.seg_n, seg = g.seg0 + sl, ncol = n0 - sl * g.seg_n;
     if (tid < BN / 4) pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
     if (tid == 0) pre_sign = pfirst == plast ? g.sign[pfirst] : 0.f;
     const int row = min(m0 + tid % BM, g.M - 1), grp = tid / BM;
@@ -291,7 +291,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     // ---- epilogue. Lane holds, for token row m0 + wm*WM + i*16 + (lane & 15), the output columns
     // cb .. cb + CW - 1 with cb = n0 + wn*WN + (lane >> 4) * CW; acc[i][j][e] is column cb + 4j + e.
     const int lcol = wn * WN + (lane >> 4) * CW, cb = n0 + lcol;
-    const int seg = n0 / g.seg_n, scol = cb - seg * g.seg_n;  // column inside the segment
+    const int sl = n0 / g.seg_n, seg = g.seg0 + sl, scol = cb - sl * g.seg_n;  // column inside the segment
     const bool uniform = m0 / g.T == min(m0 + BM - 1, g.M - 1) / g.T;
     const float s_uni = ep_sign;
 #pragma unroll
@@ -519,11 +519,11 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
-      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.N / g.seg_n > 3 || g.u_qstride < 1)
+      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.seg0 < 0 || g.seg0 + g.N / g.seg_n > 3 || g.u_qstride < 1)
     return NOISE_EINVAL;
   const int nseg = g.N / g.seg_n;
-  if (g.u_qstride == 1 && g.u_ld < nseg * g.u_parts) return NOISE_EINVAL;
-  for (int s = 0; s < nseg; ++s)
+  if (g.u_qstride == 1 && g.u_ld < (g.seg0 + nseg) * g.u_parts) return NOISE_EINVAL;
+  for (int s = g.seg0; s < g.seg0 + nseg; ++s)
     if (!g.ra[s] || ((uintptr_t)g.ra[s] & 15)) return NOISE_EINVAL;
   if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return NOISE_EINVAL;
   if (((uintptr_t)g.out_f32 | (uintptr_t)g.out_bf16) & 15) return NOISE_EINVAL;
@@ -538,7 +538,7 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
       if (!g.out_f32) return NOISE_EINVAL;
       return launch_epi<EPI_RESID>(g, stream);
     case EPI_QKV:
-      if (!g.out_bf16 || g.seg_n != 512 || nseg != 3 || !g.rot_cos || !g.rot_sin ||
+      if (!g.out_bf16 || g.seg_n != 512 || g.seg0 + nseg != 3 || !g.rot_cos || !g.rot_sin ||
           (g.gate && (!g.ve_w || !g.ve_a || !g.ve_b || !g.idx || g.ve_v <= 0)))
         return NOISE_EINVAL;
       return launch_epi<EPI_QKV>(g, stream);

@@ -56,9 +56,23 @@ constexpr int XROW = KD * 2 + 16;     // LDS bytes per x row (1 KiB + 16: bank-g
 constexpr int XBYTES = R * XROW;      // LDS bytes of one x block
 constexpr int VEC = 512;              // per-wave vector area: a (128 B) | b_next (128 B) | u (128 B) | .. | sign
 constexpr int SIGN_OFF = VEC - 8;
-// per wave and block: 4 x rows, then (relu^2 mode) a|b_next|u and the sign
-template <bool DENSE>
-constexpr int DMA_PER_BLOCK = DENSE ? 4 : 6;
+// Epilogue modes of the kernel.
+enum : int {
+  XS_RELU2 = 0,  // MLP c_fc: bf16(relu(lowrank)^2) + partial dots with b_next
+  XS_DENSE = 1,  // c_proj dense product y = bf16(x W^T), row-major
+  XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, bf16
+};
+// per wave and block: 4 x rows, then the mode's vectors (relu^2: a|b_next|u and the sign; q|k: a, and one
+// of cos / sin / u|sign / padding)
+template <int MODE>
+constexpr int DMA_PER_BLOCK = MODE == XS_DENSE ? 4 : 6;
+
+// q|k mode: the per-block vectors shared by the workgroup's 8 waves (5.5 KiB per ring slot).
+struct QkVec {
+  bf16 cs[2][R][32];  // rotary cos / sin rows of the block's 32 tokens
+  float uq[R][4];     // u_qkv rows: bf16 dots with b_q, b_k, b_v and the member's sign
+  float av[NW][32];   // a over each wave's 32 columns
+};
 constexpr int STORES_PER_EPI = 2;     // lower bound on an epilogue's store instructions (two h rows)
 
 template <int N>
@@ -91,12 +105,27 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
 }
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned v) { return *reinterpret_cast<bf16x2*>(&v); }
 
+// q|k mode column map: slice s covers segment s / 2 (q, k), heads 4 (s % 2) .. + 3; wave w takes head
+// 4 (s % 2) + w / 2 and, of its 64 dims, half h = w % 2: local columns 0-15 are dims 16 h .. 16 h + 15 and
+// 16-31 are dims 32 + 16 h .. 47 + 16 h, so every rotary pair (d, d + 32) lies in one lane pair l, l ^ 32
+// and the head's RMSNorm needs only the partner wave w ^ 1.
+__device__ __forceinline__ int qk_col(int nslice, int wave, int lc) {
+  const int seg = nslice >> 1, head = 4 * (nslice & 1) + (wave >> 1), half = wave & 1;
+  const int dim = lc < 16 ? 16 * half + lc : 32 + 16 * half + (lc - 16);
+  return seg * 512 + head * 64 + dim;
+}
+
 // DENSE: the c_proj dense product y = bf16(x W^T) only (no rank-1 term, no vectors, no partial dots), row-major.
-template <bool DENSE>
+template <int MODE>
 __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
+  constexpr bool DENSE = MODE == XS_DENSE, QK = MODE == XS_QK;
+  constexpr int FIRST_STORE = QK ? 2 : 1;
   __shared__ __attribute__((aligned(16))) char smem[NBUF * XBYTES];
   __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
   __shared__ __attribute__((aligned(16))) float red[2][R][NW];
+  __shared__ __attribute__((aligned(16))) QkVec qv[NBUF];
+  __shared__ __attribute__((aligned(16))) float ssq[2][R][NW];  // q|k: per-row partial sums of squares
+  __shared__ __attribute__((aligned(16))) float qpad[R][4];     // q|k: landing area of the padding loads
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
   const int nslices = g.N / BN;
@@ -108,7 +137,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // this workgroup's blocks: lo + stream + k * streams, k = 0 .. nb - 1 (the same for every wave)
   const int nb = stream < streams && lo + stream < hi ? (hi - lo - stream + streams - 1) / streams : 0;
   if (nb == 0) return;
-  const int fw = nslice * BN + wave * 32;  // first column of this wave
+  const int fw = nslice * BN + wave * 32;  // first column of this wave (relu^2 / dense)
 
   // ---- resident W: fragment [j][s] holds W row fw + 8 (r >> 2) + 4 j + (r & 3), r = lane & 15,
   // k = 128 grp + 8 s. MFMA output element e of column block j in lane l is then column
@@ -118,7 +147,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     const int r = lane & 15;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const bf16* wp = g.W + (long)(fw + 8 * (r >> 2) + 4 * j + (r & 3)) * g.ldw + 128 * grp;
+      const int lcol = 8 * (r >> 2) + 4 * j + (r & 3);
+      const bf16* wp = g.W + (long)(QK ? qk_col(nslice, wave, lcol) : fw + lcol) * g.ldw + 128 * grp;
 #pragma unroll
       for (int s = 0; s < KS; ++s) wr[j][s] = *reinterpret_cast<const bf16x8*>(wp + 8 * s);
     }
@@ -138,10 +168,26 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_x4(abase + q * g.lda, xsl + q * XROW);
+    if constexpr (QK) {
+      // a over the wave's columns (lanes 0-7: two 64-byte runs of dims); then wave 0-3: cos / sin rows
+      // (1 KiB each), wave 4: the block's u_qkv rows, waves 5-7: the same rows into a padding area (every
+      // wave issues DMA_PER_BLOCK loads per block)
+      const int seg = nslice >> 1;
+      if (lane < 8)
+        dma_x4(g.ra[seg] + (long)dir * g.ra_ld + qk_col(nslice, wave, 16 * (lane >> 2)) - seg * 512 + 4 * (lane & 3),
+               &qv[buf].av[wave][0]);
+      if (wave < 4) {
+        const bf16* tab = (wave >> 1) ? g.rot_sin : g.rot_cos;
+        dma_x4(tab + (long)(t0 + 16 * (wave & 1)) * 32 + 8 * lane, &qv[buf].cs[wave >> 1][16 * (wave & 1)][0]);
+      } else if (lane < R) {
+        dma_x4(g.u + (long)(row0 + lane) * 4, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
+      }
+      return;
+    }
     const float* vsrc = lane < 8 ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
                         : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
                                     : g.u + row0 + 4 * (lane - 16);
-    if constexpr (!DENSE) {
+    if constexpr (MODE == XS_RELU2) {
       if (lane < 24) dma_x4(vsrc, &svec[buf][wave][0]);
       if (lane == 0) dma_x1(g.sign + p, &svec[buf][wave][SIGN_OFF]);
     }
@@ -150,7 +196,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // Block k has landed for this wave once at most nd * DMA_PER_BLOCK + ne * STORES_PER_EPI later operations
   // are outstanding: the nd later load groups and the stores of the ne epilogues issued since.
   auto wait_block = [&](int nd, int ne) {
-    constexpr int D = DMA_PER_BLOCK<DENSE>, S = STORES_PER_EPI;
+    constexpr int D = DMA_PER_BLOCK<MODE>, S = STORES_PER_EPI;
     switch (nd * 3 + ne) {
       case 0: wait_vm_lgkm0<0>(); break;
       case 1: wait_vm_lgkm0<S>(); break;
@@ -167,12 +213,76 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   f32x4 accA[2][2], accB[2][2];
   float ev_a[8], ev_u[2], ev_dot[2];
   unsigned ev_bp[4], ev_h[2][4];
+  float ev_v[2][8], ev_ss[2];   // q|k: rotated values and the wave's sums of squares per row half
+  bf16x8 ev_cs[2][2];           // q|k: cos / sin of the lane's 8 dims for rows r, r + 16
+  const int qk_ocol = QK ? qk_col(nslice, wave, 8 * grp) : 0;  // the lane's first output column
 
   // Stage st (0 .. 15) of the epilogue of block pk (ring slot pbuf) from acc:
   //   0: vectors from LDS; 1-4 / 7-10: column pairs of row half 0 / 1; 5 / 11: h store and first shuffle;
   //   6 / 12: second shuffle and the wave partial into LDS.
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
+    if constexpr (QK) {
+      // Iteration k runs, for block pk - 1 (held from iteration k - 1): stages 0 / 1, the head's RMSNorm
+      // (utils/model.py:46-47, eps = 2^-23) of row half 0 / 1 from both waves' sums of squares, written
+      // to LDS last iteration and visible since this iteration's barrier, and the bf16 store; for block pk:
+      // stage 2 the vectors, 3-6 / 8-11 v = bf16(dense) + s bf16(u) a of row half 0 / 1, 7 / 12 rotary
+      // (utils/model.py:55-58) and the wave's sum of squares into LDS.
+      const QkVec& q = qv[pbuf];
+      const int r = lane & 15, seg = nslice >> 1;
+      if (st < 2) {
+        if (pk < 1) return;
+        const int i = st;
+        const float tot = ev_ss[i] + ssq[(pk - 1) & 1][16 * i + r][wave ^ 1];
+        const float rn = rsqrtf(tot * (1.f / 64.f) + 1.1920928955078125e-07f);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = pack_bf16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
+        const long row = (long)blk_of(pk - 1) * R + 16 * i + r;
+        store_stream_x4(g.out_bf16 + row * g.ldo + qk_ocol, o);
+        return;
+      }
+      if (pk < 0 || st > 12) return;
+      if (st == 2) {
+        const float4 a0 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp]);
+        const float4 a1 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp + 4]);
+        ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
+        ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
+        const float4 u0 = *reinterpret_cast<const float4*>(&q.uq[r][0]);
+        const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
+        ev_u[0] = u0.w * bf16r(seg ? u0.y : u0.x);
+        ev_u[1] = u1.w * bf16r(seg ? u1.y : u1.x);
+        const int dd = (qk_ocol & 63) & 31;  // the lane's first dim modulo 32
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ev_cs[i][c] = *reinterpret_cast<const bf16x8*>(&q.cs[c][16 * i + r][dd]);
+        return;
+      }
+      const int i = st < 8 ? 0 : 1, sub = st - (i ? 8 : 3);
+      if (sub < 4) {
+        const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
+        ev_v[i][c] = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
+        ev_v[i][c + 1] = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+      } else {
+        // dims d < 32 (lane groups 0, 1): x_d cos + x_{d+32} sin; d >= 32: x_d cos - x_{d-32} sin
+        const bool first = grp < 2;
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pv = __shfl_xor(ev_v[i][e], 32, 64);
+          const float cv = (float)ev_cs[i][0][e], sv = (float)ev_cs[i][1][e];
+          const float y = first ? ev_v[i][e] * cv + pv * sv : ev_v[i][e] * cv - pv * sv;
+          ev_v[i][e] = y;
+          ss += y * y;
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        ev_ss[i] = ss;
+        if (grp == 0) ssq[pk & 1][16 * i + r][wave] = ss;
+      }
+      return;
+    }
     if constexpr (DENSE) {
       // stages 1-4 / 7-10: bf16 pairs of row half 0 / 1; 5 / 11: the row half's store
       if (st == 0 || st > 11 || st == 6) return;
@@ -242,7 +352,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // of block k - 1 (epi) and the partial sums of block k - 2 (sum); then the loads of block k + NBUF - 1
   // into the slot block k - 1 used.
   auto iter = [&](f32x4 (&acc)[2][2], const f32x4 (&prev)[2][2], int k, bool epi, bool sum) {
-    wait_block(min(NBUF - 2, nb - 1 - k), min(2, max(0, k - 1)));
+    // stores are issued in iterations j >= FIRST_STORE (q|k stores block j - 2's rows, the others block j - 1's)
+    wait_block(min(NBUF - 2, nb - 1 - k), min(2, max(0, k - FIRST_STORE)));
     __builtin_amdgcn_s_barrier();
     const int pbuf = (k + NBUF - 1) % NBUF;
     // lane (row r = lane & 15, group grp): row-half i at LDS row 16 i + r, step s at chunk 16 grp + s
@@ -267,7 +378,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma16x16x32(wr[j][s], xc[i], acc[i][j]);
       if (epi) epi_stage(prev, k - 1, pbuf, s);
-      if constexpr (!DENSE) {
+      if constexpr (MODE == XS_RELU2) {
         if (s == 13 && sum) sum_partials(k - 2);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -293,7 +404,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   }
   wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
-  if constexpr (!DENSE) {
+  if constexpr (MODE == XS_RELU2) {
     if (last >= 1) sum_partials(last - 1);
   }
 #pragma unroll
@@ -301,10 +412,16 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     if (last == k) epi_stage(accB, last, last % NBUF, st);
     else epi_stage(accA, last, last % NBUF, st);
   }
-  if constexpr (!DENSE) {
+  if constexpr (MODE == XS_RELU2) {
     wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     sum_partials(last);
+  }
+  if constexpr (QK) {
+    // the last block's normalisation, once every wave's sums of squares are in LDS
+    __builtin_amdgcn_s_barrier();
+    epi_stage(accA, last + 1, 0, 0);
+    epi_stage(accA, last + 1, 0, 1);
   }
 }
 
@@ -318,7 +435,7 @@ bool xs_shape_ok(const LowrankGemmArgs& g) {
          g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.lda >= g.K && g.ldw >= g.K && g.ldo >= g.N &&
          g.A && g.W && g.out_bf16 && !(((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15);
 }
-template <bool DENSE>
+template <int MODE>
 int xs_launch(const LowrankGemmArgs& g, hipStream_t stream) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -326,7 +443,7 @@ int xs_launch(const LowrankGemmArgs& g, hipStream_t stream) {
     cus = 256;
   const int nslices = g.N / BN, per_xcd = std::max(1, cus / 8);
   const int streams = std::max(1, per_xcd / nslices);
-  hipLaunchKernelGGL((xs_kernel<DENSE>), dim3(8 * streams * nslices), dim3(512), 0, stream, g);
+  hipLaunchKernelGGL((xs_kernel<MODE>), dim3(8 * streams * nslices), dim3(512), 0, stream, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
@@ -342,12 +459,25 @@ int xs_relu2_launch(const LowrankGemmArgs& g, hipStream_t stream) {
       g.pair_shift > 1)
     return NOISE_EINVAL;
   if (((uintptr_t)g.ra[0] | (uintptr_t)g.rb_next | (uintptr_t)g.u) & 15) return NOISE_EINVAL;
-  return xs_launch<false>(g, stream);
+  return xs_launch<XS_RELU2>(g, stream);
 }
 
 bool xs_dense_supported(const LowrankGemmArgs& g) { return xs_shape_ok(g) && !g.out_tiled; }
 
 int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream) {
   if (!xs_dense_supported(g)) return NOISE_EINVAL;
-  return xs_launch<true>(g, stream);
+  return xs_launch<XS_DENSE>(g, stream);
+}
+
+bool xs_qk_supported(const LowrankGemmArgs& g) {
+  return xs_shape_ok(g) && !g.out_tiled && g.N == 1024 && g.u_ld == 4 && g.ra_ld % 4 == 0 && g.T % R == 0;
+}
+
+int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_qk_supported(g) || !g.u || !g.ra[0] || !g.ra[1] || !g.rot_cos || !g.rot_sin || g.pair_shift < 0 ||
+      g.pair_shift > 1)
+    return NOISE_EINVAL;
+  if (((uintptr_t)g.ra[0] | (uintptr_t)g.ra[1] | (uintptr_t)g.u | (uintptr_t)g.rot_cos | (uintptr_t)g.rot_sin) & 15)
+    return NOISE_EINVAL;
+  return xs_launch<XS_QK>(g, stream);
 }

@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   for (int k = 0; k < 3; ++k) u[k] = dot_bf16(x, g.b_qkv[k] + (long)dir * D + lane * 8);
   if (lane == 0) {
     float* ur = g.u_qkv + row * 4;
-    ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = 0.f;
+    ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = s;  // the member's sign rides with the dots
   }
   if (g.gate_w) {
     // lanes 0..3 hold h[:32]; every lane computes one (gate head, partial) product set

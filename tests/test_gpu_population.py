@@ -110,6 +110,8 @@ def test_block_entry_and_qkv_match_oracle():
     for k, bb in enumerate((bq, bk, bv)):
         ur = om.bf(om.bf(hr) @ om.bf(bb).unsqueeze(-1))[..., 0]
         assert torch.allclose(u.cpu()[:, k].view(m, T), ur, atol=2e-2, rtol=1e-2)
+    # column 3 carries the member's sign for the QKV epilogue
+    assert torch.equal(u.cpu()[:, 3].view(m, T), sign[:, None].expand(m, T))
     gr = 2 * torch.sigmoid(om.lowrank(hr[..., :32], gw, ga, gb, sign, 'bf16'))
     assert torch.allclose(gate.cpu().view(m, T, 8), gr, atol=2e-3)
     # q | k | v from the GPU's own h, u and gate (isolates the GEMM epilogue)
