@@ -231,6 +231,7 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
     gv.seg0 = 2;
     gv.W = g.W + (long)2 * DM * DM;
     gv.out_bf16 = g.out_bf16 + 2 * DM;
+    if (xs_v_supported(gv)) return xs_v_launch(gv, s);
     return lowrank_gemm_launch(EPI_QKV, gv, s);
   }
   return lowrank_gemm_launch(EPI_QKV, g, s);

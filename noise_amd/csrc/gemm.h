@@ -97,3 +97,6 @@ int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream);
 // u rows [M, 4] = the bf16 dots with b_q, b_k, b_v and the member's sign; ra[0] / ra[1] = a_q / a_k.
 bool xs_qk_supported(const LowrankGemmArgs& g);
 int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream);
+// ... and for c_v without value embedding (N = 512, W and out already offset to the v segment; a = ra[2]).
+bool xs_v_supported(const LowrankGemmArgs& g);
+int xs_v_launch(const LowrankGemmArgs& g, hipStream_t stream);

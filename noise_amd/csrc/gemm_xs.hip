@@ -61,6 +61,7 @@ enum : int {
   XS_RELU2 = 0,  // MLP c_fc: bf16(relu(lowrank)^2) + partial dots with b_next
   XS_DENSE = 1,  // c_proj dense product y = bf16(x W^T), row-major
   XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, bf16
+  XS_V = 3,      // c_v without value embedding: lowrank, the bf16-rounded value stored as fp16
 };
 // per wave and block: 4 x rows, then the mode's vectors (relu^2: a|b_next|u and the sign; q|k: a, and one
 // of cos / sin / u|sign / padding)
@@ -118,7 +119,7 @@ __device__ __forceinline__ int qk_col(int nslice, int wave, int lc) {
 // DENSE: the c_proj dense product y = bf16(x W^T) only (no rank-1 term, no vectors, no partial dots), row-major.
 template <int MODE>
 __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
-  constexpr bool DENSE = MODE == XS_DENSE, QK = MODE == XS_QK;
+  constexpr bool DENSE = MODE == XS_DENSE, QK = MODE == XS_QK, VV = MODE == XS_V;
   constexpr int FIRST_STORE = QK ? 2 : 1;
   __shared__ __attribute__((aligned(16))) char smem[NBUF * XBYTES];
   __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
@@ -168,6 +169,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_x4(abase + q * g.lda, xsl + q * XROW);
+    if constexpr (VV) {
+      // a over the wave's 32 columns (lanes 0-7); wave 4: the block's u_qkv rows, the others the same rows
+      // into a padding area (every wave issues DMA_PER_BLOCK loads per block)
+      if (lane < 8) dma_x4(g.ra[2] + (long)dir * g.ra_ld + fw + 4 * lane, &qv[buf].av[wave][0]);
+      if (lane < R) dma_x4(g.u + (long)(row0 + lane) * 4, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
+      return;
+    }
     if constexpr (QK) {
       // a over the wave's columns (lanes 0-7: two 64-byte runs of dims); then wave 0-3: cos / sin rows
       // (1 KiB each), wave 4: the block's u_qkv rows, waves 5-7: the same rows into a padding area (every
@@ -222,6 +230,36 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   //   6 / 12: second shuffle and the wave partial into LDS.
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
+    if constexpr (VV) {
+      // stages 0: vectors; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 as fp16 pairs
+      // holding the bf16-rounded value (exact); 5 / 10: the row half's store
+      const QkVec& q = qv[pbuf];
+      const int r = lane & 15;
+      if (st == 0) {
+        const float4 a0 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp]);
+        const float4 a1 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp + 4]);
+        ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
+        ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
+        const float4 u0 = *reinterpret_cast<const float4*>(&q.uq[r][0]);
+        const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
+        ev_u[0] = u0.w * bf16r(u0.z);
+        ev_u[1] = u1.w * bf16r(u1.z);
+        return;
+      }
+      if (st > 10) return;
+      const int i = st < 6 ? 0 : 1, sub = st - (i ? 6 : 1);
+      if (sub < 4) {
+        const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
+        const float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
+        const float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+        _Float16 __attribute__((ext_vector_type(2))) hp = {(_Float16)bf16r(v0), (_Float16)bf16r(v1)};
+        ev_h[i][sub] = *reinterpret_cast<unsigned*>(&hp);
+      } else {
+        const long row = (long)blk_of(pk) * R + 16 * i + r;
+        store_stream_x4(g.out_bf16 + row * g.ldo + fw + 8 * grp, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+      }
+      return;
+    }
     if constexpr (QK) {
       // Iteration k runs, for block pk - 1 (held from iteration k - 1): stages 0 / 1, the head's RMSNorm
       // (utils/model.py:46-47, eps = 2^-23) of row half 0 / 1 from both waves' sums of squares, written
@@ -471,6 +509,16 @@ int xs_dense_launch(const LowrankGemmArgs& g, hipStream_t stream) {
 
 bool xs_qk_supported(const LowrankGemmArgs& g) {
   return xs_shape_ok(g) && !g.out_tiled && g.N == 1024 && g.u_ld == 4 && g.ra_ld % 4 == 0 && g.T % R == 0;
+}
+
+bool xs_v_supported(const LowrankGemmArgs& g) {
+  return xs_shape_ok(g) && !g.out_tiled && g.N == 512 && g.u_ld == 4 && g.ra_ld % 4 == 0 && !g.gate;
+}
+
+int xs_v_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_v_supported(g) || !g.u || !g.ra[2] || g.pair_shift < 0 || g.pair_shift > 1) return NOISE_EINVAL;
+  if (((uintptr_t)g.ra[2] | (uintptr_t)g.u) & 15) return NOISE_EINVAL;
+  return xs_launch<XS_V>(g, stream);
 }
 
 int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream) {

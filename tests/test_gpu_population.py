@@ -132,6 +132,18 @@ def test_block_entry_and_qkv_match_oracle():
     for k, ref in enumerate((qr, kr, vv)):
         assert rel_err(got[:, :, k], om.bf(ref)) < 5e-3, k
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
+    # a block without value embedding (gate null): the same q | k, v = lowrank only
+    log_case(f'qkv without value embedding m={m} T={T}')
+    qkv2 = torch.empty_like(qkv)
+    _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
+              u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), None,
+              None, V, None, None, None, qkv2.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv2[:, :1024].cpu(), qkv[:, :1024].cpu())
+    v2 = qkv2[:, 1024:].cpu().view(torch.float16).float().view(m, T, 512)
+    vref = lin(wv, av, 2)
+    assert rel_err(v2, om.bf(vref)) < 5e-3
+    assert (v2 - vref).abs().max() <= 2 ** -7 * vref.abs().max() + 1e-3
 
 
 
