@@ -114,11 +114,22 @@ int noise_embed_norm(const float* w, long vocab, const float* a, const float* b,
  * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. The npend (<= 2) deferred
  * residuals in pend (the previous block's attention and MLP c_proj outputs) are added to x_in, in order,
  * before the mix. */
+/* The embedding a block entry recomputes x0 from: x0 = norm(w[idx] + s a[dir, idx] b[dir]), the same
+ * arithmetic as noise_embed_norm (bit-identical rows). */
+typedef struct noise_embed {
+  const float* w; /* [vocab, 512] */
+  long vocab;
+  const float* a; /* [dirs, vocab] */
+  const float* b; /* [dirs, 512] */
+  const int64_t* idx; /* [T] */
+} noise_embed_t;
+/* x0 may be null when x0_embed is given (x0 rows recomputed: no stored [members*T, 512] fp32 x0 stream);
+ * x_in may be null at block 0 (x_in = x0). */
 int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h, float* u_qkv, const float* b_q,
                       const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
                       const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
                       const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
-                      const noise_pending_t* pend, int npend, noise_stream_t stream);
+                      const noise_pending_t* pend, int npend, const noise_embed_t* x0_embed, noise_stream_t stream);
 
 /* q | k | v = lowrank(h, [W_q; W_k; W_v]) with per-segment a vectors and the u_qkv dots, then rotary +
  * QK RMSNorm on q and k (utils/model.py:55-58, :46-47; train/val/eggroll.py:90) and, when gate is not

@@ -29,7 +29,7 @@ SIGNATURES = {
     'noise_lowrank_mlp': [P, L, L, P, P, I, I, P, P, P, P, P, I, I, I, P, P, I, P, S, P],
     'noise_cast_bf16': [P, P, L, I, P],
     'noise_embed_norm': [P, L, P, P, P, P, I, I, I, P, P],
-    'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P, I, P],
+    'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P, I, P, P],
     'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, P, P],
     'noise_attention_workspace_size': [I, I, SP],
     'noise_attention': [P, I, I, I, I, P, I, P, P, P, P, S, P],
@@ -57,6 +57,17 @@ def outer_mats(items):
     """(a ptr or 0, a_ld, b ptr, b_ld, out, in, grad ptr) tuples -> (pointer to a host array, count)."""
     arr = (OuterMat * len(items))(*[OuterMat(*it) for it in items])
     return ctypes.cast(arr, P), len(items), arr
+
+
+class Embed(ctypes.Structure):
+    """noise_embed_t of include/noise_hip.h (the table a block entry recomputes x0 from)."""
+    _fields_ = [('w', P), ('vocab', L), ('a', P), ('b', P), ('idx', P)]
+
+
+def embed(w, vocab, a, b, idx):
+    """A noise_embed_t (keep the returned object alive until the call is enqueued) and its pointer."""
+    e = Embed(w, vocab, a, b, idx)
+    return e, ctypes.cast(ctypes.pointer(e), P)
 
 
 class Pending(ctypes.Structure):

@@ -167,9 +167,11 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
                       const float* b_k, const float* b_v, const float* lambda_r, const float* lambda_0, const float* eps_r,
                       const float* eps_0, long eps_ld, const float* gate_w, const float* gate_a,
                       const float* gate_b, float* gate, const float* sign, int members, int T, int pair_shift,
-                      const noise_pending_t* pend, int npend, noise_stream_t stream) {
+                      const noise_pending_t* pend, int npend, const noise_embed_t* x0_embed, noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  if (!x0 && !x0_embed) return NOISE_EINVAL;
   BlockEntryArgs g{};
+  if (!x0) g.emb = EmbedSrc{x0_embed->w, x0_embed->a, x0_embed->b, x0_embed->vocab, x0_embed->idx};
   if (int rc = copy_pending(pend, npend, g.pend)) return rc;
   g.npend = npend;
   g.x_in = x_in;

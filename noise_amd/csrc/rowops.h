@@ -27,9 +27,19 @@ struct EmbedNormArgs {
   float* x0;             // [M, 512] fp32 out
 };
 
+// Source of x0 = norm(lowrank_embed(w, a, b)) rows, recomputed where they are read instead of stored.
+struct EmbedSrc {
+  const float* w;        // [V, 512] embedding table
+  const float* a;        // [dirs, V]
+  const float* b;        // [dirs, 512]
+  long V;
+  const int64_t* idx;    // [T]
+};
+
 struct BlockEntryArgs {
-  const float* x_in;     // [M, 512] residual stream before the mix (x0 itself at block 0)
-  const float* x0;
+  const float* x_in;     // [M, 512] residual stream before the mix; null: x0 itself (block 0)
+  const float* x0;       // [M, 512]; null: recomputed from emb
+  EmbedSrc emb;
   float* x_out;          // mixed stream (may alias x_in)
   __bf16* h;             // [M, 512] bf16(norm(x))
   float* u_qkv;          // [M, 4] bf16-rounded dots with b_q, b_k, b_v (4th slot zero)

@@ -71,19 +71,25 @@ __device__ __forceinline__ void add_pending(Row8& x, const Pending* pend, int np
 }
 
 // x0 = norm(W[idx] + s a[:, idx] b) (train/val/eggroll.py:61-63, :74).
+// x0 row t of member p (sign s, direction dir): norm(w[idx[t]] + s a[dir, idx[t]] b[dir]), 8 values per lane.
+__device__ __forceinline__ Row8 embed_row(const EmbedSrc& e, int t, int dir, float s, int lane) {
+  const long tok = e.idx[t];
+  const float sa = s * e.a[(long)dir * e.V + tok];
+  Row8 w = load8(e.w + tok * D + lane * 8);
+  const Row8 b = load8(e.b + (long)dir * D + lane * 8);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) w.v[k] = w.v[k] + sa * b.v[k];
+  rms_norm_row(w);
+  return w;
+}
+
 __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
   const int p = (int)(row / g.T), t = (int)(row % g.T), dir = p >> g.pair_shift;
-  const long tok = g.idx[t];
-  const float sa = g.sign[p] * g.a[(long)dir * g.V + tok];
-  Row8 w = load8(g.w + tok * D + lane * 8);
-  const Row8 b = load8(g.b + (long)dir * D + lane * 8);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) w.v[e] = w.v[e] + sa * b.v[e];
-  rms_norm_row(w);
-  store8(g.x0 + row * D + lane * 8, w);
+  const EmbedSrc e{g.w, g.a, g.b, g.V, g.idx};
+  store8(g.x0 + row * D + lane * 8, embed_row(e, t, dir, g.sign[p], lane));
 }
 
 // Block entry (train/val/eggroll.py:77-88): x = (l_r + s e_r) x + (l_0 + s e_0) x0; h = norm(x);
@@ -96,9 +102,11 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   const float s = g.sign[p];
   const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
-  Row8 x = load8(g.x_in + row * D + lane * 8);
+  // x0: stored, or recomputed from the embedding (2 KiB gathered from an L2-resident table instead of 2 KiB
+  // streamed from HBM); block 0 mixes x0 with itself
+  const Row8 x0 = g.x0 ? load8(g.x0 + row * D + lane * 8) : embed_row(g.emb, (int)(row % g.T), dir, s, lane);
+  Row8 x = g.x_in ? load8(g.x_in + row * D + lane * 8) : x0;
   add_pending(x, g.pend, g.npend, row, dir, s, lane);
-  const Row8 x0 = load8(g.x0 + row * D + lane * 8);
 #pragma unroll
   for (int e = 0; e < 8; ++e) x.v[e] = lr * x.v[e] + l0 * x0.v[e];
   store8(g.x_out + row * D + lane * 8, x);
@@ -270,7 +278,8 @@ int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s) {
 }
 
 int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
-  if (g.M <= 0 || g.T <= 0 || !g.x_in || !g.x0 || !g.x_out || !g.h || !g.u_qkv || !g.sign || !g.eps_r || !g.eps_0 ||
+  if (!g.x0 && (!g.emb.w || !g.emb.a || !g.emb.b || !g.emb.idx || g.emb.V <= 0)) return NOISE_EINVAL;
+  if (g.M <= 0 || g.T <= 0 || !g.x_out || !g.h || !g.u_qkv || !g.sign || !g.eps_r || !g.eps_0 ||
       !g.lambda_r || !g.lambda_0 || !g.b_qkv[0] || !g.b_qkv[1] || !g.b_qkv[2])
     return NOISE_EINVAL;
   if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate)) return NOISE_EINVAL;

@@ -3,8 +3,8 @@
 
 The host side only orders kernel launches and owns device buffers (torch tensors); every op of the
 forward runs in libnoise_hip.so. Members are evaluated in chunks so activations stay bounded: a chunk
-of m members at T tokens holds about m * T * 17 KiB of activations (fp32 residual stream and x0,
-bf16 q|k|v, attention output and the 2048-wide MLP hidden).
+of m members at T tokens holds about m * T * 13 KiB of activations (fp32 residual stream, bf16 q|k|v,
+attention output and the 2048-wide MLP hidden; x0 is recomputed, never stored).
 """
 import torch
 
@@ -83,7 +83,6 @@ class Buffers:
         self.members, self.T = members, T
         f32, b16 = torch.float32, torch.bfloat16
         self.x = torch.empty(M, D, device=device, dtype=f32)
-        self.x0 = torch.empty(M, D, device=device, dtype=f32)
         self.h = torch.empty(M, D, device=device, dtype=b16)
         self.u_qkv = torch.empty(M, 4, device=device, dtype=f32)
         self.gate = torch.empty(M, H, device=device, dtype=f32)
@@ -168,10 +167,10 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     ps = pair_shift
     a, b = noise['transformer.wte.weight']
     V = p['transformer.wte.weight'].shape[0]
-    t0 = tm.mark('embed')
-    _lib.call('noise_embed_norm', _p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(sign), _p(idx), m, T, ps,
-              _p(buf.x0), s)
-    tm.close(t0)
+    # x0 = norm(lowrank_embed(wte)) (train/val/eggroll.py:74) is never stored: every block entry recomputes its
+    # rows from the L2-resident table (the same arithmetic as noise_embed_norm), which saves reading a 4 KiB
+    # per member-token fp32 stream from HBM at each of the n_layer blocks
+    emb, emb_ptr = _lib.embed(_p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(idx))
     eps_r, eps_0 = noise['resid_lambdas'], noise['x0_lambdas']
     lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
     # Deferred residuals. `x = x + lowrank(c_proj, ...)` (train/val/eggroll.py:92-93) is split: the c_proj GEMM
@@ -190,13 +189,13 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
             ga, gb = noise[pre + 'attn.ve_gate.weight']
             vw = p[f'value_embeds.{i}.weight']
             va, vb = noise[f'value_embeds.{i}.weight']
-        x_in = buf.x0 if i == 0 else buf.x
+        x_in = None if i == 0 else _p(buf.x)
         t0 = tm.mark('entry')
         pend, npend = _lib.pending(*pend_prev)
-        _lib.call('noise_block_entry', _p(x_in), _p(buf.x0), _p(buf.x), _p(buf.h), _p(buf.u_qkv), _p(bq), _p(bk),
+        _lib.call('noise_block_entry', x_in, None, _p(buf.x), _p(buf.h), _p(buf.u_qkv), _p(bq), _p(bk),
                   _p(bv), lam_r.data_ptr() + 4 * i, lam_0.data_ptr() + 4 * i, eps_r.data_ptr() + 4 * i,
                   eps_0.data_ptr() + 4 * i, eps_r.stride(0), _p(gw) if ve else 0, _p(ga) if ve else 0,
-                  _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, pend, npend, s)
+                  _p(gb) if ve else 0, _p(buf.gate) if ve else 0, _p(sign), m, T, ps, pend, npend, emb_ptr, s)
         tm.close(t0)
         t0 = tm.mark('qkv')
         _lib.call('noise_qkv', _p(buf.h), _p(W.qkv[i]), _p(aq), _p(ak), _p(av), _p(buf.u_qkv), _p(sign), m, T, ps,

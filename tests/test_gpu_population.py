@@ -62,6 +62,28 @@ def test_embed_norm_matches_oracle():
     ref = om.norm(om.lowrank_embed(w, rep(a), rep(b), idx, sign)).reshape(m * T, 512)
     assert (x0.cpu() - ref).abs().max() < 2e-5
 
+    # a block entry that recomputes x0 from the embedding (x0 and, at block 0, x_in null) equals one that
+    # reads the stored x0, bit for bit
+    log_case(f'block_entry with recomputed x0 m={m} T={T}')
+    s = torch.cuda.current_stream().cuda_stream
+    bq, bk, bv = (torch.randn(2, 512, generator=g).to(DEV) for _ in range(3))
+    lr, l0 = torch.tensor([0.9], device=DEV), torch.tensor([0.2], device=DEV)
+    er, e0 = torch.randn(2, 8, generator=g).to(DEV), torch.randn(2, 8, generator=g).to(DEV)
+    out = {}
+    emb, emb_ptr = _lib.embed(d[0].data_ptr(), V, d[1].data_ptr(), d[2].data_ptr(), d[4].data_ptr())
+    for mode in ('stored', 'recomputed'):
+        xo, h = torch.empty(m * T, 512, device=DEV), torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
+        u = torch.empty(m * T, 4, device=DEV)
+        stored = mode == 'stored'
+        _lib.call('noise_block_entry', x0.data_ptr() if stored else None, x0.data_ptr() if stored else None,
+                  xo.data_ptr(), h.data_ptr(), u.data_ptr(), bq.data_ptr(), bk.data_ptr(), bv.data_ptr(), lr.data_ptr(),
+                  l0.data_ptr(), er.data_ptr(), e0.data_ptr(), 8, 0, 0, 0, 0, d[3].data_ptr(), m, T, 1, None, 0,
+                  None if stored else emb_ptr, s)
+        torch.cuda.synchronize()
+        out[mode] = (xo.cpu(), h.cpu(), u.cpu())
+    for a_, b_ in zip(out['stored'], out['recomputed']):
+        assert torch.equal(a_, b_)
+
 
 def test_block_entry_and_qkv_match_oracle():
     """Block entry (mix, norm, q/k/v dots, value gate) and the QKV GEMM epilogue (segment rank-1,
@@ -97,7 +119,7 @@ def test_block_entry_and_qkv_match_oracle():
     _lib.call('noise_block_entry', d['x'].data_ptr(), d['x0'].data_ptr(), xo.data_ptr(), h.data_ptr(), u.data_ptr(),
               d['bq'].data_ptr(), d['bk'].data_ptr(), d['bv'].data_ptr(), d['lr'].data_ptr(), d['l0'].data_ptr(),
               d['er'].data_ptr() + 4 * 3, d['e0'].data_ptr() + 4 * 3, 8, d['gw'].data_ptr(), d['ga'].data_ptr(),
-              d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, None, 0, s)
+              d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, None, 0, None, s)
     _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
               u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), gate.data_ptr(),
               d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(), d['idx'].data_ptr(), qkv.data_ptr(), s)
@@ -176,7 +198,7 @@ def test_deferred_residuals_match_eager_lowrank():
     _lib.call('noise_block_entry', dev['x'].data_ptr(), dev['x0'].data_ptr(), xo.data_ptr(), h.data_ptr(), u.data_ptr(),
               dev['bq'].data_ptr(), dev['bk'].data_ptr(), dev['bv'].data_ptr(), dev['lr'].data_ptr(), dev['l0'].data_ptr(),
               dev['er'].data_ptr() + 4 * 3, dev['e0'].data_ptr() + 4 * 3, 8, 0, 0, 0, 0, dev['sign'].data_ptr(), m, T, 1,
-              pend, npend, s)
+              pend, npend, None, s)
     hn = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
     un = torch.empty(M, device=DEV)
     pend1, n1 = _lib.pending(p1)
