@@ -414,15 +414,20 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       } else {  // EPI_CE
         // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,
         // so the sum of exp(z') over 4096 columns needs no running maximum.
-        const long tg = g.targets[rrow % g.T];
-        float se = 0.f;
+        // Everything in log2 units: ez = exp(2 z / 15) = 2^(z 2 log2(e) / 15); zl = z' log2(e) =
+        // 15 log2(e) - 30 log2(e) / (ez + 1); exp(z') = 2^zl. The reciprocal is the hardware one
+        // (v_rcp_f32, 1 ulp): an IEEE division would cost ~10 VALU operations per logit.
+        constexpr float L2E = 1.4426950408889634f;
+        const int te = (int)(g.targets[rrow % g.T] - cb);  // the target's column among the lane's CW, if any
+        float se = 0.f, zt = 0.f;
 #pragma unroll
         for (int e = 0; e < CW; ++e) {
-          const float ez = __expf(v[e] * (2.f / 15.f));
-          const float zc = 15.f - 30.f / (ez + 1.f);
-          se += __expf(zc);
-          if (live && tg == cb + e) g.ce_tgt[row] = zc;
+          const float ez = __builtin_amdgcn_exp2f(v[e] * (2.f * L2E / 15.f));
+          const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
+          se += __builtin_amdgcn_exp2f(zl);
+          zt = e == te ? zl : zt;
         }
+        if (live && te >= 0 && te < CW) g.ce_tgt[row] = zt * 0.6931471805599453f;
         se += __shfl_xor(se, 16, 64);
         se += __shfl_xor(se, 32, 64);
         if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = se;
