@@ -279,9 +279,10 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int e = 0; e < 4; ++e) yv[4 * db + e] = bf16r(o[qb][db][e] * inv);
-    bf16* out = g.y + row * g.ldy + h * HD + 16 * grp;
-    store_stream_x4(out, pack2(yv[0], yv[1]), pack2(yv[2], yv[3]), pack2(yv[4], yv[5]), pack2(yv[6], yv[7]));
-    store_stream_x4(out + 8, pack2(yv[8], yv[9]), pack2(yv[10], yv[11]), pack2(yv[12], yv[13]), pack2(yv[14], yv[15]));
+    // ordinary stores: each instruction covers half of every 128-byte line of the rows, which L2 merges
+    uint4* out = reinterpret_cast<uint4*>(g.y + row * g.ldy + h * HD + 16 * grp);
+    out[0] = make_uint4(pack2(yv[0], yv[1]), pack2(yv[2], yv[3]), pack2(yv[4], yv[5]), pack2(yv[6], yv[7]));
+    out[1] = make_uint4(pack2(yv[8], yv[9]), pack2(yv[10], yv[11]), pack2(yv[12], yv[13]), pack2(yv[14], yv[15]));
     if (g.upart) {
       const float* br = g.b_proj + (long)dir * g.b_ld + h * HD + 16 * grp;
       float d = 0.f;

@@ -95,6 +95,16 @@ __device__ __forceinline__ void wait_stage(int ahead) {
   wait_vm_lgkm0<0>();
 }
 
+// Epilogue stores of the tile GEMM are ordinary (write-back) stores: a lane's 16-byte stores cover half of
+// each 128-byte line per instruction, and as non-temporal stores those halves reach memory separately
+// (measured: twice the written bytes in WRITE_SIZE); through L2 they merge into whole lines.
+__device__ __forceinline__ void store_x4(void* p, unsigned a, unsigned b, unsigned c, unsigned d) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(a, b, c, d);
+}
+__device__ __forceinline__ void store_f4(void* p, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+
 __device__ __forceinline__ float bf16_lo(unsigned v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(unsigned v) { return __uint_as_float(v & 0xffff0000u); }
 __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
@@ -304,7 +314,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
           for (int e = 0; e < CW; e += 8)
-            store_stream_x4(o + e, pack_bf16(acc[i][e / 4][0], acc[i][e / 4][1]), pack_bf16(acc[i][e / 4][2], acc[i][e / 4][3]),
+            store_x4(o + e, pack_bf16(acc[i][e / 4][0], acc[i][e / 4][1]), pack_bf16(acc[i][e / 4][2], acc[i][e / 4][3]),
                             pack_bf16(acc[i][e / 4 + 1][0], acc[i][e / 4 + 1][1]),
                             pack_bf16(acc[i][e / 4 + 1][2], acc[i][e / 4 + 1][3]));
         }
@@ -338,13 +348,13 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           if (g.out_f32) {
             float* o = g.out_f32 + (long)row * g.ldo + cb;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) store_stream_f4(o + 4 * j, v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            for (int j = 0; j < FN; ++j) store_f4(o + 4 * j, v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
           }
           if (g.out_bf16) {
             bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              store_stream_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
+              store_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
                               pack_bf16(v[e + 6], v[e + 7]));
           }
         }
@@ -400,14 +410,14 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           if (seg < 2) {
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              store_stream_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
+              store_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
                               pack_bf16(v[e + 4], v[e + 5]), pack_bf16(v[e + 6], v[e + 7]));
           } else {
             // v: the bf16-rounded value (the autocast rounding point) stored as fp16, which holds it exactly, so
             // attention can feed it to fp16 MFMAs straight from memory
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              store_stream_x4(o + e, pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
+              store_x4(o + e, pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
                               pack_f16_of_bf16(v[e + 4], v[e + 5]), pack_f16_of_bf16(v[e + 6], v[e + 7]));
           }
         }
