@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         ev_h[i][sub] = *reinterpret_cast<unsigned*>(&hp);
       } else {
         const long row = (long)blk_of(pk) * R + 16 * i + r;
-        store_stream_x4(g.out_bf16 + row * g.ldo + fw + 8 * grp, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
       }
       return;
     }
@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = pack_bf16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
         const long row = (long)blk_of(pk - 1) * R + 16 * i + r;
-        store_stream_x4(g.out_bf16 + row * g.ldo + qk_ocol, o);
+        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + qk_ocol) = o;
         return;
       }
       if (pk < 0 || st > 12) return;
@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         ev_h[i][sub] = pack_bf16(acc[i][j][e0], acc[i][j][e0 + 1]);
       } else {
         const long row = (long)blk_of(pk) * R + 16 * i + (lane & 15);
-        store_stream_x4(g.out_bf16 + row * g.ldo + fw + 8 * grp, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
       }
       return;
     }
