@@ -24,8 +24,8 @@ __device__ __forceinline__ Row8 load8(const float* p) {
   return Row8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
 }
 __device__ __forceinline__ void store8(float* p, const Row8& r) {
-  store_stream_f4(p, r.v[0], r.v[1], r.v[2], r.v[3]);
-  store_stream_f4(p + 4, r.v[4], r.v[5], r.v[6], r.v[7]);
+  *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
 }
 __device__ __forceinline__ void store8_bf16(bf16* p, const Row8& r) {
   bf16x8 o;
