@@ -22,10 +22,13 @@
 //   O^T += V^T P^T (fp16 MFMA): V stays row-major [key][dim] in LDS and its A fragments (8 consecutive keys
 //   of one dim per lane) come from ds_read_b64_tr_b16, which transposes 16-bit elements across each group
 //   of 16 lanes: with source lane 4 t + a of group g pointing at key 32 c + 8 g + 4 h + t, dims
-//   16 a + 4 db .. + 3, output lane 16 g + 4 a + b receives keys 32 c + 8 g + 4 h + (0..3) of dim
-//   16 a + 4 db + b. The A-row <-> dim order (row 4 a + b of block db is dim 16 a + 4 db + b) leaves each
-//   lane with 16 contiguous output dims of one query: 16-byte stores, and the c_proj dot y . b_proj over
-//   the head's 64 dims is a 4-lane reduction.
+//   16 db + 4 a .. + 3, output lane 16 g + 4 a + b receives keys 32 c + 8 g + 4 h + (0..3) of dim
+//   16 db + 4 a + b, so block db of the output is dims 16 db .. 16 db + 15 in order. The four lanes of a
+//   key row read both 8-byte halves of two adjacent 16-byte chunks (32 bytes), and the rows' chunk pairs are
+//   XOR-swizzled so that the rows read together cover the banks once (no conflicts for 16 lanes on 32
+//   banks, nor for 32 lanes on 64 banks). Each lane ends with dims 16 db + 4 (lane / 16) .. + 3 of one
+//   query for db = 0..3: 8-byte stores, and the c_proj dot y . b_proj over the head's 64 dims is a 4-lane
+//   reduction.
 #include "attention.h"
 #include "common.h"
 
@@ -66,9 +69,12 @@ __device__ __forceinline__ int key_of_krow(int R) {
   const int kb = R >> 4, r = R & 15;
   return 32 * (kb >> 1) + 8 * (r >> 2) + 4 * (kb & 1) + (r & 3);
 }
-// V tile [BKV keys][64 dims] fp16, 128-byte rows in key order; chunk c of row R sits at chunk c ^ vsw(R),
-// which spreads the transposing reads of 16 rows over the banks.
-__device__ __forceinline__ int vsw(int R) { return (R >> 1) & 7; }
+// V tile [BKV keys][64 dims] fp16, 128-byte rows in key order; chunk c of row R sits at chunk c ^ vsw(R). A
+// transposing read takes one aligned chunk pair of each of the rows 8 g + 4 h + t (t = 0..3) of four groups g;
+// with R = 8 g + 4 h + t the pair index is XORed with (t / 2) | ((g ^ t) % 2) << 1, distinct over t for one g
+// (16 lanes x 8 bytes over 32 banks) and over (t / 2, g % 2) for one t % 2 (32 lanes x 8 bytes over 64 banks,
+// where rows of one parity share a bank half).
+__device__ __forceinline__ int vsw(int R) { return 2 * (((R >> 1) & 1) | ((((R >> 3) ^ R) & 1) << 1)); }
 
 __device__ __forceinline__ unsigned pack2(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
@@ -141,8 +147,9 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   // per-lane LDS offsets of the MFMA operand reads (the block / step index adds a constant)
   // K block kb: row 16 kb + lane % 16, chunk grp and 4 + grp
   const int kofs0 = kswz(lane & 15, grp), kofs1 = kswz(lane & 15, 4 + grp);
-  // V fragment (step c, dim block db, half hh): source row 32 c + 8 grp + 4 hh + t, dims 16 a + 4 db ..
-  // (t = (lane % 16) / 4, a = lane % 4); byte offset within the tile, without the 4096 c of the step
+  // V fragment (step c, dim block db, half hh): source row 32 c + 8 grp + 4 hh + t, dims 16 db + 4 a ..
+  // (t = (lane % 16) / 4, a = lane % 4), i.e. half a % 2 of chunk 2 db + a / 2; byte offset within the tile,
+  // without the 4096 c of the step
   int vofs[2][4];
   {
     const int t = (lane & 15) >> 2, a = lane & 3;
@@ -151,7 +158,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int R = 8 * grp + 4 * hh + t;
-        vofs[hh][db] = R * 128 + 16 * ((2 * a + (db >> 1)) ^ vsw(R)) + 8 * (db & 1);
+        vofs[hh][db] = R * 128 + 16 * ((2 * db + (a >> 1)) ^ vsw(R)) + 8 * (a & 1);
       }
   }
   const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
@@ -274,20 +281,24 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     const float inv = 1.f / osum[qb][0];
     const int q = q0 + 32 * wave + 16 * qb + (lane & 15);
     const long row = rbase + q;
+    // yv[4 db + e] is dim 16 db + 4 grp + e
     float yv[16];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int e = 0; e < 4; ++e) yv[4 * db + e] = bf16r(o[qb][db][e] * inv);
-    // ordinary stores: each instruction covers half of every 128-byte line of the rows, which L2 merges
-    uint4* out = reinterpret_cast<uint4*>(g.y + row * g.ldy + h * HD + 16 * grp);
-    out[0] = make_uint4(pack2(yv[0], yv[1]), pack2(yv[2], yv[3]), pack2(yv[4], yv[5]), pack2(yv[6], yv[7]));
-    out[1] = make_uint4(pack2(yv[8], yv[9]), pack2(yv[10], yv[11]), pack2(yv[12], yv[13]), pack2(yv[14], yv[15]));
+    // ordinary stores: the four lane groups fill 32 bytes of each row per instruction, which L2 merges
+    bf16* out = g.y + row * g.ldy + h * HD + 4 * grp;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      *reinterpret_cast<uint2*>(out + 16 * db) = make_uint2(pack2(yv[4 * db], yv[4 * db + 1]), pack2(yv[4 * db + 2], yv[4 * db + 3]));
     if (g.upart) {
-      const float* br = g.b_proj + (long)dir * g.b_ld + h * HD + 16 * grp;
+      const float* br = g.b_proj + (long)dir * g.b_ld + h * HD + 4 * grp;
       float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) d += yv[e] * bf16r(br[e]);
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d += yv[4 * db + e] * bf16r(br[16 * db + e]);
       d += __shfl_xor(d, 16, 64);
       d += __shfl_xor(d, 32, 64);
       if (grp == 0) g.upart[row * g.upart_ld + h] = d;
@@ -308,8 +319,8 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     if ((lane & 15) == 0) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        smom[wave][0][16 * grp + e] = mom1[e];
-        smom[wave][1][16 * grp + e] = mom2[e];
+        smom[wave][0][16 * (e >> 2) + 4 * grp + (e & 3)] = mom1[e];
+        smom[wave][1][16 * (e >> 2) + 4 * grp + (e & 3)] = mom2[e];
       }
     }
     __syncthreads();
