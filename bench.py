@@ -295,8 +295,8 @@ def run_head(args):
 
     def step():
         _lib.call('noise_head_ce', h.data_ptr(), 1, gain.data_ptr(), wsplit.data_ptr(), V, 1, a.data_ptr(),
-                  b.data_ptr(), sign.data_ptr(), tgt.data_ptr(), P, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(),
-                  None, 0, s)
+                  b.data_ptr(), sign.data_ptr(), tgt.data_ptr(), 0, P, T, 1, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None,
+                  ws.data_ptr(), ws.numel(), None, 0, s)
     ms_step, ms_launch = _timed(step, args.steps, args.warmup)
     flop = 2 * D * V * P * T  # algorithmic fp32 head FLOPs (run as 3 bf16 MFMA passes)
     achieved = flop / (ms_launch * 1e-3) / 1e12

@@ -33,6 +33,12 @@ extern "C" {
 #define NOISE_FITNESS_ZSCORE 0 /* train/val/eggroll.py:151-152 */
 #define NOISE_FITNESS_RANK 1   /* centred ranks, ties by index (config-4 option) */
 
+/* Reductions of noise_head_ce's per-token losses. */
+#define NOISE_CE_MEMBER_MEAN 0 /* loss[members]: mean over each member's T tokens (train/val/eggroll.py:101-102) */
+#define NOISE_CE_NONE 1        /* loss[members*T] per token, 0 where the target is -1 (utils/model.py:205-208) */
+#define NOISE_CE_SUM 2         /* loss[1]: sum over the tokens whose target is not -1 */
+#define NOISE_CE_MEAN 3        /* loss[1]: that sum over their count (NaN when none is valid) */
+
 typedef void* noise_stream_t; /* hipStream_t */
 
 /* Layouts of a bf16 activation [rows, cols] exchanged between entry points. */
@@ -115,13 +121,16 @@ int noise_embed_norm(const float* w, long vocab, const float* a, const float* b,
  * residuals in pend (the previous block's attention and MLP c_proj outputs) are added to x_in, in order,
  * before the mix. */
 /* The embedding a block entry recomputes x0 from: x0 = norm(w[idx] + s a[dir, idx] b[dir]), the same
- * arithmetic as noise_embed_norm (bit-identical rows). */
+ * arithmetic as noise_embed_norm (bit-identical rows). Member p reads the token ids idx[p * idx_mstride ..
+ * + T): idx_mstride 0 for one sequence shared by all members (population_loss), T for one sequence per
+ * member (GPT.forward's batch rows, utils/model.py:193-196). */
 typedef struct noise_embed {
   const float* w; /* [vocab, 512] */
   long vocab;
   const float* a; /* [dirs, vocab] */
   const float* b; /* [dirs, 512] */
-  const int64_t* idx; /* [T] */
+  const int64_t* idx;
+  long idx_mstride;
 } noise_embed_t;
 /* x0 may be null when x0_embed is given (x0 rows recomputed: no stored [members*T, 512] fp32 x0 stream);
  * x_in may be null at block 0 (x_in = x0). */
@@ -133,7 +142,8 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
 
 /* q | k | v = lowrank(h, [W_q; W_k; W_v]) with per-segment a vectors and the u_qkv dots, then rotary +
  * QK RMSNorm on q and k (utils/model.py:55-58, :46-47; train/val/eggroll.py:90) and, when gate is not
- * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89). Output
+ * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89), member p reading the
+ * token ids idx[p * idx_mstride .. + T] (0: one shared sequence; T: a sequence per member). Output
  * [members*T, 1536] 16-bit (q | k | v, head h at columns h*64 of each segment): q and k bf16, v the
  * bf16-rounded value stored as fp16 (exact), the operand format of noise_attention.
  *   w_qkv    bf16 [1536, 512] = c_q ; c_k ; c_v
@@ -142,7 +152,7 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
 int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
               const float* u_qkv, const float* sign, int members, int T, int pair_shift, const void* rot_cos,
               const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
-              const float* ve_b, const int64_t* idx, void* qkv, noise_stream_t stream);
+              const float* ve_b, const int64_t* idx, long idx_mstride, void* qkv, noise_stream_t stream);
 
 /* Windowed causal attention on the q | k | v rows as noise_qkv writes them (q, k bf16; v fp16; 8 heads x 64):
  * y bf16 [members*T, 512]; a query at s
@@ -189,9 +199,13 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
                  const float* b_proj, const float* sign, int members, int T, int pair_shift, void* hidden,
                  int hidden_layout, float* upart, noise_stream_t stream);
 
-/* Per-member mean soft-capped cross-entropy (train/val/eggroll.py:94-103): h = norm(x) (times gain
- * when gain is not null: the config-3 extension; null reproduces utils/model.py:46-47);
- * z = h W^T + s (h . b) a; z' = 15 tanh(z / 15); loss[p] = mean_t(logsumexp(z'_t) - z'_t[target_t]).
+/* Soft-capped cross-entropy of the head (train/val/eggroll.py:94-103; utils/model.py:202-208): h = norm(x)
+ * (times gain when gain is not null: the config-3 extension; null reproduces utils/model.py:46-47);
+ * z = h W^T + s (h . b) a; z' = 15 tanh(z / 15); the token loss logsumexp(z'_t) - z'_t[target_t] reduced by
+ * `reduction` (NOISE_CE_*) into loss: the per-member mean of population_loss, or F.cross_entropy's
+ * 'none' / 'sum' / 'mean' with ignore_index = -1 (GPT.forward). Member p's targets are
+ * targets[p * tgt_mstride .. + T]. When logits is not null the capped logits z' are also written, fp32
+ * [members*T, vocab] (GPT.forward without targets); targets and loss may then both be null.
  *   x       [members*T, 512] fp32 (x_bf16 == 0) or bf16 (x_bf16 != 0)
  *   gain    [512] fp32 or null
  *   fp32_head != 0: w_head is the [vocab, 1536] split operand from noise_cast_bf16(split_cols = 512)
@@ -201,9 +215,9 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
  * pend are added to an fp32 x, in order, before the norm (the last block's c_proj outputs). */
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes);
 int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
-                  const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
-                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, const noise_pending_t* pend,
-                  int npend, noise_stream_t stream);
+                  const float* a, const float* b, const float* sign, const int64_t* targets, long tgt_mstride,
+                  int members, int T, int pair_shift, int reduction, float* loss, float* logits, void* workspace,
+                  size_t workspace_bytes, const noise_pending_t* pend, int npend, noise_stream_t stream);
 
 /* ---------------------------------------------------------------- EGGROLL update */
 

@@ -18,6 +18,7 @@ ERRORS = {-1: 'NOISE_EINVAL (rejected argument)', -2: 'NOISE_ENOSPC (workspace t
 
 FITNESS_ZSCORE, FITNESS_RANK = 0, 1
 LAYOUT_ROWS, LAYOUT_TILE16 = 0, 1
+CE_MEMBER_MEAN, CE_NONE, CE_SUM, CE_MEAN = 0, 1, 2, 3
 
 # name -> argtypes in declaration order; every entry point returns int. Pointers (device buffers,
 # the stream) are c_void_p.
@@ -30,7 +31,7 @@ SIGNATURES = {
     'noise_cast_bf16': [P, P, L, I, P],
     'noise_embed_norm': [P, L, P, P, P, P, I, I, I, P, P],
     'noise_block_entry': [P, P, P, P, P, P, P, P, P, P, P, P, L, P, P, P, P, P, I, I, I, P, I, P, P],
-    'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, P, P],
+    'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, L, P, P],
     'noise_attention_workspace_size': [I, I, SP],
     'noise_attention': [P, I, I, I, I, P, I, P, P, P, P, S, P],
     'noise_lowrank_resid': [P, P, I, I, P, P, I, L, L, P, I, I, I, P, P],
@@ -39,7 +40,7 @@ SIGNATURES = {
     'noise_mlp_fc_parts': [I],
     'noise_mlp_fc': [P, P, I, I, P, P, P, P, I, I, I, P, I, P, P],
     'noise_head_ce_workspace_size': [I, I, I, I, SP],
-    'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, I, I, I, P, P, S, P, I, P],
+    'noise_head_ce': [P, I, P, P, I, I, P, P, P, P, L, I, I, I, I, P, P, P, S, P, I, P],
     'noise_fitness': [P, I, I, I, P, P, P],
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
     'noise_outer_update_batch': [P, I, P, I, F, P],
@@ -61,12 +62,12 @@ def outer_mats(items):
 
 class Embed(ctypes.Structure):
     """noise_embed_t of include/noise_hip.h (the table a block entry recomputes x0 from)."""
-    _fields_ = [('w', P), ('vocab', L), ('a', P), ('b', P), ('idx', P)]
+    _fields_ = [('w', P), ('vocab', L), ('a', P), ('b', P), ('idx', P), ('idx_mstride', L)]
 
 
-def embed(w, vocab, a, b, idx):
+def embed(w, vocab, a, b, idx, idx_mstride=0):
     """A noise_embed_t (keep the returned object alive until the call is enqueued) and its pointer."""
-    e = Embed(w, vocab, a, b, idx)
+    e = Embed(w, vocab, a, b, idx, idx_mstride)
     return e, ctypes.cast(ctypes.pointer(e), P)
 
 

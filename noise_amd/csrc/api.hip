@@ -8,6 +8,10 @@
 #include "gemm.h"
 #include "rowops.h"
 
+static_assert(NOISE_CE_MEMBER_MEAN == CE_MEMBER_MEAN && NOISE_CE_NONE == CE_NONE && NOISE_CE_SUM == CE_SUM &&
+                  NOISE_CE_MEAN == CE_MEAN,
+              "reduction codes");
+
 namespace {
 
 // Bump allocator over the caller's workspace (256-byte aligned slices).
@@ -171,7 +175,10 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
   if (!x0 && !x0_embed) return NOISE_EINVAL;
   BlockEntryArgs g{};
-  if (!x0) g.emb = EmbedSrc{x0_embed->w, x0_embed->a, x0_embed->b, x0_embed->vocab, x0_embed->idx};
+  if (!x0) {
+    if (x0_embed->idx_mstride < 0) return NOISE_EINVAL;
+    g.emb = EmbedSrc{x0_embed->w, x0_embed->a, x0_embed->b, x0_embed->vocab, x0_embed->idx, x0_embed->idx_mstride};
+  }
   if (int rc = copy_pending(pend, npend, g.pend)) return rc;
   g.npend = npend;
   g.x_in = x_in;
@@ -201,8 +208,8 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
 int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a_k, const float* a_v,
               const float* u_qkv, const float* sign, int members, int T, int pair_shift, const void* rot_cos,
               const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
-              const float* ve_b, const int64_t* idx, void* qkv, noise_stream_t stream) {
-  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+              const float* ve_b, const int64_t* idx, long idx_mstride, void* qkv, noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift) || idx_mstride < 0) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(h, DM, (long)T * DM, w_qkv, DM, 3 * DM, a_q, sign, members, T, pair_shift);
   g.ra[1] = a_k;
   g.ra[2] = a_v;
@@ -221,6 +228,7 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
   g.ve_b = ve_b;
   g.ve_v = vocab;
   g.idx = idx;
+  g.tok_mstride = idx_mstride;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // q | k on the weight-resident kernel (rotary and the head RMSNorm in its epilogue), v (with the value
   // embedding) on the tile GEMM; both read the same h
@@ -345,12 +353,16 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
 }
 
 int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_head, int vocab, int fp32_head,
-                  const float* a, const float* b, const float* sign, const int64_t* targets, int members, int T,
-                  int pair_shift, float* loss, void* workspace, size_t workspace_bytes, const noise_pending_t* pend,
-                  int npend, noise_stream_t stream) {
+                  const float* a, const float* b, const float* sign, const int64_t* targets, long tgt_mstride,
+                  int members, int T, int pair_shift, int reduction, float* loss, float* logits, void* workspace,
+                  size_t workspace_bytes, const noise_pending_t* pend, int npend, noise_stream_t stream) {
   size_t need = 0;
   if (int rc = noise_head_ce_workspace_size(members, T, vocab, fp32_head, &need)) return rc;
-  if (bad_members(members, T, pair_shift) || !x || !w_head || !loss) return NOISE_EINVAL;
+  if (bad_members(members, T, pair_shift) || !x || !w_head || tgt_mstride < 0 || reduction < NOISE_CE_MEMBER_MEAN ||
+      reduction > NOISE_CE_MEAN)
+    return NOISE_EINVAL;
+  // targets and loss go together; without targets only the logits are produced
+  if (!targets ? (!logits || loss) : !loss) return NOISE_EINVAL;
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t M = (size_t)members * T;
@@ -370,12 +382,15 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   g.u_ld = 1;
   g.round_bf16 = fp32_head ? 0 : 1;
   g.targets = targets;
+  g.tok_mstride = tgt_mstride;
+  g.logits = logits;
   g.ce_tgt = tgt;
   g.upart_out = part;
   g.upart_ld = parts;
   g.ldo = vocab;
   if (int rc = lowrank_gemm_launch(EPI_CE, g, s)) return rc;
-  CeFinalizeArgs f{part, tgt, parts, members, T, loss};
+  if (!targets) return NOISE_OK;
+  CeFinalizeArgs f{part, tgt, parts, members, T, loss, targets, tgt_mstride, reduction};
   return ce_finalize_launch(f, s);
 }
 

@@ -75,10 +75,14 @@ struct LowrankGemmArgs {
   const float* ve_a;     // [dirs, V]
   const float* ve_b;     // [dirs, 512]
   long ve_v;             // V (row stride of ve_a)
-  const int64_t* idx;    // [T] token ids
-  // EPI_CE: targets [T]; partial sums of exp(z) [M, upart_ld]; z at the target [M]
+  const int64_t* idx;    // token ids: member p, position t reads idx[p * tok_mstride + t]
+  // EPI_CE: targets (member p, position t: targets[p * tok_mstride + t]; -1 = ignored; may be null when
+  // logits is set); partial sums of exp(z) [M, upart_ld]; z at the target [M]; optionally the capped logits
+  // z' fp32 [M, ldo]
   const int64_t* targets;
   float* ce_tgt;
+  long tok_mstride;      // 0: one sequence shared by every member; T: one sequence per member
+  float* logits;
 };
 
 // Number of per-row partials EPI_CE writes for an N-column output (0: N unsupported).

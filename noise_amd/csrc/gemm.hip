@@ -397,7 +397,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           for (int e = 0; e < CW; ++e) v[e] *= r;
         } else if (g.gate) {
           // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
-          const long tok = g.idx[t];
+          const long tok = g.idx[(long)p * g.tok_mstride + t];
           const float gt = g.gate[(long)rrow * 8 + scol / 64];
           const float sa = sgn * g.ve_a[(long)dir * g.ve_v + tok];
           const float* wr = g.ve_w + tok * 512 + scol;
@@ -428,14 +428,25 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         // 15 log2(e) - 30 log2(e) / (ez + 1); exp(z') = 2^zl. The reciprocal is the hardware one
         // (v_rcp_f32, 1 ulp): an IEEE division would cost ~10 VALU operations per logit.
         constexpr float L2E = 1.4426950408889634f;
-        const int te = (int)(g.targets[rrow % g.T] - cb);  // the target's column among the lane's CW, if any
+        // the target's column among the lane's CW, if any (a target of -1, or none, matches no column)
+        const long tk = g.targets ? g.targets[(long)p * g.tok_mstride + rrow % g.T] : -1;
+        const int te = tk < 0 ? -1 : (int)(tk - cb);
         float se = 0.f, zt = 0.f;
+        float* lg = g.logits && live ? g.logits + (long)row * g.ldo + cb : nullptr;
 #pragma unroll
-        for (int e = 0; e < CW; ++e) {
-          const float ez = __builtin_amdgcn_exp2f(v[e] * (2.f * L2E / 15.f));
-          const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
-          se += __builtin_amdgcn_exp2f(zl);
-          zt = e == te ? zl : zt;
+        for (int j = 0; j < FN; ++j) {
+          float zq[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float ez = __builtin_amdgcn_exp2f(v[4 * j + e] * (2.f * L2E / 15.f));
+            const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
+            se += __builtin_amdgcn_exp2f(zl);
+            zt = 4 * j + e == te ? zl : zt;
+            zq[e] = zl;
+          }
+          // the capped logits themselves (utils/model.py:203-204, returned when no targets are given)
+          if (lg) store_f4(lg + 4 * j, zq[0] * 0.6931471805599453f, zq[1] * 0.6931471805599453f,
+                           zq[2] * 0.6931471805599453f, zq[3] * 0.6931471805599453f);
         }
         if (live && te >= 0 && te < CW) g.ce_tgt[row] = zt * 0.6931471805599453f;
         se += __shfl_xor(se, 16, 64);
@@ -558,7 +569,9 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
         return NOISE_EINVAL;
       return launch_epi<EPI_QKV>(g, stream);
     case EPI_CE:
-      if (!g.targets || !g.ce_tgt || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N)) return NOISE_EINVAL;
+      if ((!g.targets && !g.logits) || !g.ce_tgt || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N) ||
+          (g.logits && g.ldo < g.N) || g.tok_mstride < 0)
+        return NOISE_EINVAL;
       return launch_epi<EPI_CE>(g, stream);
   }
   return NOISE_EINVAL;

@@ -33,7 +33,8 @@ struct EmbedSrc {
   const float* a;        // [dirs, V]
   const float* b;        // [dirs, 512]
   long V;
-  const int64_t* idx;    // [T]
+  const int64_t* idx;    // token ids: member p, position t reads idx[p * mstride + t]
+  long mstride;          // 0: every member reads the same T ids; T: one sequence per member
 };
 
 struct BlockEntryArgs {
@@ -88,11 +89,21 @@ struct HeadNormArgs {
   int npend;
 };
 
+// Reductions of the per-token losses logsumexp(z'_t) - z'_t[target_t].
+enum : int {
+  CE_MEMBER_MEAN = 0,  // loss[p] = mean over member p's T tokens (every target valid)
+  CE_NONE = 1,         // loss[row] per token; 0 where the target is -1 (ignored)
+  CE_SUM = 2,          // loss[0] = sum over the tokens whose target is not -1
+  CE_MEAN = 3,         // loss[0] = that sum / their count (NaN when every target is -1)
+};
 struct CeFinalizeArgs {
   const float* part;     // [members * T, parts] sums of exp(z)
-  const float* tgt;      // [members * T] z at the target
+  const float* tgt;      // [members * T] z at the target (written only where the target is valid)
   int parts, members, T;
-  float* loss;           // [members]
+  float* loss;           // [members] / [members * T] / [1] by reduction
+  const int64_t* targets;  // member p, position t: targets[p * tgt_mstride + t]
+  long tgt_mstride;
+  int reduction;
 };
 
 int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s);

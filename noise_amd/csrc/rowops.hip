@@ -71,9 +71,10 @@ __device__ __forceinline__ void add_pending(Row8& x, const Pending* pend, int np
 }
 
 // x0 = norm(W[idx] + s a[:, idx] b) (train/val/eggroll.py:61-63, :74).
-// x0 row t of member p (sign s, direction dir): norm(w[idx[t]] + s a[dir, idx[t]] b[dir]), 8 values per lane.
-__device__ __forceinline__ Row8 embed_row(const EmbedSrc& e, int t, int dir, float s, int lane) {
-  const long tok = e.idx[t];
+// x0 row t of member p (sign s, direction dir): norm(w[tok] + s a[dir, tok] b[dir]) with tok the member's
+// token id at position t, 8 values per lane.
+__device__ __forceinline__ Row8 embed_row(const EmbedSrc& e, int p, int t, int dir, float s, int lane) {
+  const long tok = e.idx[(long)p * e.mstride + t];
   const float sa = s * e.a[(long)dir * e.V + tok];
   Row8 w = load8(e.w + tok * D + lane * 8);
   const Row8 b = load8(e.b + (long)dir * D + lane * 8);
@@ -88,8 +89,8 @@ __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
   const int p = (int)(row / g.T), t = (int)(row % g.T), dir = p >> g.pair_shift;
-  const EmbedSrc e{g.w, g.a, g.b, g.V, g.idx};
-  store8(g.x0 + row * D + lane * 8, embed_row(e, t, dir, g.sign[p], lane));
+  const EmbedSrc e{g.w, g.a, g.b, g.V, g.idx, 0};
+  store8(g.x0 + row * D + lane * 8, embed_row(e, p, t, dir, g.sign[p], lane));
 }
 
 // Block entry (train/val/eggroll.py:77-88): x = (l_r + s e_r) x + (l_0 + s e_0) x0; h = norm(x);
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
   // x0: stored, or recomputed from the embedding (2 KiB gathered from an L2-resident table instead of 2 KiB
   // streamed from HBM); block 0 mixes x0 with itself
-  const Row8 x0 = g.x0 ? load8(g.x0 + row * D + lane * 8) : embed_row(g.emb, (int)(row % g.T), dir, s, lane);
+  const Row8 x0 = g.x0 ? load8(g.x0 + row * D + lane * 8) : embed_row(g.emb, p, (int)(row % g.T), dir, s, lane);
   Row8 x = g.x_in ? load8(g.x_in + row * D + lane * 8) : x0;
   add_pending(x, g.pend, g.npend, row, dir, s, lane);
 #pragma unroll
@@ -214,26 +215,54 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
   }
 }
 
-// Per-member mean cross-entropy (train/val/eggroll.py:101-102): row r's loss is
-// log(sum_j part[r, j]) - z[r, target]; one workgroup sums its member's T rows in a fixed order.
+// Cross-entropy of the soft-capped logits: row r's loss is log(sum_j part[r, j]) - z[r, target].
+__device__ __forceinline__ float ce_row_loss(const CeFinalizeArgs& g, long row) {
+  const float* pr = g.part + row * g.parts;
+  float s = 0.f;
+  for (int j = 0; j < g.parts; ++j) s += pr[j];
+  return __logf(s) - g.tgt[row];
+}
+// ignore_index = -1 (utils/model.py:206-207)
+__device__ __forceinline__ bool ce_row_valid(const CeFinalizeArgs& g, long row) {
+  return g.targets[(row / g.T) * g.tgt_mstride + row % g.T] != -1;
+}
+
+// CE_MEMBER_MEAN (population_loss, train/val/eggroll.py:101-102): workgroup p sums member p's T rows.
+// CE_NONE / CE_SUM / CE_MEAN (F.cross_entropy's reductions with ignore_index = -1, utils/model.py:205-208):
+// per row; or one workgroup sums every valid row. Each thread sums a fixed stride of rows, then a fixed
+// tree: the result does not depend on scheduling.
 __global__ void __launch_bounds__(256) ce_finalize_kernel(CeFinalizeArgs g) {
-  __shared__ float red[256];
-  const int p = blockIdx.x, tid = threadIdx.x;
-  float acc = 0.f;
-  for (int t = tid; t < g.T; t += 256) {
-    const long row = (long)p * g.T + t;
-    const float* pr = g.part + row * g.parts;
-    float s = 0.f;
-    for (int j = 0; j < g.parts; ++j) s += pr[j];
-    acc += __logf(s) - g.tgt[row];
+  __shared__ float red[256], cnt[256];
+  const int tid = threadIdx.x;
+  if (g.reduction == CE_NONE) {
+    const long row = (long)blockIdx.x * 256 + tid;
+    if (row < (long)g.members * g.T) g.loss[row] = ce_row_valid(g, row) ? ce_row_loss(g, row) : 0.f;
+    return;
+  }
+  const bool all = g.reduction != CE_MEMBER_MEAN;
+  const long r0 = all ? 0 : (long)blockIdx.x * g.T, n = all ? (long)g.members * g.T : g.T;
+  float acc = 0.f, c = 0.f;
+  for (long i = tid; i < n; i += 256) {
+    const long row = r0 + i;
+    if (!all || ce_row_valid(g, row)) {
+      acc += ce_row_loss(g, row);
+      c += 1.f;
+    }
   }
   red[tid] = acc;
+  cnt[tid] = c;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
+    if (tid < w) {
+      red[tid] += red[tid + w];
+      cnt[tid] += cnt[tid + w];
+    }
     __syncthreads();
   }
-  if (tid == 0) g.loss[p] = red[0] / (float)g.T;
+  if (tid == 0) {
+    if (!all) g.loss[blockIdx.x] = red[0] / (float)g.T;
+    else g.loss[0] = g.reduction == CE_SUM ? red[0] : red[0] / cnt[0];  // 0 / 0 = NaN, as torch's mean
+  }
 }
 
 // fp32 -> bf16 (round to nearest even); with split != 0 also writes [hi | lo | hi] rows of width
@@ -307,8 +336,13 @@ int head_norm_launch(const HeadNormArgs& g, hipStream_t s) {
 }
 
 int ce_finalize_launch(const CeFinalizeArgs& g, hipStream_t s) {
-  if (g.members <= 0 || g.T <= 0 || g.parts <= 0 || !g.part || !g.tgt || !g.loss) return NOISE_EINVAL;
-  hipLaunchKernelGGL(ce_finalize_kernel, dim3(g.members), dim3(256), 0, s, g);
+  if (g.members <= 0 || g.T <= 0 || g.parts <= 0 || !g.part || !g.tgt || !g.loss || g.reduction < CE_MEMBER_MEAN ||
+      g.reduction > CE_MEAN || (g.reduction != CE_MEMBER_MEAN && !g.targets))
+    return NOISE_EINVAL;
+  const long rows = (long)g.members * g.T;
+  const long grid = g.reduction == CE_MEMBER_MEAN ? g.members : g.reduction == CE_NONE ? (rows + 255) / 256 : 1;
+  if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
+  hipLaunchKernelGGL(ce_finalize_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }

@@ -2,8 +2,8 @@
 
 The module tree (names, shapes, parameter order) is the contract `utils/eval.py:24-31` loads with
 `strict=True`, so it is kept identical to `utils/model.py:61-147`. Compute never runs through these
-nn.Modules: `GPT.forward` dispatches to the population kernels with one member and sigma = 0
-(`noise_amd.population.clean_forward`).
+nn.Modules: `GPT.forward` dispatches to the population kernels with one member per batch row and
+sigma = 0 (`noise_amd.population.clean_forward`).
 """
 from dataclasses import dataclass
 
@@ -129,7 +129,7 @@ class GPT(nn.Module):
         self.cos, self.sin = cos[None, :, None, :], sin[None, :, None, :]
 
     def forward(self, idx, targets=None, loss_reduction='mean'):
-        """Clean forward (utils/model.py:193-210) on the HIP kernels: one member, sigma = 0."""
+        """Clean forward (utils/model.py:193-210) on the HIP kernels: one member per batch row, sigma = 0."""
         from .population import clean_forward
         return clean_forward(self, idx, targets, loss_reduction)
 

@@ -156,13 +156,29 @@ TIMER = _NoTimer()
 QK_NORM = True
 
 
-def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, windows):
-    """Losses of members 0..m-1 of `sign` (m = len(sign)) into out[0:m]; noise rows are indexed by
-    p >> pair_shift. Follows train/val/eggroll.py:72-103 op for op."""
+def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, windows, tok_mstride=0,
+                  reduction=_lib.CE_MEMBER_MEAN, logits=None):
+    """Losses of members 0..m-1 of `sign` (m = len(sign)) into `out` (per member, or reduced as
+    `reduction` says); noise rows are indexed by p >> pair_shift. Member p reads the token ids and targets
+    at p * tok_mstride (0: one shared sequence). When `logits` is given, the capped logits are written there
+    too (targets and out may then be None). Follows train/val/eggroll.py:72-103 op for op."""
     tm = TIMER
     cfg = W.config
     p = W.p
-    m, T = sign.shape[0], idx.shape[0]
+    m, T = sign.shape[0], idx.shape[-1]
+    # every launch below sizes its grid from (m, T): refuse anything the buffers or token ids do not cover
+    if not buf.fits(m, T):
+        raise ValueError(f'buffers hold {buf.members} members x {buf.T} tokens, not {m} x {T}')
+    ntok = T if tok_mstride == 0 else (m - 1) * tok_mstride + T
+    for name, t in (('idx', idx), ('targets', targets)):
+        if t is not None and (not t.is_contiguous() or t.numel() < ntok):
+            raise ValueError(f'{name} must be contiguous with >= {ntok} ids for {m} members x {T} tokens')
+    if logits is not None and (not logits.is_contiguous() or logits.numel() < m * T * W.head_w.shape[0]):
+        raise ValueError(f'logits must be contiguous [{m}, {T}, {W.head_w.shape[0]}]')
+    if out is not None:
+        nout = m * T if reduction == _lib.CE_NONE else m if reduction == _lib.CE_MEMBER_MEAN else 1
+        if out.numel() < nout:
+            raise ValueError(f'out must hold {nout} losses')
     s = _stream()
     ps = pair_shift
     a, b = noise['transformer.wte.weight']
@@ -170,7 +186,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     # x0 = norm(lowrank_embed(wte)) (train/val/eggroll.py:74) is never stored: every block entry recomputes its
     # rows from the L2-resident table (the same arithmetic as noise_embed_norm), which saves reading a 4 KiB
     # per member-token fp32 stream from HBM at each of the n_layer blocks
-    emb, emb_ptr = _lib.embed(_p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(idx))
+    emb, emb_ptr = _lib.embed(_p(p['transformer.wte.weight']), V, _p(a), _p(b), _p(idx), tok_mstride)
     eps_r, eps_0 = noise['resid_lambdas'], noise['x0_lambdas']
     lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
     # Deferred residuals. `x = x + lowrank(c_proj, ...)` (train/val/eggroll.py:92-93) is split: the c_proj GEMM
@@ -200,7 +216,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         t0 = tm.mark('qkv')
         _lib.call('noise_qkv', _p(buf.h), _p(W.qkv[i]), _p(aq), _p(ak), _p(av), _p(buf.u_qkv), _p(sign), m, T, ps,
                   _p(cos), _p(sin), _p(buf.gate) if ve else 0, _p(vw) if ve else 0, V, _p(va) if ve else 0,
-                  _p(vb) if ve else 0, _p(idx), _p(buf.qkv), s)
+                  _p(vb) if ve else 0, _p(idx), tok_mstride, _p(buf.qkv), s)
         tm.close(t0)
         ap, bp = noise[pre + 'attn.c_proj.weight']
         t0 = tm.mark('attention')
@@ -232,7 +248,8 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     t0 = tm.mark('head')
     pend, npend = _lib.pending(*pend_prev)
     _lib.call('noise_head_ce', _p(buf.x), 0, 0, _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
-              _p(targets), m, T, ps, _p(out), _p(buf.head_ws), buf.head_ws.numel(), pend, npend, s)
+              _p(targets), tok_mstride, m, T, ps, reduction, _p(out), _p(logits), _p(buf.head_ws), buf.head_ws.numel(),
+              pend, npend, s)
     tm.close(t0)
 
 
@@ -319,7 +336,51 @@ def population_loss(model, p, noise, sign, idx, targets, head='fp32', chunk=256)
     return Population(model, chunk=chunk, head=head).loss(p, noise, sign, idx, targets)
 
 
-def clean_forward(model, idx, targets=None, loss_reduction='mean'):
-    """GPT.forward (utils/model.py:193-210) is the P = 1, sigma = 0 case of the population forward; the
-    per-sequence token layout it needs is not wired into the kernels yet."""
-    raise NotImplementedError('GPT.forward on the HIP kernels is not available yet; use population_loss')
+REDUCTIONS = {'mean': _lib.CE_MEAN, 'sum': _lib.CE_SUM, 'none': _lib.CE_NONE}
+
+
+def clean_forward(model, idx, targets=None, loss_reduction='mean', head='fp32', weights=None):
+    """GPT.forward (utils/model.py:193-210) on the HIP kernels.
+
+    The clean model is the population forward at sigma = 0: the B batch rows run as B members in one pass,
+    member b reading its own sequence (token stride T), with zero signs, so every rank-1 term and every
+    lambda perturbation vanishes exactly. With targets, the loss is F.cross_entropy of the capped logits with
+    ignore_index = -1 and `loss_reduction` 'mean' / 'sum' (0-dim) or 'none' ([B * T]); without, the capped
+    fp32 logits [B, T, vocab] are returned. The GEMMs keep the autocast rounding points of the population
+    path; head='fp32' keeps the head fp32-accurate, 'bf16' rounds it as autocast does."""
+    if loss_reduction not in REDUCTIONS:
+        raise ValueError(f"loss_reduction must be one of {tuple(REDUCTIONS)}, got {loss_reduction!r}")
+    _need_cuda(idx, torch.int64, 'idx')
+    if idx.dim() != 2:
+        raise ValueError(f'idx must be [B, T], got {tuple(idx.shape)}')
+    B, T = idx.shape
+    if T % 128:
+        raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')
+    p = dict(model.named_parameters())
+    V = p['transformer.wte.weight'].shape[0]
+    if idx.min().item() < 0 or idx.max().item() >= V:
+        raise IndexError(f'token ids must lie in [0, {V})')
+    if targets is not None:
+        _need_cuda(targets, torch.int64, 'targets')
+        if targets.shape != idx.shape:
+            raise ValueError(f'targets must be {tuple(idx.shape)}, got {tuple(targets.shape)}')
+        valid = targets != -1
+        if ((targets < 0) & valid).any().item() or (targets >= V).any().item():
+            raise IndexError(f'targets must lie in [0, {V}) or be -1 (ignored)')
+    dev = idx.device
+    # sigma = 0: zero signs and zero noise rows (finite, so s * (x . b) * a is exactly zero)
+    noise = {n: (torch.zeros(B, t.shape[0], device=dev), torch.zeros(B, t.shape[1], device=dev)) if t.dim() == 2
+             else torch.zeros(B, t.shape[0], device=dev) for n, t in p.items()}
+    sign = torch.zeros(B, device=dev)
+    pop = Population(model, chunk=B, head=head)
+    W = weights or Weights(p, model.config, head)
+    cos, sin = pop.tables(T)
+    buf = pop.buffers(B, T, dev)
+    if targets is None:
+        logits = torch.empty(B, T, W.head_w.shape[0], device=dev, dtype=torch.float32)
+        forward_chunk(W, buf, noise, sign, idx, None, 0, None, cos, sin, pop.windows, tok_mstride=T, logits=logits)
+        return logits
+    red = REDUCTIONS[loss_reduction]
+    out = torch.empty(B * T if red == _lib.CE_NONE else 1, device=dev, dtype=torch.float32)
+    forward_chunk(W, buf, noise, sign, idx, targets, 0, out, cos, sin, pop.windows, tok_mstride=T, reduction=red)
+    return out if red == _lib.CE_NONE else out[0]

@@ -75,7 +75,14 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_fitness(1, 8, 4, 5, 1, 1, None) == EINVAL        # unknown mode
     assert lib.noise_adam(None, None, None, None, 10, 1e-3, .5, .95, 1e-8, 1.0, None) == EINVAL
     assert lib.noise_attention(1, 1, 100, 50, 0, None, 0, 1, None, None, None, 0, None) == EINVAL  # T % 128
-    assert lib.noise_head_ce(1, 0, None, 1, 4096, 1, 1, 1, 1, 1, 1, 256, 0, 1, None, 0, None, 0, None) == ENOSPC
+    head = lambda tgt, stride, red, loss, logits: lib.noise_head_ce(  # noqa: E731
+        1, 0, None, 1, 4096, 1, 1, 1, 1, tgt, stride, 1, 256, 0, red, loss, logits, None, 0, None, 0, None)
+    assert head(1, 0, 0, 1, None) == ENOSPC
+    assert head(1, 0, 4, 1, None) == EINVAL          # unknown reduction
+    assert head(1, -1, 1, 1, None) == EINVAL         # negative token stride
+    assert head(None, 0, 0, 1, None) == EINVAL       # a loss needs targets
+    assert head(None, 0, 0, None, None) == EINVAL    # nothing to produce
+    assert head(None, 256, 0, None, 1) == ENOSPC     # logits only
     assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
     assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
 

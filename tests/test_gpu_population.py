@@ -122,7 +122,7 @@ def test_block_entry_and_qkv_match_oracle():
               d['gb'].data_ptr(), gate.data_ptr(), d['sign'].data_ptr(), m, T, 0, None, 0, None, s)
     _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
               u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), gate.data_ptr(),
-              d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(), d['idx'].data_ptr(), qkv.data_ptr(), s)
+              d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(), d['idx'].data_ptr(), 0, qkv.data_ptr(), s)
     torch.cuda.synchronize()
     sg = sign[:, None, None]
     xr = (lam_r + sg * eps[0][:, 3, None, None]) * x + (lam_0 + sg * eps[1][:, 3, None, None]) * x0
@@ -159,7 +159,7 @@ def test_block_entry_and_qkv_match_oracle():
     qkv2 = torch.empty_like(qkv)
     _lib.call('noise_qkv', h.data_ptr(), wqkv16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(), d['av'].data_ptr(),
               u.data_ptr(), d['sign'].data_ptr(), m, T, 0, d['cos'].data_ptr(), d['sin'].data_ptr(), None,
-              None, V, None, None, None, qkv2.data_ptr(), s)
+              None, V, None, None, None, 0, qkv2.data_ptr(), s)
     torch.cuda.synchronize()
     assert torch.equal(qkv2[:, :1024].cpu(), qkv[:, :1024].cpu())
     v2 = qkv2[:, 1024:].cpu().view(torch.float16).float().view(m, T, 512)
@@ -334,7 +334,8 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
         ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV,
                          dtype=torch.uint8)
         _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
-                  sd.data_ptr(), td.data_ptr(), m, T, 0, loss.data_ptr(), ws.data_ptr(), ws.numel(), None, 0, s)
+                  sd.data_ptr(), td.data_ptr(), 0, m, T, 0, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None, ws.data_ptr(),
+                  ws.numel(), None, 0, s)
         torch.cuda.synchronize()
         if fp32:
             ref = om.head_loss(h, W, a, b, sign, targets, 'fp32', 'fp32')
@@ -362,7 +363,8 @@ def test_head_ce_config3_bf16_input_with_gain():
     loss = torch.empty(m, device=DEV)
     ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, 1), device=DEV, dtype=torch.uint8)
     _lib.call('noise_head_ce', hd.data_ptr(), 1, gd.data_ptr(), wd.data_ptr(), V, 1, ad.data_ptr(), bd.data_ptr(),
-              sd.data_ptr(), td.data_ptr(), m, T, 1, loss.data_ptr(), ws.data_ptr(), ws.numel(), None, 0, s)
+              sd.data_ptr(), td.data_ptr(), 0, m, T, 1, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None, ws.data_ptr(),
+              ws.numel(), None, 0, s)
     torch.cuda.synchronize()
     rep = lambda t: t.repeat_interleave(2, 0)  # noqa: E731
     ref = om.norm_head_ce(h.float(), gain, W, rep(a), rep(b), sign, targets)

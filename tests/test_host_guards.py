@@ -1,0 +1,58 @@
+"""Host-side guards of the forward: a shape the activation buffers or token ids do not cover is refused
+before any kernel is launched (CPU only; the library is never called)."""
+import types
+
+import pytest
+import torch
+
+from noise_amd import _lib, population
+
+
+class _Buf:
+    def __init__(self, members, T):
+        self.members, self.T = members, T
+
+    def fits(self, members, T):
+        return members <= self.members and T == self.T
+
+
+def _weights():
+    return types.SimpleNamespace(config=None, p={}, head_w=torch.empty(4096, 1))
+
+
+@pytest.fixture
+def no_launch(monkeypatch):
+    def refuse(*a, **k):
+        raise AssertionError('a kernel was launched')
+    monkeypatch.setattr(_lib, 'call', refuse)
+    monkeypatch.setattr(_lib, 'embed', refuse)
+
+
+def _run(buf, sign, idx, targets=None, out=None, tok_mstride=0, reduction=_lib.CE_MEMBER_MEAN, logits=None):
+    population.forward_chunk(_weights(), buf, {}, sign, idx, targets, 0, out, None, None, [], tok_mstride=tok_mstride,
+                             reduction=reduction, logits=logits)
+
+
+def test_flattened_batch_ids_are_refused(no_launch):
+    """[B * T] ids read as one sequence of B * T tokens would size every grid three times too large."""
+    B, T = 3, 256
+    with pytest.raises(ValueError, match='buffers hold'):
+        _run(_Buf(B, T), torch.zeros(B), torch.zeros(B * T, dtype=torch.int64), tok_mstride=T)
+
+
+def test_short_token_ids_and_outputs_are_refused(no_launch):
+    B, T = 3, 256
+    buf = _Buf(B, T)
+    with pytest.raises(ValueError, match='idx must'):
+        _run(buf, torch.zeros(B), torch.zeros(2, T, dtype=torch.int64), tok_mstride=T)
+    with pytest.raises(ValueError, match='targets must'):
+        _run(buf, torch.zeros(B), torch.zeros(B, T, dtype=torch.int64), torch.zeros(T, dtype=torch.int64),
+             tok_mstride=T)
+    with pytest.raises(ValueError, match='out must'):
+        _run(buf, torch.zeros(B), torch.zeros(B, T, dtype=torch.int64), torch.zeros(B, T, dtype=torch.int64),
+             out=torch.zeros(B), tok_mstride=T, reduction=_lib.CE_NONE)
+    with pytest.raises(ValueError, match='logits must'):
+        _run(buf, torch.zeros(B), torch.zeros(B, T, dtype=torch.int64), tok_mstride=T,
+             logits=torch.zeros(B, T, 100))
+    with pytest.raises(ValueError, match='buffers hold'):
+        _run(buf, torch.zeros(B + 1), torch.zeros(T, dtype=torch.int64))
