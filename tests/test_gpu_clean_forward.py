@@ -129,3 +129,20 @@ def test_clean_forward_sequences_and_logits_at_trained_scale():
     assert (lse - none.double()).abs().max() < 1e-4, float((lse - none.double()).abs().max())
     ref = _oracle_logits(params, idx)
     assert rel_err(logits, ref) < 1e-2, rel_err(logits, ref)
+
+
+def test_evaluate_score_matches_oracle_with_ragged_batches():
+    """utils/eval.py's evaluate: bf16 embedding storage, autocast head, fp64 sums over ragged batches."""
+    from noise_amd.eval import evaluate
+    model = make_model('cpu', 0)
+    sd = model.state_dict()
+    n, T = 4, 256
+    rows = torch.stack([torch.cat([i, t[-1:]]) for i, t in (zipf_tokens(T, seed=61 + r) for r in range(n))])
+    log_case(f'evaluate rows={n} T={T} batch 3')
+    got = evaluate(sd, rows=rows, batch_size=3)
+    params = {k: v.detach().clone() for k, v in model.named_parameters()}
+    for k in ['transformer.wte.weight'] + [k for k in params if k.startswith('value_embeds.')]:
+        params[k] = params[k].bfloat16().float()  # the reference's bf16 embedding storage on a GPU
+    ref = torch.cat([om.population_loss(params, _zero_noise(params), torch.zeros(1), r[:-1], r[1:], mode='bf16',
+                                        head='bf16') for r in rows]).double().mean()
+    assert abs(got - float(ref)) < 1e-4, (got, float(ref))
