@@ -198,8 +198,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
         m1 = fmaxf(m1, fmaxf(fmaxf(s[qb][kb + 1][0], s[qb][kb + 1][1]), fmaxf(s[qb][kb + 1][2], s[qb][kb + 1][3])));
       }
       float mx = fmaxf(m0, m1);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_rows4(mx);
       const bool move = mx * c2 > mref[qb] * c2 + LAZY;
       if (__any(move)) {
         const float mnew = move ? mx : mref[qb];
@@ -299,8 +298,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int e = 0; e < 4; ++e) d += yv[4 * db + e] * bf16r(br[16 * db + e]);
-      d += __shfl_xor(d, 16, 64);
-      d += __shfl_xor(d, 32, 64);
+      d = sum_rows4(d);
       if (grp == 0) g.upart[row * g.upart_ld + h] = d;
     }
 #pragma unroll

@@ -34,13 +34,61 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Butterfly reductions inside groups of lanes.
+// A DPP lane permutation of a float inside each row of 16 lanes (every lane reads a valid source).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i inside each 8
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i inside each 16
+
+// Sum over aligned groups of WIDTH lanes, every lane of a group receiving it. Inside a row of 16 lanes the
+// partial sums combine through DPP operands of the adds (after the two quad steps all lanes of a quad hold
+// its sum, so the mirrors pair whole quads, then whole halves); the four row sums of a 64-lane group meet
+// through v_readlane. No LDS permute: ds_bpermute costs an LDS round trip per step.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 || WIDTH == 64, "group width");
+  v += dpp_f32<DPP_QUAD_XOR1>(v);
+  if constexpr (WIDTH >= 4) v += dpp_f32<DPP_QUAD_XOR2>(v);
+  if constexpr (WIDTH >= 8) v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+  if constexpr (WIDTH >= 16) v += dpp_f32<DPP_ROW_MIRROR>(v);
+  if constexpr (WIDTH == 64) {
+    const int b = __float_as_int(v);
+    v = (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+        (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+  }
   return v;
 }
+// gfx950 VALU lane swaps. v_permlane32_swap(x, x) returns {x[l % 32], x[l % 32 + 32]} in lane l: the values of
+// the lower and the upper half-wave side by side; v_permlane16_swap(x, x) likewise {x of row 2 (r / 2),
+// x of row 2 (r / 2) + 1} for lane l of 16-lane row r. No LDS round trip (ds_bpermute) and no address VGPR.
+struct f32pair {
+  float lo, hi;
+};
+__device__ __forceinline__ f32pair halves32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ f32pair rowpair16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+// Sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows' lane l % 16), in the butterfly order
+// (x[r0] + x[r1]) + (x[r2] + x[r3]) in every lane.
+__device__ __forceinline__ float sum_rows4(float x) {
+  const f32pair a = rowpair16(x);
+  const f32pair b = halves32(a.lo + a.hi);
+  return b.lo + b.hi;
+}
+__device__ __forceinline__ float max_rows4(float x) {
+  const f32pair a = rowpair16(x);
+  const f32pair b = halves32(fmaxf(a.lo, a.hi));
+  return fmaxf(b.lo, b.hi);
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll

@@ -375,7 +375,8 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         // the wave's WN = 64 columns are one head; lane group lane / 16 holds head dims 16 (lane / 16) ..
         const int t = rrow % g.T;
         if (seg < 2) {
-          // rotary (utils/model.py:55-58): dims d and d + 32 pair up, held by lanes l and l ^ 32
+          // rotary (utils/model.py:55-58): dims d and d + 32 pair up, held by lanes l and l ^ 32 (exchanged by
+          // v_permlane32_swap)
           const int dd = (lane >> 4) * CW & 31;
           const bool first = (lane >> 4) < 2;
           const __bf16* cr = g.rot_cos + (long)t * 32 + dd;
@@ -383,15 +384,14 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           float ss = 0.f;
 #pragma unroll
           for (int e = 0; e < CW; ++e) {
-            const float partner = __shfl_xor(v[e], 32, 64);
+            const f32pair hv = halves32(v[e]);  // dims d (lanes 0-31) and d + 32 (lanes 32-63)
             const float c = (float)cr[e], sn = (float)sr[e];
-            const float y = first ? v[e] * c + partner * sn : v[e] * c - partner * sn;
+            const float y = first ? hv.lo * c + hv.hi * sn : hv.hi * c - hv.lo * sn;
             v[e] = y;
             ss += y * y;
           }
           // QK RMSNorm over the head's 64 dims (eps = 2^-23, utils/model.py:46-47)
-          ss += __shfl_xor(ss, 16, 64);
-          ss += __shfl_xor(ss, 32, 64);
+          ss = sum_rows4(ss);
           const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f);
 #pragma unroll
           for (int e = 0; e < CW; ++e) v[e] *= r;
@@ -449,8 +449,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
                            zq[2] * 0.6931471805599453f, zq[3] * 0.6931471805599453f);
         }
         if (live && te >= 0 && te < CW) g.ce_tgt[row] = zt * 0.6931471805599453f;
-        se += __shfl_xor(se, 16, 64);
-        se += __shfl_xor(se, 32, 64);
+        se = sum_rows4(se);
         if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = se;
       }
     }

@@ -34,7 +34,7 @@
 // accumulator set: the epilogue VALU work issues in the shadow of the MFMAs.
 //
 // h . b_next. Each lane holds 8 consecutive bf16 h of a row and the matching bf16(b_next) pairs: 4
-// v_dot2_f32_bf16 per row, two lane shuffles give the wave's 32-column partial, and the 8 wave partials of a
+// v_dot2_f32_bf16 per row, two VALU lane swaps (v_permlane16/32_swap) give the wave's 32-column partial, and the 8 wave partials of a
 // row are summed in LDS (fixed order) by wave 0, which stores one partial per (slice, row): upart_out is
 // part-major [N / 256][M], 128 contiguous bytes per block.
 #include <algorithm>
@@ -308,14 +308,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pv = __shfl_xor(ev_v[i][e], 32, 64);
+          const f32pair hv = halves32(ev_v[i][e]);  // dims d (lane groups 0, 1) and d + 32 (groups 2, 3)
           const float cv = (float)ev_cs[i][0][e], sv = (float)ev_cs[i][1][e];
-          const float y = first ? ev_v[i][e] * cv + pv * sv : ev_v[i][e] * cv - pv * sv;
+          const float y = first ? hv.lo * cv + hv.hi * sv : hv.hi * cv - hv.lo * sv;
           ev_v[i][e] = y;
           ss += y * y;
         }
-        ss += __shfl_xor(ss, 16, 64);
-        ss += __shfl_xor(ss, 32, 64);
+        ss = sum_rows4(ss);
         ev_ss[i] = ss;
         if (grp == 0) ssq[pk & 1][16 * i + r][wave] = ss;
       }
@@ -370,9 +369,11 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       bf16* dst = g.out_tiled ? g.out_bf16 + (row - r) * g.ldo + (fw >> 5) * 512 + 8 * (4 * r + (grp ^ ((r >> 1) & 3)))
                               : g.out_bf16 + row * g.ldo + fw + 8 * grp;
       store_stream_x4(dst, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
-      ev_dot[i] += __shfl_xor(ev_dot[i], 16, 64);
+      const f32pair a = rowpair16(ev_dot[i]);  // rows 0 + 1 and 2 + 3 of the 16-lane rows
+      ev_dot[i] = a.lo + a.hi;
     } else {
-      ev_dot[i] += __shfl_xor(ev_dot[i], 32, 64);
+      const f32pair b = halves32(ev_dot[i]);
+      ev_dot[i] = b.lo + b.hi;
       red[pk & 1][lr][wave] = ev_dot[i];  // the row's four lanes write the same value
     }
   };
