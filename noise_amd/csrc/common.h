@@ -116,6 +116,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 __device__ __forceinline__ void store_stream_x4(void* p, u32x4 v) {
   asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
+// The same store at a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void store_stream_x4_s(void* base, unsigned voff, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, %2 nt\n\ts_nop 1" : : "v"(voff), "v"(v), "s"(base) : "memory");
+}
 __device__ __forceinline__ void store_stream_x4(void* p, unsigned a, unsigned b, unsigned c, unsigned d) {
   store_stream_x4(p, u32x4{a, b, c, d});
 }

@@ -91,6 +91,16 @@ __device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
                : "v"(src), "s"(off)
                : "memory");
 }
+// The same load from a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset: the address arithmetic
+// stays on the scalar unit and the offset VGPR is computed once.
+__device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(voff), "s"(base), "s"(off)
+               : "memory");
+}
 __device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
   const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
   unsigned saved;
@@ -128,7 +138,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   __shared__ __attribute__((aligned(16))) float ssq[2][R][NW];  // q|k: per-row partial sums of squares
   __shared__ __attribute__((aligned(16))) float qpad[R][4];     // q|k: landing area of the padding loads
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
+  // the wave index is uniform: keeping it in an SGPR keeps every per-wave address on the scalar unit
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), grp = lane >> 4;
   const int nslices = g.N / BN;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int streams = (gridDim.x >> 3) / nslices;
@@ -162,33 +173,47 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // ---- loads of block k into ring slot k % NBUF. Wave w fills x rows 4 w + q: lane L loads k 8 L .. 8 L + 7.
   // Lanes 0-7 load a_p, 8-15 b_next over the wave's 32 columns, 16-23 the block's 32 input-side dots; lane 0
   // the member's sign.
+  // Blocks are issued in order k = 0, 1, 2, ...: the next one's first row, member and token advance by
+  // streams * R rows per call (no integer division per block).
+  int nx_row = blk_of(0) * R;
+  int nx_p = nx_row / g.T, nx_t0 = nx_row - nx_p * g.T;
+  const int step_rows = streams * R;
+  const unsigned lane16 = 16u * lane;  // the lane's byte offset in a 1 KiB row load
   auto issue = [&](int k) {
-    const int buf = k % NBUF, row0 = blk_of(k) * R;
-    const int p = row0 / g.T, t0 = row0 - p * g.T, dir = p >> g.pair_shift;
-    const bf16* abase = g.A + (long)p * g.a_mstride + (long)(t0 + 4 * wave) * g.lda + 8 * lane;
+    const int buf = k % NBUF, row0 = nx_row, p = nx_p, t0 = nx_t0, dir = p >> g.pair_shift;
+    nx_row += step_rows;
+    nx_t0 += step_rows;
+    while (nx_t0 >= g.T) {
+      nx_t0 -= g.T;
+      ++nx_p;
+    }
+    const char* xb = reinterpret_cast<const char*>(g.A + (long)p * g.a_mstride + (long)(t0 + 4 * wave) * g.lda);
     char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_x4(abase + q * g.lda, xsl + q * XROW);
+    for (int q = 0; q < 4; ++q) dma_x4_s(xb + (long)q * g.lda * 2, lane16, xsl + q * XROW);
+    // u_qkv rows of the block: 16 bytes per row (lanes 0-31)
+    const float* urows = g.u + (long)row0 * 4;
     if constexpr (VV) {
       // a over the wave's 32 columns (lanes 0-7); wave 4: the block's u_qkv rows, the others the same rows
       // into a padding area (every wave issues DMA_PER_BLOCK loads per block)
-      if (lane < 8) dma_x4(g.ra[2] + (long)dir * g.ra_ld + fw + 4 * lane, &qv[buf].av[wave][0]);
-      if (lane < R) dma_x4(g.u + (long)(row0 + lane) * 4, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
+      if (lane < 8) dma_x4_s(g.ra[2] + (long)dir * g.ra_ld + fw, lane16, &qv[buf].av[wave][0]);
+      if (lane < R) dma_x4_s(urows, lane16, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
       return;
     }
     if constexpr (QK) {
       // a over the wave's columns (lanes 0-7: two 64-byte runs of dims); then wave 0-3: cos / sin rows
       // (1 KiB each), wave 4: the block's u_qkv rows, waves 5-7: the same rows into a padding area (every
       // wave issues DMA_PER_BLOCK loads per block)
+      // lanes 0-3: dims qk_col(.., 0 .. 15), lanes 4-7: qk_col(.., 16 .. 31) = the first run + 32
       const int seg = nslice >> 1;
       if (lane < 8)
-        dma_x4(g.ra[seg] + (long)dir * g.ra_ld + qk_col(nslice, wave, 16 * (lane >> 2)) - seg * 512 + 4 * (lane & 3),
-               &qv[buf].av[wave][0]);
+        dma_x4_s(g.ra[seg] + (long)dir * g.ra_ld + qk_col(nslice, wave, 0) - seg * 512, 128u * (lane >> 2) + 16u * (lane & 3),
+                 &qv[buf].av[wave][0]);
       if (wave < 4) {
         const bf16* tab = (wave >> 1) ? g.rot_sin : g.rot_cos;
-        dma_x4(tab + (long)(t0 + 16 * (wave & 1)) * 32 + 8 * lane, &qv[buf].cs[wave >> 1][16 * (wave & 1)][0]);
+        dma_x4_s(tab + (long)(t0 + 16 * (wave & 1)) * 32, lane16, &qv[buf].cs[wave >> 1][16 * (wave & 1)][0]);
       } else if (lane < R) {
-        dma_x4(g.u + (long)(row0 + lane) * 4, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
+        dma_x4_s(urows, lane16, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
       }
       return;
     }
@@ -224,6 +249,16 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   float ev_v[2][8], ev_ss[2];   // q|k: rotated values and the wave's sums of squares per row half
   bf16x8 ev_cs[2][2];           // q|k: cos / sin of the lane's 8 dims for rows r, r + 16
   const int qk_ocol = QK ? qk_col(nslice, wave, 8 * grp) : 0;  // the lane's first output column
+  // Stores of a row half go to a uniform base (the half's first row, the wave's first column) plus a per-lane
+  // byte offset fixed for the kernel: row lane % 16, the lane's 8 columns.
+  const int col0 = QK ? qk_col(nslice, wave, 0) : fw;
+  const unsigned st_off = 2u * (unsigned)((lane & 15) * g.ldo + (QK ? qk_ocol - col0 : 8 * grp));
+  // TILE16 (c_fc h): the half's 1 KiB tile of the wave's 32 columns, 16-byte unit 4 r + (grp ^ ((r / 2) % 4))
+  const unsigned tile_off = 16u * (unsigned)(4 * (lane & 15) + (grp ^ (((lane & 15) >> 1) & 3)));
+  auto half_base = [&](int blk, int i) { return g.out_bf16 + ((long)blk * R + 16 * i) * g.ldo + col0; };
+  auto store_half = [&](int blk, int i, u32x4 v) {
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(half_base(blk, i)) + st_off) = v;
+  };
 
   // Stage st (0 .. 15) of the epilogue of block pk (ring slot pbuf) from acc:
   //   0: vectors from LDS; 1-4 / 7-10: column pairs of row half 0 / 1; 5 / 11: h store and first shuffle;
@@ -255,8 +290,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         _Float16 __attribute__((ext_vector_type(2))) hp = {(_Float16)bf16r(v0), (_Float16)bf16r(v1)};
         ev_h[i][sub] = *reinterpret_cast<unsigned*>(&hp);
       } else {
-        const long row = (long)blk_of(pk) * R + 16 * i + r;
-        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
+        store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       }
       return;
     }
@@ -276,8 +310,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = pack_bf16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
-        const long row = (long)blk_of(pk - 1) * R + 16 * i + r;
-        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + qk_ocol) = o;
+        store_half(blk_of(pk - 1), i, o);
         return;
       }
       if (pk < 0 || st > 12) return;
@@ -328,8 +361,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         const int j = sub >> 1, e0 = (sub & 1) * 2;
         ev_h[i][sub] = pack_bf16(acc[i][j][e0], acc[i][j][e0 + 1]);
       } else {
-        const long row = (long)blk_of(pk) * R + 16 * i + (lane & 15);
-        *reinterpret_cast<u32x4*>(g.out_bf16 + row * g.ldo + fw + 8 * grp) = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
+        store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       }
       return;
     }
@@ -364,11 +396,11 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     } else if (sub == 4) {
       // row-major: 16 rows x 64 bytes per instruction; TILE16: one contiguous 1 KiB tile (16 rows, the
       // wave's 32 columns), eight whole 128-byte lines
-      const long row = (long)blk_of(pk) * R + lr;
-      const int r = lane & 15;
-      bf16* dst = g.out_tiled ? g.out_bf16 + (row - r) * g.ldo + (fw >> 5) * 512 + 8 * (4 * r + (grp ^ ((r >> 1) & 3)))
-                              : g.out_bf16 + row * g.ldo + fw + 8 * grp;
-      store_stream_x4(dst, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+      const u32x4 hv = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
+      if (g.out_tiled)
+        store_stream_x4_s(g.out_bf16 + ((long)blk_of(pk) * R + 16 * i) * g.ldo + (fw >> 5) * 512, tile_off, hv);
+      else
+        store_stream_x4_s(half_base(blk_of(pk), i), st_off, hv);
       const f32pair a = rowpair16(ev_dot[i]);  // rows 0 + 1 and 2 + 3 of the 16-lane rows
       ev_dot[i] = a.lo + a.hi;
     } else {
