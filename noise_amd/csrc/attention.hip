@@ -45,21 +45,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
 __device__ __forceinline__ f32x4 mfma16x16x32_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// global_load_lds_dwordx4: each lane's 16 bytes land at lds + 16 * lane. M0 is saved and restored.
-__device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
-  unsigned saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(src), "s"(off)
-               : "memory");
 }
 
 // K tile [BKV keys][64 dims] bf16, 128-byte rows, 16-byte chunks XOR-swizzled by row.
@@ -91,7 +80,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
   __shared__ float smom[NWAVE][2][HD];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), grp = lane >> 4;
   // XCD-aware order. Workgroups reach the 8 XCDs round-robin (workgroup b runs on XCD b % 8), so XCD x takes
   // a contiguous range of logical indices n: the query blocks of one (member, head) run together on one XCD
   // and read its K/V through that XCD's L2 once from HBM. Heavier (later) query blocks first.
@@ -118,20 +107,23 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
 
   // ---- loads of key block j into ring slot buf: 8 K and 8 V instructions of 1 KiB, 2 + 2 per wave.
   // Instruction d fills LDS rows 8 d .. 8 d + 7; lane L -> row R = 8 d + L / 8, physical chunk L % 8.
+  // The block's first key row is a wave-uniform base (SGPRs); each lane's byte offset from it is fixed.
   const int lrow = lane >> 3, lchunk = lane & 7;
+  unsigned koffs[DH], voffs[DH];
+#pragma unroll
+  for (int q = 0; q < DH; ++q) {
+    const int R = 8 * (DH * wave + q) + lrow;
+    koffs[q] = 2u * (unsigned)(key_of_krow(R) * g.ldq + kcol + 8 * (lchunk ^ (R & 7)));
+    voffs[q] = 2u * (unsigned)(R * g.ldq + vcol + 8 * (lchunk ^ vsw(R)));
+  }
   auto issue = [&](int j, int buf) {
-    const long kr0 = rbase + (long)j * BKV;
+    const bf16* kv0 = qkv + (rbase + (long)j * BKV) * g.ldq;
 #pragma unroll
-    for (int q = 0; q < DH; ++q) {
-      const int d = DH * wave + q, R = 8 * d + lrow;
-      dma_x4(qkv + (kr0 + key_of_krow(R)) * g.ldq + kcol + 8 * (lchunk ^ (R & 7)),
-             reinterpret_cast<const char*>(sk[buf]) + d * 1024);
-    }
+    for (int q = 0; q < DH; ++q)
+      dma_x4_s(kv0, koffs[q], reinterpret_cast<const char*>(sk[buf]) + (DH * wave + q) * 1024);
 #pragma unroll
-    for (int q = 0; q < DH; ++q) {
-      const int d = DH * wave + q, R = 8 * d + lrow;
-      dma_x4(qkv + (kr0 + R) * g.ldq + vcol + 8 * (lchunk ^ vsw(R)), reinterpret_cast<const char*>(sv[buf]) + d * 1024);
-    }
+    for (int q = 0; q < DH; ++q)
+      dma_x4_s(kv0, voffs[q], reinterpret_cast<const char*>(sv[buf]) + (DH * wave + q) * 1024);
   };
 
   const float c2 = 0.125f * 1.4426950408889634f;  // scores -> log2 units: 1/sqrt(64) * log2(e)

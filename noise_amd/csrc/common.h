@@ -116,6 +116,38 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 __device__ __forceinline__ void store_stream_x4(void* p, u32x4 v) {
   asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
+// Direct global -> LDS loads, issued from inline assembly (the compiler would otherwise make every later LDS
+// read wait for every outstanding LDS-bound load). The kernels wait for them themselves: vector memory
+// operations complete in issue order.
+typedef __attribute__((address_space(3))) void lds_void_t;
+// global_load_lds_dword{x4}: each active lane's bytes land at lds + size * lane. M0 is saved and restored.
+__device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(src), "s"(off)
+               : "memory");
+}
+// The same load from a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset: the address arithmetic
+// stays on the scalar unit and the offset VGPR is computed once.
+__device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(voff), "s"(base), "s"(off)
+               : "memory");
+}
+__device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(src), "s"(off)
+               : "memory");
+}
+
 // The same store at a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset.
 __device__ __forceinline__ void store_stream_x4_s(void* base, unsigned voff, u32x4 v) {
   asm volatile("global_store_dwordx4 %0, %1, %2 nt\n\ts_nop 1" : : "v"(voff), "v"(v), "s"(base) : "memory");

@@ -41,7 +41,6 @@
 
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
 struct Cfg {

@@ -44,8 +44,6 @@
 
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
 constexpr int R = 32;                 // rows per block
 constexpr int NBUF = 4;               // LDS ring depth (blocks)
 constexpr int NW = 8;                 // waves per workgroup
@@ -80,34 +78,6 @@ template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(N >= 0 && N <= 63, "vmcnt");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
-}
-
-// global_load_lds_dword{x4}: each active lane's bytes land at lds + size * lane. M0 is saved and restored.
-__device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
-  unsigned saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(src), "s"(off)
-               : "memory");
-}
-// The same load from a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset: the address arithmetic
-// stays on the scalar unit and the offset VGPR is computed once.
-__device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
-  unsigned saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(voff), "s"(base), "s"(off)
-               : "memory");
-}
-__device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
-  unsigned saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved)
-               : "v"(src), "s"(off)
-               : "memory");
 }
 
 __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
