@@ -43,45 +43,84 @@ __device__ __forceinline__ void rms_norm_row(Row8& r) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) r.v[e] *= s;
 }
-// bf16(sum_c bf16(h_c) bf16(b_c)) over the row: the autocast rank-1 GEMV.
-__device__ __forceinline__ float dot_bf16(const Row8& h, const float* b) {
-  const Row8 bv = load8(b);
+// A row's 8 values of a lane rounded to bf16 (round to nearest even) as 4 packed pairs: the GEMM operand that
+// is stored, and the operand of the rank-1 dots.
+struct RowBf {
+  unsigned p[4];
+};
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
+  bf16x2 p = {to_bf16(a), to_bf16(b)};
+  return *reinterpret_cast<unsigned*>(&p);
+}
+__device__ __forceinline__ RowBf pack_row(const Row8& r) {
+  return RowBf{{pack_bf16x2(r.v[0], r.v[1]), pack_bf16x2(r.v[2], r.v[3]), pack_bf16x2(r.v[4], r.v[5]),
+                pack_bf16x2(r.v[6], r.v[7])}};
+}
+__device__ __forceinline__ void store_bf(bf16* p, const RowBf& h) { store_stream_x4(p, h.p[0], h.p[1], h.p[2], h.p[3]); }
+// bf16(sum_c bf16(h_c) bf16(b_c)) over the row: the autocast rank-1 GEMV, on v_dot2_f32_bf16 (exact bf16
+// products, fp32 accumulation).
+__device__ __forceinline__ float dot_bf16(const RowBf& h, const Row8& bv) {
   float acc = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc += bf16r(h.v[e]) * bf16r(bv.v[e]);
+  for (int e = 0; e < 4; ++e)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, h.p[e]),
+                                          __builtin_bit_cast(bf16x2, pack_bf16x2(bv.v[2 * e], bv.v[2 * e + 1])), acc,
+                                          false);
   return bf16r(group_sum<64>(acc));
 }
 
 // x += the deferred c_proj outputs (`x = x + lowrank(...)`, train/val/eggroll.py:92-93): the same fp32
 // operations the GEMM epilogue would have done, v = fma(s bf16(u), a, bf16 dense) then x + v, in order.
-__device__ __forceinline__ void add_pending(Row8& x, const Pending* pend, int npend, long row, int dir, float s,
-                                            int lane) {
-  for (int k = 0; k < npend; ++k) {
-    const Pending& pd = pend[k];
-    const bf16x8 yv = *reinterpret_cast<const bf16x8*>(pd.y + row * D + lane * 8);
-    // lane q loads partial q; the sum runs q = 0, 1, ... on the broadcast values (a fixed order)
-    const float uq = lane < pd.u_parts ? pd.u[row * pd.u_ld + lane * pd.u_qstride] : 0.f;
-    float u = 0.f;
-    for (int q = 0; q < pd.u_parts; ++q) u += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uq), q));
-    const float su = s * bf16r(u);
-    const Row8 a = load8(pd.a + (long)dir * D + lane * 8);
+// Loads and arithmetic are split: every pending row, partial and vector of a row is loaded before any is
+// used, so a row waits for one memory round trip instead of one per deferred residual.
+struct PendRow {
+  bf16x8 y[MAX_PENDING];
+  float uq[MAX_PENDING];  // lane q: partial q
+  Row8 a[MAX_PENDING];
+};
+__device__ __forceinline__ void load_pending(PendRow& L, const Pending* pend, int npend, long row, int dir, int lane) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x.v[e] = x.v[e] + fmaf(su, a.v[e], (float)yv[e]);
+  for (int k = 0; k < MAX_PENDING; ++k) {
+    if (k < npend) {
+      const Pending& pd = pend[k];
+      L.y[k] = *reinterpret_cast<const bf16x8*>(pd.y + row * D + lane * 8);
+      L.uq[k] = lane < pd.u_parts ? pd.u[row * pd.u_ld + lane * pd.u_qstride] : 0.f;
+      L.a[k] = load8(pd.a + (long)dir * D + lane * 8);
+    }
+  }
+}
+__device__ __forceinline__ void add_pending(Row8& x, const PendRow& L, const Pending* pend, int npend, float s) {
+#pragma unroll
+  for (int k = 0; k < MAX_PENDING; ++k) {
+    if (k < npend) {
+      // the sum runs q = 0, 1, ... on the broadcast partials (a fixed order)
+      const int parts = pend[k].u_parts;
+      float u = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q < parts) u += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L.uq[k]), q));
+      for (int q = 8; q < parts; ++q) u += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L.uq[k]), q));
+      const float su = s * bf16r(u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x.v[e] = x.v[e] + fmaf(su, L.a[k].v[e], (float)L.y[k][e]);
+    }
   }
 }
 
 // x0 = norm(W[idx] + s a[:, idx] b) (train/val/eggroll.py:61-63, :74).
 // x0 row t of member p (sign s, direction dir): norm(w[tok] + s a[dir, tok] b[dir]) with tok the member's
 // token id at position t, 8 values per lane.
-__device__ __forceinline__ Row8 embed_row(const EmbedSrc& e, int p, int t, int dir, float s, int lane) {
-  const long tok = e.idx[(long)p * e.mstride + t];
+__device__ __forceinline__ Row8 embed_finish(const EmbedSrc& e, long tok, int dir, float s, const Row8& b, int lane) {
   const float sa = s * e.a[(long)dir * e.V + tok];
   Row8 w = load8(e.w + tok * D + lane * 8);
-  const Row8 b = load8(e.b + (long)dir * D + lane * 8);
 #pragma unroll
   for (int k = 0; k < 8; ++k) w.v[k] = w.v[k] + sa * b.v[k];
   rms_norm_row(w);
   return w;
+}
+__device__ __forceinline__ Row8 embed_row(const EmbedSrc& e, int p, int t, int dir, float s, int lane) {
+  const long tok = e.idx[(long)p * e.mstride + t];
+  return embed_finish(e, tok, dir, s, load8(e.b + (long)dir * D + lane * 8), lane);
 }
 
 __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
@@ -99,23 +138,40 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
-  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  const int p = (int)(row / g.T), t = (int)(row % g.T), dir = p >> g.pair_shift;
+  // Every load that depends on no other is issued first (the row then waits for its longest chain of dependent
+  // loads, the token id before the embedding row, not for the sum of all of them).
+  // x0: stored, or recomputed from the embedding (2 KiB gathered from an L2-resident table instead of 2 KiB
+  // streamed from HBM); block 0 mixes x0 with itself
+  const bool recompute = !g.x0;
+  long tok = 0;
+  Row8 x0, xin, eb, bqkv[3];
+  if (recompute) {
+    tok = g.emb.idx[(long)p * g.emb.mstride + t];
+    eb = load8(g.emb.b + (long)dir * D + lane * 8);
+  } else {
+    x0 = load8(g.x0 + row * D + lane * 8);
+  }
+  if (g.x_in) xin = load8(g.x_in + row * D + lane * 8);
+  PendRow pr;
+  load_pending(pr, g.pend, g.npend, row, dir, lane);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) bqkv[k] = load8(g.b_qkv[k] + (long)dir * D + lane * 8);
   const float s = g.sign[p];
   const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
-  // x0: stored, or recomputed from the embedding (2 KiB gathered from an L2-resident table instead of 2 KiB
-  // streamed from HBM); block 0 mixes x0 with itself
-  const Row8 x0 = g.x0 ? load8(g.x0 + row * D + lane * 8) : embed_row(g.emb, p, (int)(row % g.T), dir, s, lane);
-  Row8 x = g.x_in ? load8(g.x_in + row * D + lane * 8) : x0;
-  add_pending(x, g.pend, g.npend, row, dir, s, lane);
+  if (recompute) x0 = embed_finish(g.emb, tok, dir, s, eb, lane);
+  Row8 x = g.x_in ? xin : x0;
+  add_pending(x, pr, g.pend, g.npend, s);
 #pragma unroll
   for (int e = 0; e < 8; ++e) x.v[e] = lr * x.v[e] + l0 * x0.v[e];
   store8(g.x_out + row * D + lane * 8, x);
   rms_norm_row(x);
-  store8_bf16(g.h + row * D + lane * 8, x);
+  const RowBf hb = pack_row(x);
+  store_bf(g.h + row * D + lane * 8, hb);
   float u[3];
 #pragma unroll
-  for (int k = 0; k < 3; ++k) u[k] = dot_bf16(x, g.b_qkv[k] + (long)dir * D + lane * 8);
+  for (int k = 0; k < 3; ++k) u[k] = dot_bf16(hb, bqkv[k]);
   if (lane == 0) {
     float* ur = g.u_qkv + row * 4;
     ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = s;  // the member's sign rides with the dots
@@ -163,10 +219,14 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
   if (row >= g.M) return;
   const int p = (int)(row / g.T), dir = p >> g.pair_shift;
   Row8 x = load8(g.x + row * D + lane * 8);
-  if (g.npend) add_pending(x, g.pend, g.npend, row, dir, g.sign[p], lane);
+  PendRow pr;
+  load_pending(pr, g.pend, g.npend, row, dir, lane);
+  const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
+  if (g.npend) add_pending(x, pr, g.pend, g.npend, g.sign[p]);
   rms_norm_row(x);
-  store8_bf16(g.h + row * D + lane * 8, x);
-  const float u = dot_bf16(x, g.b + (long)dir * D + lane * 8);
+  const RowBf hb = pack_row(x);
+  store_bf(g.h + row * D + lane * 8, hb);
+  const float u = dot_bf16(hb, bv);
   if (lane == 0) g.u[row] = u;
 }
 
@@ -186,7 +246,9 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     for (int e = 0; e < 8; ++e) x.v[e] = (float)xv[e];
   } else {
     x = load8(static_cast<const float*>(g.x) + row * D + lane * 8);
-    if (g.npend) add_pending(x, g.pend, g.npend, row, dir, g.sign[p], lane);
+    PendRow pr;
+    load_pending(pr, g.pend, g.npend, row, dir, lane);
+    if (g.npend) add_pending(x, pr, g.pend, g.npend, g.sign[p]);
   }
   rms_norm_row(x);
   if (g.gain) {
@@ -209,17 +271,23 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     acc = group_sum<64>(acc);
     if (lane == 0) g.u[row] = acc;
   } else {
-    store8_bf16(g.h + row * D + lane * 8, x);
-    const float u = dot_bf16(x, g.b + (long)dir * D + lane * 8);
+    const RowBf hb = pack_row(x);
+    store_bf(g.h + row * D + lane * 8, hb);
+    const float u = dot_bf16(hb, load8(g.b + (long)dir * D + lane * 8));
     if (lane == 0) g.u[row] = u;
   }
 }
 
-// Cross-entropy of the soft-capped logits: row r's loss is log(sum_j part[r, j]) - z[r, target].
-__device__ __forceinline__ float ce_row_loss(const CeFinalizeArgs& g, long row) {
-  const float* pr = g.part + row * g.parts;
+// Cross-entropy of the soft-capped logits: row r's loss is log(sum_j part[r, j]) - z[r, target]. Sixteen lanes
+// share a row: lane j of the group loads partials 4 j .. 4 j + 3, + 64, ... (parts a multiple of 4), so a wave
+// reads four whole 256-byte runs per instruction.
+__device__ __forceinline__ float ce_row_loss(const CeFinalizeArgs& g, long row, int gl) {
   float s = 0.f;
-  for (int j = 0; j < g.parts; ++j) s += pr[j];
+  for (int c = 4 * gl; c < g.parts; c += 64) {
+    const float4 v = *reinterpret_cast<const float4*>(g.part + row * g.parts + c);
+    s += (v.x + v.y) + (v.z + v.w);
+  }
+  s = group_sum<16>(s);
   return __logf(s) - g.tgt[row];
 }
 // ignore_index = -1 (utils/model.py:206-207)
@@ -229,39 +297,43 @@ __device__ __forceinline__ bool ce_row_valid(const CeFinalizeArgs& g, long row) 
 
 // CE_MEMBER_MEAN (population_loss, train/val/eggroll.py:101-102): workgroup p sums member p's T rows.
 // CE_NONE / CE_SUM / CE_MEAN (F.cross_entropy's reductions with ignore_index = -1, utils/model.py:205-208):
-// per row; or one workgroup sums every valid row. Each thread sums a fixed stride of rows, then a fixed
-// tree: the result does not depend on scheduling.
+// per row; or one workgroup sums every valid row. Each 16-lane group sums a fixed stride of rows, then the 16
+// group sums add in a fixed order: the result does not depend on scheduling.
 __global__ void __launch_bounds__(256) ce_finalize_kernel(CeFinalizeArgs g) {
-  __shared__ float red[256], cnt[256];
-  const int tid = threadIdx.x;
+  __shared__ float red[16], cnt[16];
+  const int tid = threadIdx.x, gl = tid & 15, gid = tid >> 4;
   if (g.reduction == CE_NONE) {
-    const long row = (long)blockIdx.x * 256 + tid;
-    if (row < (long)g.members * g.T) g.loss[row] = ce_row_valid(g, row) ? ce_row_loss(g, row) : 0.f;
+    const long row = (long)blockIdx.x * 16 + gid;
+    if (row < (long)g.members * g.T) {
+      const float l = ce_row_loss(g, row, gl);
+      if (gl == 0) g.loss[row] = ce_row_valid(g, row) ? l : 0.f;
+    }
     return;
   }
   const bool all = g.reduction != CE_MEMBER_MEAN;
   const long r0 = all ? 0 : (long)blockIdx.x * g.T, n = all ? (long)g.members * g.T : g.T;
   float acc = 0.f, c = 0.f;
-  for (long i = tid; i < n; i += 256) {
+  for (long i = gid; i < n; i += 16) {
     const long row = r0 + i;
+    const float l = ce_row_loss(g, row, gl);
     if (!all || ce_row_valid(g, row)) {
-      acc += ce_row_loss(g, row);
+      acc += l;
       c += 1.f;
     }
   }
-  red[tid] = acc;
-  cnt[tid] = c;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) {
-      red[tid] += red[tid + w];
-      cnt[tid] += cnt[tid + w];
-    }
-    __syncthreads();
+  if (gl == 0) {
+    red[gid] = acc;
+    cnt[gid] = c;
   }
+  __syncthreads();
   if (tid == 0) {
-    if (!all) g.loss[blockIdx.x] = red[0] / (float)g.T;
-    else g.loss[0] = g.reduction == CE_SUM ? red[0] : red[0] / cnt[0];  // 0 / 0 = NaN, as torch's mean
+    float t = 0.f, k = 0.f;
+    for (int q = 0; q < 16; ++q) {
+      t += red[q];
+      k += cnt[q];
+    }
+    if (!all) g.loss[blockIdx.x] = t / (float)g.T;
+    else g.loss[0] = g.reduction == CE_SUM ? t : t / k;  // 0 / 0 = NaN, as torch's mean
   }
 }
 
@@ -340,7 +412,8 @@ int ce_finalize_launch(const CeFinalizeArgs& g, hipStream_t s) {
       g.reduction > CE_MEAN || (g.reduction != CE_MEMBER_MEAN && !g.targets))
     return NOISE_EINVAL;
   const long rows = (long)g.members * g.T;
-  const long grid = g.reduction == CE_MEMBER_MEAN ? g.members : g.reduction == CE_NONE ? (rows + 255) / 256 : 1;
+  if (g.parts % 4 || ((uintptr_t)g.part & 15)) return NOISE_ENOTSUP;
+  const long grid = g.reduction == CE_MEMBER_MEAN ? g.members : g.reduction == CE_NONE ? (rows + 15) / 16 : 1;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   hipLaunchKernelGGL(ce_finalize_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
