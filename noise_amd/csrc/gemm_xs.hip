@@ -68,7 +68,9 @@ constexpr int DMA_PER_BLOCK = MODE == XS_DENSE ? 4 : 6;
 
 // q|k mode: the per-block vectors shared by the workgroup's 8 waves (5.5 KiB per ring slot).
 struct QkVec {
-  bf16 cs[2][R][32];  // rotary cos / sin rows of the block's 32 tokens
+  // rotary cos / sin rows of the block's 32 tokens; the 16-byte chunk c of row r sits at chunk c ^ ((r / 4) % 4),
+  // so the 16 rows one read instruction touches fall in distinct banks
+  bf16 cs[2][R][32];
   float uq[R][4];     // u_qkv rows: bf16 dots with b_q, b_k, b_v and the member's sign
   float av[NW][32];   // a over each wave's 32 columns
 };
@@ -181,7 +183,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
                  &qv[buf].av[wave][0]);
       if (wave < 4) {
         const bf16* tab = (wave >> 1) ? g.rot_sin : g.rot_cos;
-        dma_x4_s(tab + (long)(t0 + 16 * (wave & 1)) * 32, lane16, &qv[buf].cs[wave >> 1][16 * (wave & 1)][0]);
+        dma_x4_s(tab + (long)(t0 + 16 * (wave & 1)) * 32, 64u * (lane >> 2) + 16u * ((lane & 3) ^ ((lane >> 4) & 3)),
+                 &qv[buf].cs[wave >> 1][16 * (wave & 1)][0]);
       } else if (lane < R) {
         dma_x4_s(urows, lane16, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
       }
@@ -297,7 +300,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int c = 0; c < 2; ++c) ev_cs[i][c] = *reinterpret_cast<const bf16x8*>(&q.cs[c][16 * i + r][dd]);
+          for (int c = 0; c < 2; ++c)
+            ev_cs[i][c] = *reinterpret_cast<const bf16x8*>(&q.cs[c][16 * i + r][8 * ((dd >> 3) ^ ((r >> 2) & 3))]);
         return;
       }
       const int i = st < 8 ? 0 : 1, sub = st - (i ? 8 : 3);
