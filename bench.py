@@ -7,7 +7,8 @@ model (8 layers, d 512, vocab 4096) with bf16 GEMM weights and an fp32 head, 307
 antithetic pairs of rank-1 perturbations on every matrix and embedding (Gaussian on the 16 mixing
 scalars), sigma = 1e-3, one 2048-token Zipf(1.1) sequence; then the rank-normalised fitness, the
 fitness-weighted sum of the perturbation outer products and an Adam step on all 37,749,776 weights.
-One step = all of that (Eggroll.step). Weights are the reference's seed-0 initialisation, data is
+One step = all of that (Eggroll.step). All 3072 members run as one pass of the kernels (`--chunk`, about
+105 GB of activations in HBM; smaller chunks run the same kernels on fewer rows per launch). Weights are the reference's seed-0 initialisation, data is
 synthetic and resident in HBM before the timed region.
 
 `--workload mlp` times BASELINE config 1 alone (the rank-1-perturbed relu^2 MLP, P = 256, T = 2048,
@@ -42,11 +43,18 @@ def attention_flop_per_token(T, windows, H=8, hd=64):
     return 4 * hd * H * pairs / T
 
 
-def roofline_traffic():
+def roofline_traffic(chunk):
+    """HBM bytes of one MLP launch pair, from the PMC passes recorded in profiles/mlp_traffic.json (measured
+    at its `chunk_members`; every kernel of the pair streams per row, so another chunk scales the bytes by
+    the ratio of rows)."""
     path = ROOT / 'profiles' / 'mlp_traffic.json'
-    if path.exists():
-        return json.loads(path.read_text()).get('hbm_bytes_per_launch')
-    return None
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text())
+    b, c = rec.get('hbm_bytes_per_launch'), rec.get('chunk_members')
+    if b is None or not c:
+        return None
+    return b if c == chunk else b * chunk / c
 
 
 def cpu_baseline_step(budget_s=15.0):
@@ -152,7 +160,7 @@ def run_step(args):
                    'sigma': SIGMA, 'fitness': 'rank', 'optimizer': 'Adam (HIP)', 'chunk_members': args.chunk,
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
+                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(args.chunk),
                      'kernel': 'fused relu^2 MLP: xs_relu2_kernel (c_fc, weight-resident) + lowrank_gemm<EPI_DENSE> (c_proj)',
                      'flop_per_launch': mlp_flop, 'ms_per_launch': mlp_ms},
         'forward_tflops': flop_tok * P * T / (sum(v for k, v in stages.items()) / args.steps * 1e-3) / 1e12,
@@ -206,7 +214,7 @@ def run_mlp(args):
                    'd_model': D, 'd_hidden': F, 'sigma': SIGMA, 'x': 'shared [2048, 512]', 'output': 'bf16',
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(),
+                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None,
                      'kernel': 'noise_lowrank_mlp (rowdot + xs_relu2_kernel + lowrank_gemm<EPI_STORE> proj)',
                      'flop_per_launch': flop, 'ms_per_launch': ms_launch},
     }
@@ -337,7 +345,8 @@ def main():
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
     ap.add_argument('--qk-norm', action='store_true', help='config 2 with RMS-normalised q, k rows (the model case)')
     ap.add_argument('--pairs', type=int, default=1536)
-    ap.add_argument('--chunk', type=int, default=1024, help='members per kernel pass')
+    ap.add_argument('--chunk', type=int, default=3072,
+                    help='members per kernel pass (default: the whole population in one pass, ~105 GB of activations)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     args = ap.parse_args()
     if args.gpus != 1:
