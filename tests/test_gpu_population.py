@@ -449,6 +449,35 @@ def test_population_loss_config0_at_reference_init():
     assert (dg - dr).abs().max() < 1e-4, (dg, dr)
 
 
+def test_population_loss_config4_full_size_sampled_members():
+    """Config 4 at its real shape: 3072 members (1536 antithetic pairs, per-pair noise rows) on one 2048-token
+    Zipf sequence at the reference's initialisation, in 1024-member passes. Every loss is finite and near
+    ln 4096 (the init's head is N(0, 1e-6)); four members (both ends of the population, both signs) match
+    the bf16-mode oracle within the 1e-4 loss bar, and so do their antithetic differences."""
+    from noise_amd.population import Population
+    model = make_model('cpu', 0)
+    params = {n: p.detach().clone() for n, p in model.named_parameters()}
+    pairs, T = 1536, 2048
+    P = 2 * pairs
+    log_case(f'population_loss config4 P={P} T={T} (1024-member passes)')
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    noise = population_noise(shapes, pairs, seed=71, per_member=False)
+    sign = antithetic_signs(P, 1e-3)
+    idx, tgt = zipf_tokens(T, seed=72)
+    gm = _gpu_model(model)
+    got = Population(gm, chunk=1024).loss(dict(gm.named_parameters()), _dev(noise), sign.to(DEV), idx.to(DEV),
+                                          tgt.to(DEV), pair_shift=1).cpu()
+    assert got.shape == (P,) and torch.isfinite(got).all()
+    assert (got - math.log(4096)).abs().max() < 0.05
+    members = [0, 1, P - 2, P - 1]
+    rows = [m // 2 for m in members]
+    sub = {n: tuple(t[rows] for t in v) if isinstance(v, tuple) else v[rows] for n, v in noise.items()}
+    ref = om.population_loss(params, sub, sign[members], idx, tgt, mode='bf16', head='fp32')
+    assert (got[members] - ref).abs().max() < 1e-4, (got[members], ref)
+    dg, dr = got[members][1::2] - got[members][0::2], ref[1::2] - ref[0::2]
+    assert (dg - dr).abs().max() < 1e-4, (dg, dr)
+
+
 def test_population_loss_trained_weights_within_rounding_floor(trained):
     model, params = trained
     P, T = 8, 256
