@@ -248,6 +248,22 @@ typedef struct noise_outer_mat {
 int noise_outer_update_batch(const noise_outer_mat_t* mats, int n, const float* w, int ndir, float scale,
                              noise_stream_t stream);
 
+/* The perturbation rows of a set of directions, gathered from the shared N(0, 1) noise buffer: for every
+ * parameter k and direction j, the slice buffer[offsets_k[directions[j]] .. + out_k + in_k] split into
+ * a_k[j, :out_k] and b_k[j, :in_k] (in_k == 0 and b_k null for a 1-D parameter's eps rows). Replaces
+ * Eggroll.noise (train/val/eggroll.py:122-128): one launch for every parameter. params is a host array,
+ * read before the call returns; offsets are [pairs] int64 device arrays. A direction outside [0, pairs) or
+ * a slice outside the buffer writes NaN rows. */
+typedef struct noise_gather_param {
+  const int64_t* offsets;
+  float* a;
+  float* b;
+  int out;
+  int in;
+} noise_gather_param_t;
+int noise_gather_rows(const float* buffer, long buffer_len, const noise_gather_param_t* params, int nparams,
+                      const int64_t* directions, int ndir, int pairs, noise_stream_t stream);
+
 /* One torch.optim.AdamW step with weight_decay 0 on n fp32 values (train/val/eggroll.py:205, :167):
  * step_size = lr / (1 - beta1^t), bc2_sqrt = sqrt(1 - beta2^t). */
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,

@@ -44,6 +44,7 @@ SIGNATURES = {
     'noise_fitness': [P, I, I, I, P, P, P],
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
     'noise_outer_update_batch': [P, I, P, I, F, P],
+    'noise_gather_rows': [P, L, P, I, P, I, I, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
 
@@ -57,6 +58,18 @@ class OuterMat(ctypes.Structure):
 def outer_mats(items):
     """(a ptr or 0, a_ld, b ptr, b_ld, out, in, grad ptr) tuples -> (pointer to a host array, count)."""
     arr = (OuterMat * len(items))(*[OuterMat(*it) for it in items])
+    return ctypes.cast(arr, P), len(items), arr
+
+
+class GatherParam(ctypes.Structure):
+    """noise_gather_param_t of include/noise_hip.h."""
+    _fields_ = [('offsets', P), ('a', P), ('b', P), ('out', ctypes.c_int), ('in', ctypes.c_int)]
+
+
+def gather_params(items):
+    """A host array of noise_gather_param_t from (offsets, a, b, out, in) tuples of device pointers: returns
+    (pointer, count, array) -- keep the array alive until the call is enqueued."""
+    arr = (GatherParam * len(items))(*[GatherParam(*it) for it in items])
     return ctypes.cast(arr, P), len(items), arr
 
 

@@ -413,6 +413,16 @@ int noise_outer_update_batch(const noise_outer_mat_t* mats, int n, const float* 
   return outer_update_launch(u.data(), n, w, ndir, scale, static_cast<hipStream_t>(stream));
 }
 
+int noise_gather_rows(const float* buffer, long buffer_len, const noise_gather_param_t* params, int nparams,
+                      const int64_t* directions, int ndir, int pairs, noise_stream_t stream) {
+  if (nparams <= 0 || !params) return NOISE_EINVAL;
+  std::vector<GatherParam> q(nparams);
+  for (int k = 0; k < nparams; ++k)
+    q[k] = GatherParam{params[k].offsets, params[k].a, params[k].b, params[k].out, params[k].in};
+  return gather_rows_launch(q.data(), nparams, buffer, buffer_len, directions, ndir, pairs,
+                            static_cast<hipStream_t>(stream));
+}
+
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
                float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream) {
   AdamArgs g{param, grad, exp_avg, exp_avg_sq, n, step_size, beta1, beta2, eps, bc2_sqrt};

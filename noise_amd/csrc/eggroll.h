@@ -33,6 +33,26 @@ struct OuterBatchArgs {
   float scale;
 };
 
+// Rows of the noise buffer per (parameter, direction): buffer[offsets[directions[j]] ..] split into a [out]
+// and b [in] (train/val/eggroll.py:122-128). Up to GATHER_MAX parameters per launch, passed by value.
+constexpr int GATHER_MAX = 64;
+struct GatherParam {
+  const int64_t* offsets;  // [pairs] slice starts of this parameter
+  float* a;                // [ndir, out]
+  float* b;                // [ndir, in] (null when in == 0: a 1-D parameter's eps rows)
+  int out, in;
+};
+struct GatherArgs {
+  GatherParam p[GATHER_MAX];
+  int n;
+  const float* buffer;
+  long buffer_len;
+  const int64_t* directions;  // [ndir] pair indices
+  int ndir, pairs;
+};
+int gather_rows_launch(const GatherParam* params, int n, const float* buffer, long buffer_len,
+                       const int64_t* directions, int ndir, int pairs, hipStream_t s);
+
 struct AdamArgs {
   float* param;
   const float* grad;

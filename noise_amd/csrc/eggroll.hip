@@ -191,6 +191,44 @@ int fitness_launch(const float* losses, int n, int pairs, int mode, float* fit, 
   return NOISE_OK;
 }
 
+namespace {
+// One workgroup per (direction j, parameter k): copies the out + in floats of the parameter's slice for pair
+// directions[j]. A direction or offset outside its range writes NaN rows (never an out-of-bounds read).
+__global__ void __launch_bounds__(256) gather_rows_kernel(const GatherArgs g) {
+  const int j = blockIdx.x, k = blockIdx.y, tid = threadIdx.x;
+  const GatherParam& q = g.p[k];
+  const long d = g.directions[j];
+  const long off = (d >= 0 && d < g.pairs) ? q.offsets[d] : -1;
+  const bool ok = off >= 0 && off <= g.buffer_len - (long)(q.out + q.in);
+  const float* src = g.buffer + (ok ? off : 0);
+  for (int c = tid; c < q.out; c += 256) q.a[(long)j * q.out + c] = ok ? src[c] : __builtin_nanf("");
+  for (int c = tid; c < q.in; c += 256) q.b[(long)j * q.in + c] = ok ? src[q.out + c] : __builtin_nanf("");
+}
+}  // namespace
+
+int gather_rows_launch(const GatherParam* params, int n, const float* buffer, long buffer_len,
+                       const int64_t* directions, int ndir, int pairs, hipStream_t s) {
+  if (n <= 0 || !params || !buffer || buffer_len <= 0 || !directions || ndir <= 0 || pairs <= 0) return NOISE_EINVAL;
+  if (ndir > 0x7fffffff) return NOISE_ENOTSUP;
+  for (int base = 0; base < n; base += GATHER_MAX) {
+    GatherArgs g{};
+    g.n = std::min(GATHER_MAX, n - base);
+    g.buffer = buffer;
+    g.buffer_len = buffer_len;
+    g.directions = directions;
+    g.ndir = ndir;
+    g.pairs = pairs;
+    for (int k = 0; k < g.n; ++k) {
+      const GatherParam& q = params[base + k];
+      if (!q.offsets || !q.a || q.out <= 0 || q.in < 0 || (q.in > 0 && !q.b)) return NOISE_EINVAL;
+      g.p[k] = q;
+    }
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)ndir, (unsigned)g.n), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+  }
+  return NOISE_OK;
+}
+
 int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int ndir, float scale, hipStream_t s) {
   if (n <= 0 || !mats || !w || ndir <= 0) return NOISE_EINVAL;
   for (int base = 0; base < n; base += OUTER_MAX) {

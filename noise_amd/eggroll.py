@@ -51,11 +51,26 @@ class Eggroll:
 
     def noise(self, offsets, directions):
         """name -> (a [n, out], b [n, in]) for matrices and embeddings, eps [n, L] for the mixing scalars
-        (train/val/eggroll.py:122-128), as contiguous tensors."""
-        out = {}
+        (train/val/eggroll.py:122-128), as contiguous tensors: every parameter's rows gathered from the buffer
+        by one noise_gather_rows launch."""
+        directions = directions.to(device=self.device, dtype=torch.int64).contiguous()
+        n = directions.numel()
+        out, items = {}, []
         for name, p in self.params.items():
-            rows = self.buffer[offsets[name][directions, None] + torch.arange(sum(p.shape), device=self.device)]
-            out[name] = tuple(t.contiguous() for t in rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+            off = offsets[name]
+            if p.dim() == 2:
+                a = torch.empty(n, p.shape[0], device=self.device)
+                b = torch.empty(n, p.shape[1], device=self.device)
+                out[name] = (a, b)
+                items.append((off.data_ptr(), a.data_ptr(), b.data_ptr(), p.shape[0], p.shape[1]))
+            else:
+                e = torch.empty(n, p.shape[0], device=self.device)
+                out[name] = e
+                items.append((off.data_ptr(), e.data_ptr(), None, p.shape[0], 0))
+        if n:
+            ptr, count, _keep = _lib.gather_params(items)
+            _lib.call('noise_gather_rows', self.buffer.data_ptr(), self.buffer.numel(), ptr, count,
+                      directions.data_ptr(), n, self.pairs, torch.cuda.current_stream().cuda_stream)
         return out
 
     @torch.no_grad()

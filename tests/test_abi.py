@@ -85,6 +85,10 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert head(None, 256, 0, None, 1) == ENOSPC     # logits only
     assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
     assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
+    ptr, count, _keep = _lib.gather_params([(1, 1, None, 8, 4)])   # b null with in > 0
+    assert lib.noise_gather_rows(1, 1 << 20, ptr, count, 1, 4, 2, None) == EINVAL
+    ptr, count, _keep = _lib.gather_params([(1, 1, 1, 8, 4)])
+    assert lib.noise_gather_rows(1, 1 << 20, ptr, count, 1, 4, 0, None) == EINVAL  # no pairs
 
 
 def test_ops_refuse_cpu_tensors():

@@ -551,6 +551,31 @@ def test_population_loss_golden_reference_fp32(golden):
 
 # ---------------------------------------------------------------- update path
 
+def test_noise_gather_rows_equal_buffer_slices():
+    """Eggroll.noise on the library's grouped gather equals the reference's indexing of the buffer
+    (train/val/eggroll.py:122-128, restated in oracle.eggroll.gather_noise) bit for bit, for every parameter,
+    repeated and unordered directions included; a direction outside [0, pairs) yields NaN rows."""
+    from noise_amd.eggroll import Eggroll
+    model = make_model(DEV, 0)
+    pairs = 6
+    es = Eggroll(model, pairs, chunk=4, noise_len=1 << 20)
+    offs = es.offsets(3)
+    dirs = torch.tensor([0, 5, 2, 2, 4], device=DEV)
+    log_case('noise gather rows')
+    got = es.noise(offs, dirs)
+    shapes = {n: tuple(p.shape) for n, p in es.params.items()}
+    ref = oe.gather_noise(es.buffer.cpu(), {n: o.cpu() for n, o in offs.items()}, shapes, dirs.cpu())
+    torch.cuda.synchronize()
+    for n, shape in shapes.items():
+        if len(shape) == 2:
+            assert torch.equal(got[n][0].cpu(), ref[n][0]) and torch.equal(got[n][1].cpu(), ref[n][1]), n
+        else:
+            assert torch.equal(got[n].cpu(), ref[n]), n
+    bad = es.noise(offs, torch.tensor([pairs, -1], device=DEV))
+    torch.cuda.synchronize()
+    assert torch.isnan(bad['lm_head.weight'][0]).all() and torch.isnan(bad['resid_lambdas']).all()
+
+
 def test_fitness_update_adam_match_oracle():
     g = torch.Generator().manual_seed(7)
     pairs, nl = 6, 24
