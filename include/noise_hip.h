@@ -219,6 +219,18 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
                   int members, int T, int pair_shift, int reduction, float* loss, float* logits, void* workspace,
                   size_t workspace_bytes, const noise_pending_t* pend, int npend, noise_stream_t stream);
 
+/* Readout-probe forward differences (train/val/run.py:154-185, `cycle_derivatives` and `row_derivatives`):
+ * for token i (logits base_i = W x_i [vocab], |x_i|^2 = sq[i], target targets[i], step steps[i]) and each of
+ * its K directions j (dirs row j = W D_j, x_i . D_j = dots[i, k], |D_j|^2 = dir_sq), out[i, k] = (L_ij - L_i0) /
+ * steps[i], L the soft-capped cross-entropy of the head on norm(x_i + steps[i] D_j) (its RMS from sq, dots and
+ * dir_sq) and L_i0 on norm(x_i); 0 where the target is -1. rows null: every direction, K == P, dir_sq [P]
+ * (cycle_derivatives); rows [n, K] int64: the token's own directions, dir_sq [n, K] with dir_sq_per_token != 0
+ * (row_derivatives). fp32; vocab % 256 == 0, vocab <= 4096; width is the stream width of the RMS. */
+int noise_readout_probes(const float* base, long base_ld, const float* dirs, long dirs_ld, const int64_t* rows, int K,
+                         const int64_t* targets, const float* steps, const float* sq, const float* dots, long dots_ld,
+                         const float* dir_sq, int dir_sq_per_token, int n, int vocab, int P, int width, float* out,
+                         noise_stream_t stream);
+
 /* ---------------------------------------------------------------- EGGROLL update */
 
 /* fitness[j] = L[2j+1] - L[2j] transformed by mode (z-score: divided by the unbiased std + 1e-8, no

@@ -45,6 +45,7 @@ SIGNATURES = {
     'noise_outer_update': [P, L, P, L, P, I, I, I, F, P, P],
     'noise_outer_update_batch': [P, I, P, I, F, P],
     'noise_gather_rows': [P, L, P, I, P, I, I, P],
+    'noise_readout_probes': [P, L, P, L, P, I, P, P, P, P, L, P, I, I, I, I, I, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
 

@@ -6,6 +6,7 @@
 #include "common.h"
 #include "eggroll.h"
 #include "gemm.h"
+#include "probes.h"
 #include "rowops.h"
 
 static_assert(NOISE_CE_MEMBER_MEAN == CE_MEMBER_MEAN && NOISE_CE_NONE == CE_NONE && NOISE_CE_SUM == CE_SUM &&
@@ -421,6 +422,15 @@ int noise_gather_rows(const float* buffer, long buffer_len, const noise_gather_p
     q[k] = GatherParam{params[k].offsets, params[k].a, params[k].b, params[k].out, params[k].in};
   return gather_rows_launch(q.data(), nparams, buffer, buffer_len, directions, ndir, pairs,
                             static_cast<hipStream_t>(stream));
+}
+
+int noise_readout_probes(const float* base, long base_ld, const float* dirs, long dirs_ld, const int64_t* rows, int K,
+                         const int64_t* targets, const float* steps, const float* sq, const float* dots, long dots_ld,
+                         const float* dir_sq, int dir_sq_per_token, int n, int vocab, int P, int width, float* out,
+                         noise_stream_t stream) {
+  const ProbeArgs g{base, base_ld, dirs, dirs_ld, rows, K, targets, steps, sq, dots, dots_ld, dir_sq,
+                    dir_sq_per_token ? 1 : 0, n, vocab, P, width, out};
+  return probe_launch(g, static_cast<hipStream_t>(stream));
 }
 
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,

@@ -89,6 +89,11 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_gather_rows(1, 1 << 20, ptr, count, 1, 4, 2, None) == EINVAL
     ptr, count, _keep = _lib.gather_params([(1, 1, 1, 8, 4)])
     assert lib.noise_gather_rows(1, 1 << 20, ptr, count, 1, 4, 0, None) == EINVAL  # no pairs
+    probe = lambda rows, K, vocab, P: lib.noise_readout_probes(  # noqa: E731
+        16, vocab, 16, vocab, rows, K, 1, 1, 1, 1, K, 1, 0, 4, vocab, P, 512, 1, None)
+    assert probe(None, 8, 4096, 16) == EINVAL      # every direction needs K == P
+    assert probe(None, 16, 4000, 16) == EINVAL     # vocab % 256
+    assert probe(None, 16, 8192, 16) == EINVAL     # vocab above 4096
 
 
 def test_ops_refuse_cpu_tensors():

@@ -269,3 +269,27 @@ def test_norm_head_ce_with_gain_is_capped_cross_entropy():
     # gain = 1 reproduces the reference head path
     ones = om.norm_head_ce(h, torch.ones(D), W, a, b, sign, tgt)
     assert torch.allclose(ones, om.head_loss(om.norm(h), W, a, b, sign, tgt), atol=1e-6)
+
+
+def test_readout_probes_equal_moved_stream_brute_force():
+    """cycle_derivatives / row_derivatives (train/val/run.py:154-185) against moving the stream itself:
+    norm(x + s D_j) through the head, capped, cross-entropy; the RMS-from-dots algebra and C = W D are what
+    the brute force does not assume. float64; a target of -1 gives 0."""
+    from oracle import probes as op
+    g = torch.Generator().manual_seed(5)
+    n, width, V, P, K = 4, 16, 32, 6, 3
+    x = torch.randn(n, width, generator=g, dtype=torch.float64) * 2
+    W = torch.randn(V, width, generator=g, dtype=torch.float64)
+    D = torch.randn(width, P, generator=g, dtype=torch.float64)
+    y = torch.tensor([3, -1, 31, 0])
+    steps = torch.tensor([[1e-2], [3e-2], [5e-3], [2e-2]], dtype=torch.float64)
+    base, C = x @ W.T, (W @ D).T
+    sq, dots, dir_sq = x.square().sum(-1, keepdim=True), x @ D, D.square().sum(0)
+    got = op.cycle_derivatives(base, C, y, steps, sq, dots, dir_sq, width=width)
+    moved, clean = op.moved_stream_losses(x, W, D, y, steps)
+    ref = (moved - clean[:, None]) / steps * (y >= 0)[:, None]
+    assert torch.allclose(got, ref, rtol=1e-9, atol=1e-9)
+    assert torch.all(got[1] == 0) and got.abs().sum() > 0
+    rows = torch.randint(0, P, (n, K), generator=g)
+    got_r = op.row_derivatives(base, C, rows, y, steps, sq, dots.gather(1, rows), dir_sq[rows], width=width)
+    assert torch.allclose(got_r, ref.gather(1, rows), rtol=1e-9, atol=1e-9)
