@@ -250,10 +250,23 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(wc[j], xf[i], acc[i][j]);
   };
 
+  // Tile order: row block outer, column tile inner, except for the head (EPI_CE: 16 column tiles of a W that
+  // does not fit an XCD's L2), which walks groups of CE_GROUP row blocks per column tile so each W column tile
+  // is read once per group rather than once per row block (measured: config 3 15.4 -> 14.7 ms; groups of 4:
+  // 14.8, 32: 17.4).
+  constexpr int CE_GROUP = 8;
+  auto tile_mn = [&](int t, int which) {
+    if (EPI == EPI_CE) {
+      const int span = CE_GROUP * tiles_n, grp = t / span, rem = t % span;
+      const int gm = min(CE_GROUP, tiles_m - grp * CE_GROUP);
+      return which == 0 ? (grp * CE_GROUP + rem % gm) * BM : (rem / gm) * BN;
+    }
+    return which == 0 ? (t / tiles_n) * BM : (t % tiles_n) * BN;
+  };
   int tile = t_lo + slot;
   if (tile >= t_hi) return;
   {
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    const int m0 = tile_mn(tile, 0), n0 = tile_mn(tile, 1);
     prefetch_ep(m0, n0);
     set_sources(m0, n0);
 #pragma unroll
@@ -261,7 +274,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       if (s < KT) issue(s, s);
   }
   while (true) {
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    const int m0 = tile_mn(tile, 0), n0 = tile_mn(tile, 1);
     // the previous tile's epilogue has finished reading the staged vectors
     wait_vm_lgkm0<63>();
     __builtin_amdgcn_s_barrier();
@@ -289,7 +302,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     wait_vm_lgkm0<63>();
     __builtin_amdgcn_s_barrier();
     if (next < t_hi) {
-      const int nm0 = (next / tiles_n) * BM, nn0 = (next % tiles_n) * BN;
+      const int nm0 = tile_mn(next, 0), nn0 = tile_mn(next, 1);
       prefetch_ep(nm0, nn0);
       set_sources(nm0, nn0);
 #pragma unroll
