@@ -231,6 +231,22 @@ int noise_readout_probes(const float* base, long base_ld, const float* dirs, lon
                          const float* dir_sq, int dir_sq_per_token, int n, int vocab, int P, int width, float* out,
                          noise_stream_t stream);
 
+/* Credit scoring around batched attention reruns (train/val/run.py:186-211, used by query_key_errors :594-634),
+ * 64-dim heads, draws j, batch b, position t, head h:
+ * noise_moved_heads: out row (j, b, t), head h = bf16(norm(rotary(raw[b, t, h] + sigma a[j, b, t, h]))) in fp32
+ *   (`moved_heads`, :186-189; rotary of utils/model.py:55-58 with fp32 tables [>= T, 32]); raw fp32
+ *   [batch, T, heads, 64], a bf16 [draws, batch, T, heads, 64], out bf16 rows of out_ld elements.
+ * noise_head_scores: score[b, h, t, j] = sum_d (out[j, b, t, h, d] - baseline[b, t, h, d]) hub[b, t, h, d]
+ *   (`head_scores`, :192-195); out bf16 rows of out_ld elements (noise_attention's y), baseline and hub fp32.
+ * noise_code_estimate: est[b, t, h, d] = sum_j credited[b, h, t, j] a[j, b, t, h, d] (`code_estimate`,
+ *   :208-210), fp32 out, draws summed in order. */
+int noise_moved_heads(const float* raw, const void* a, float sigma, const float* rot_cos, const float* rot_sin, int draws,
+                      int batch, int T, int heads, void* out, long out_ld, noise_stream_t stream);
+int noise_head_scores(const void* out, long out_ld, const float* baseline, const float* hub, int draws, int batch, int T,
+                      int heads, float* score, noise_stream_t stream);
+int noise_code_estimate(const float* credited, const void* a, int draws, int batch, int T, int heads, float* est,
+                        noise_stream_t stream);
+
 /* ---------------------------------------------------------------- EGGROLL update */
 
 /* fitness[j] = L[2j+1] - L[2j] transformed by mode (z-score: divided by the unbiased std + 1e-8, no

@@ -46,6 +46,9 @@ SIGNATURES = {
     'noise_outer_update_batch': [P, I, P, I, F, P],
     'noise_gather_rows': [P, L, P, I, P, I, I, P],
     'noise_readout_probes': [P, L, P, L, P, I, P, P, P, P, L, P, I, I, I, I, I, P, P],
+    'noise_moved_heads': [P, P, F, P, P, I, I, I, I, P, L, P],
+    'noise_head_scores': [P, L, P, P, I, I, I, I, P, P],
+    'noise_code_estimate': [P, P, I, I, I, I, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
 }
 

@@ -4,6 +4,7 @@
 #include "../../include/noise_hip.h"
 #include "attention.h"
 #include "common.h"
+#include "credit.h"
 #include "eggroll.h"
 #include "gemm.h"
 #include "probes.h"
@@ -431,6 +432,26 @@ int noise_readout_probes(const float* base, long base_ld, const float* dirs, lon
   const ProbeArgs g{base, base_ld, dirs, dirs_ld, rows, K, targets, steps, sq, dots, dots_ld, dir_sq,
                     dir_sq_per_token ? 1 : 0, n, vocab, P, width, out};
   return probe_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_moved_heads(const float* raw, const void* a, float sigma, const float* rot_cos, const float* rot_sin, int draws,
+                      int batch, int T, int heads, void* out, long out_ld, noise_stream_t stream) {
+  const MovedHeadsArgs g{raw, static_cast<const bf16*>(a), sigma, rot_cos, rot_sin, static_cast<bf16*>(out), out_ld,
+                         draws, batch, T, heads, (long)draws * batch * T * heads};
+  return moved_heads_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_head_scores(const void* out, long out_ld, const float* baseline, const float* hub, int draws, int batch, int T,
+                      int heads, float* score, noise_stream_t stream) {
+  const HeadScoresArgs g{static_cast<const bf16*>(out), out_ld, baseline, hub, score, draws, batch, T, heads,
+                         (long)draws * batch * T * heads};
+  return head_scores_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_code_estimate(const float* credited, const void* a, int draws, int batch, int T, int heads, float* est,
+                        noise_stream_t stream) {
+  const CodeEstimateArgs g{credited, static_cast<const bf16*>(a), est, draws, T, heads, (long)batch * T * heads * 64};
+  return code_estimate_launch(g, static_cast<hipStream_t>(stream));
 }
 
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,

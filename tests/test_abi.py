@@ -94,6 +94,10 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert probe(None, 8, 4096, 16) == EINVAL      # every direction needs K == P
     assert probe(None, 16, 4000, 16) == EINVAL     # vocab % 256
     assert probe(None, 16, 8192, 16) == EINVAL     # vocab above 4096
+    assert lib.noise_moved_heads(1, 1, 0.1, 1, 1, 2, 1, 128, 8, 1, 256, None) == EINVAL  # out_ld < heads * 64
+    assert lib.noise_moved_heads(None, 1, 0.1, 1, 1, 2, 1, 128, 8, 1, 512, None) == EINVAL
+    assert lib.noise_head_scores(1, 512, 1, 1, 0, 1, 128, 8, 1, None) == EINVAL          # no draws
+    assert lib.noise_code_estimate(1, None, 2, 1, 128, 8, 1, None) == EINVAL
 
 
 def test_ops_refuse_cpu_tensors():
@@ -103,6 +107,9 @@ def test_ops_refuse_cpu_tensors():
     a = torch.zeros(2, 512)
     with pytest.raises(ValueError, match='CUDA'):
         ops.lowrank_linear(x, w, a, a, torch.zeros(2))
+    from noise_amd import credit
+    with pytest.raises(ValueError, match='CUDA'):
+        credit.code_estimate(torch.zeros(1, 8, 128, 2), torch.zeros(2, 1, 128, 8, 64, dtype=torch.bfloat16))
 
 
 def test_tile16_layout_is_a_permutation_of_whole_tiles():

@@ -1,0 +1,102 @@
+"""Credit scoring around attention reruns on the HIP kernels (train/val/run.py:186-211, composed by
+query_key_errors :594-634) against the CPU oracle on the same seeded inputs."""
+import pytest
+import torch
+
+from noise_amd import credit
+from oracle import credit as oc
+from oracle import model as om
+from tests._util import log_case, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+
+
+def _tables(T):
+    cos, sin = om.rotary_tables()
+    return cos[:T].float(), sin[:T].float()
+
+
+def _heads(g, n, b, T, h=8):
+    raw = torch.randn(b, T, h, 64, generator=g) * 2
+    a = torch.randn(n, b, T, h, 64, generator=g).bfloat16()
+    return raw, a
+
+
+def test_moved_heads_match_oracle_within_one_bf16_step():
+    g = torch.Generator().manual_seed(21)
+    n, b, T = 4, 2, 256
+    log_case(f'moved_heads n={n} b={b} T={T}')
+    raw, a = _heads(g, n, b, T)
+    cos, sin = _tables(T)
+    got = credit.moved_heads(raw.to(DEV), a.to(DEV), 0.1, cos.to(DEV), sin.to(DEV))
+    torch.cuda.synchronize()
+    ref = oc.moved_heads(raw, a, 0.1, cos, sin)
+    got = got.cpu().float()
+    assert got.shape == ref.shape
+    # fp32 arithmetic in a different order (fused multiply-adds on the GPU): a result may round to the
+    # neighbouring bf16 value; near-cancelling rotations (|y| far below the row RMS of 1) carry the fp32
+    # error of the unit-size terms, 1e-6 absolute
+    diff = (got - ref.float()).abs()
+    bound = ref.float().abs() * 2.0 ** -7 + 1e-6
+    worst = int((diff - bound).flatten().argmax())
+    print(f'moved_heads: exact {float((diff == 0).float().mean()):.5f}, worst got {float(got.flatten()[worst]):.6e} '
+          f'ref {float(ref.float().flatten()[worst]):.6e}', flush=True)
+    assert (diff <= bound).all()
+    assert float((diff == 0).float().mean()) > 0.99
+
+
+def test_head_scores_and_code_estimate_match_oracle():
+    g = torch.Generator().manual_seed(22)
+    n, b, T, h = 6, 2, 128, 8
+    log_case(f'head_scores / code_estimate n={n} b={b} T={T}')
+    out = torch.randn(n, b, T, h, 64, generator=g).bfloat16()
+    base, hub = torch.randn(b, T, h, 64, generator=g), torch.randn(b, T, h, 64, generator=g)
+    score = credit.head_scores(out.to(DEV), base.to(DEV), hub.to(DEV))
+    cr = torch.randn(b, h, T, n, generator=g)
+    a = torch.randn(n, b, T, h, 64, generator=g).bfloat16()
+    est = credit.code_estimate(cr.to(DEV), a.to(DEV))
+    torch.cuda.synchronize()
+    ref_s, ref_e = oc.head_scores(out, base, hub), oc.code_estimate(cr, a)
+    print(f'head_scores max diff {float((score.cpu() - ref_s).abs().max()):.3e}, code_estimate max diff '
+          f'{float((est.cpu() - ref_e).abs().max()):.3e}', flush=True)
+    assert torch.allclose(score.cpu(), ref_s, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(est.cpu(), ref_e, rtol=1e-5, atol=1e-5)
+
+
+def test_attention_wrapper_matches_oracle():
+    g = torch.Generator().manual_seed(23)
+    b, T, window = 2, 256, 100
+    log_case(f'credit.attention b={b} T={T} window={window}')
+    q, k, v = (torch.randn(b, T, 8, 64, generator=g).bfloat16() for _ in range(3))
+    got = credit.attention(q.to(DEV), k.to(DEV), v.to(DEV), window).cpu().float()
+    ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))
+    assert rel_err(got, ref) < 1e-2
+    assert (got - ref).abs().max() < 2e-2
+
+
+@pytest.mark.parametrize('kind', ['q', 'k'])
+def test_credit_chunk_matches_oracle(kind):
+    """One chunk of query / key credit: GPU estimate within twice the oracle's own bf16-output floor (oracle
+    with the attention output rounded to bf16, as the reference's, against the unrounded oracle) plus 1e-3."""
+    g = torch.Generator().manual_seed(24 if kind == 'q' else 25)
+    n, b, T, window, sigma = 8, 2, 256, 128, 0.1
+    log_case(f'credit_chunk kind={kind} n={n} b={b} T={T} window={window}')
+    raw, a = _heads(g, n, b, T)
+    cos, sin = _tables(T)
+    other = om.norm(om.apply_rotary(torch.randn(b, T, 8, 64, generator=g), cos, sin)).bfloat16()
+    values = torch.randn(b, T, 8, 64, generator=g).bfloat16()
+    processed = om.norm(om.apply_rotary(raw, cos, sin)).bfloat16()
+    qp, kp = (processed, other) if kind == 'q' else (other, processed)
+    baseline = om.bf(om.attention(qp.float(), kp.float(), values.float(), window))
+    target = torch.randn(b, T, 8, 64, generator=g)
+    kf = torch.rand(b, 8, T, T, generator=g).tril().bfloat16() if kind == 'k' else None
+    fixed = other
+    args = lambda d: [t.to(d) if isinstance(t, torch.Tensor) else t for t in  # noqa: E731
+                      (raw, a, sigma, cos, sin, fixed, values, window, baseline, target, kf)]
+    got = credit.credit_chunk(kind, *args(DEV)).cpu()
+    ref32 = oc.credit_chunk(kind, *args('cpu'), round_out=False)
+    ref16 = oc.credit_chunk(kind, *args('cpu'), round_out=True)
+    floor = rel_err(ref16, ref32)
+    log_case(f'credit_chunk kind={kind}: gpu {rel_err(got, ref32):.3e} floor {floor:.3e}')
+    assert rel_err(got, ref32) <= 2 * floor + 1e-3

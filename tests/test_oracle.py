@@ -293,3 +293,71 @@ def test_readout_probes_equal_moved_stream_brute_force():
     rows = torch.randint(0, P, (n, K), generator=g)
     got_r = op.row_derivatives(base, C, rows, y, steps, sq, dots.gather(1, rows), dir_sq[rows], width=width)
     assert torch.allclose(got_r, ref.gather(1, rows), rtol=1e-9, atol=1e-9)
+
+
+def test_credit_helpers_equal_index_loops():
+    """moved_heads / head_scores / code_estimate (train/val/run.py:186-211) against per-element loops: the
+    rotation as a complex product, the RMS as an explicit mean, the sums over their named indices."""
+    from oracle import credit as oc
+    g = torch.Generator().manual_seed(11)
+    n, b, t, h = 3, 2, 4, 2
+    raw = torch.randn(b, t, h, 64, generator=g).double()
+    a = torch.randn(n, b, t, h, 64, generator=g).double()
+    ang = torch.rand(t, 32, generator=g).double() * 6
+    cos, sin, sigma = ang.cos(), ang.sin(), 0.3
+    got = oc.moved_heads(raw, a, sigma, cos, sin).view(n, b, t, h, 64)
+    for j in range(n):
+        for bb in range(b):
+            for tt in range(t):
+                for hh in range(h):
+                    x = raw[bb, tt, hh] + sigma * a[j, bb, tt, hh]
+                    z = torch.complex(x[:32], x[32:]) * torch.complex(cos[tt], -sin[tt])
+                    y = torch.cat([z.real, z.imag])
+                    y = y / math.sqrt(float((y * y).sum()) / 64 + torch.finfo(torch.float32).eps)
+                    assert torch.allclose(got[j, bb, tt, hh], y, rtol=1e-6, atol=1e-6)
+    out = torch.randn(n, b, t, h, 64, generator=g).double()
+    base, hub = torch.randn(b, t, h, 64, generator=g).double(), torch.randn(b, t, h, 64, generator=g).double()
+    score = oc.head_scores(out, base, hub)
+    assert score.shape == (b, h, t, n)
+    cr = torch.randn(b, h, t, n, generator=g).double()
+    est = oc.code_estimate(cr, a)
+    for bb in range(b):
+        for hh in range(h):
+            for tt in range(t):
+                for j in range(n):
+                    want = sum(float((out[j, bb, tt, hh, d] - base[bb, tt, hh, d]) * hub[bb, tt, hh, d])
+                               for d in range(64))
+                    assert abs(float(score[bb, hh, tt, j]) - want) < 1e-5 * (1 + abs(want))  # fp32 sums
+                for d in (0, 17, 63):
+                    want = sum(float(cr[bb, hh, tt, j] * a[j, bb, tt, hh, d]) for j in range(n))
+                    assert abs(float(est[bb, tt, hh, d]) - want) < 1e-5 * (1 + abs(want))
+
+
+def test_query_credit_with_basis_draws_is_the_gradient():
+    """With the 64 draws a_j = e_j at every (b, t, h) and a small sigma, the query estimate of one chunk
+    (train/val/run.py:617-625) divided by sigma is the gradient of sum(target * attention output) with respect
+    to the raw queries (each query's output depends on its own query only): fp64 autograd through
+    norm(rotary(.)) and a dense masked softmax."""
+    from oracle import credit as oc
+    g = torch.Generator().manual_seed(12)
+    b, t, h, window, sigma = 1, 6, 2, 3, 1e-3
+    raw = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    kp = om.norm(torch.randn(b, t, h, 64, generator=g, dtype=torch.float64))
+    v = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    hub = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    ang = torch.rand(t, 32, generator=g, dtype=torch.float64) * 6
+    cos, sin = ang.cos(), ang.sin()
+    a = torch.eye(64, dtype=torch.float64)[:, None, None, None, :].expand(64, b, t, h, 64).contiguous()
+
+    def out_of(q_raw):
+        x1, x2 = q_raw[..., :32], q_raw[..., 32:]
+        c, s = cos[None, :, None, :], sin[None, :, None, :]
+        y = torch.cat([x1 * c + x2 * s, -x1 * s + x2 * c], -1)
+        y = y * torch.rsqrt((y * y).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)
+        return om.attention(y, kp, v, window, dtype=torch.float64)
+
+    q = raw.clone().requires_grad_(True)
+    (out_of(q) * hub).sum().backward()
+    baseline = out_of(raw)
+    est = oc.credit_chunk('q', raw, a, sigma, cos, sin, kp, v, window, baseline, hub, round_out=False)
+    assert torch.allclose(est.double() / sigma, q.grad, rtol=2e-2, atol=2e-3 * float(q.grad.abs().max()))
