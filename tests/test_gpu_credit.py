@@ -100,3 +100,40 @@ def test_credit_chunk_matches_oracle(kind):
     floor = rel_err(ref16, ref32)
     log_case(f'credit_chunk kind={kind}: gpu {rel_err(got, ref32):.3e} floor {floor:.3e}')
     assert rel_err(got, ref32) <= 2 * floor + 1e-3
+
+
+def test_query_credit_full_length_sampled_positions():
+    """The model's 2048-token sequence, 16 draws, the short window 1024: the query estimate at sampled
+    positions (first and last tokens, both sides of the window edge) against a per-position oracle: each
+    query's output depends on its own moved query only (train/val/run.py:617-625). GPU error within twice the
+    oracle's bf16-output floor plus 1e-3, as for the small chunk."""
+    g = torch.Generator().manual_seed(26)
+    n, b, T, window, sigma = 16, 2, 2048, 1024, 0.1
+    log_case(f'credit_chunk kind=q n={n} b={b} T={T} window={window}')
+    raw, a = _heads(g, n, b, T)
+    cos, sin = _tables(T)
+    kp = om.norm(om.apply_rotary(torch.randn(b, T, 8, 64, generator=g), cos, sin)).bfloat16()
+    values = torch.randn(b, T, 8, 64, generator=g).bfloat16()
+    target = torch.randn(b, T, 8, 64, generator=g)
+    qp = om.norm(om.apply_rotary(raw, cos, sin)).bfloat16()
+    base = credit.attention(qp.to(DEV), kp.to(DEV), values.to(DEV), window)
+    est = credit.credit_chunk('q', raw.to(DEV), a.to(DEV), sigma, cos.to(DEV), sin.to(DEV), kp.to(DEV),
+                              values.to(DEV), window, base, target.to(DEV)).cpu()
+    base = base.cpu().float()
+    got, ref16, ref32 = [], [], []
+    for bb, t in [(0, 0), (0, 1), (0, 1023), (0, 1024), (0, 1025), (0, 2047), (1, 7), (1, 1500), (1, 2047)]:
+        lo = max(0, t - window)
+        K, V = kp[bb, lo:t + 1].float(), values[bb, lo:t + 1].float()
+        mq = oc.moved_heads(raw[bb:bb + 1, t:t + 1], a[:, bb:bb + 1, t:t + 1], sigma, cos[t:t + 1],
+                            sin[t:t + 1]).float()[:, 0]                               # [n, 8, 64]
+        p = (torch.einsum('nhd,whd->nhw', mq, K) / 8).softmax(-1)
+        out = torch.einsum('nhw,whd->nhd', p, V)
+        for rnd, acc in ((True, ref16), (False, ref32)):
+            o = out.bfloat16().float() if rnd else out
+            score = ((o - base[bb, t]) * target[bb, t]).sum(-1)                          # [n, 8]
+            acc.append(torch.einsum('nh,nhd->hd', score, a[:, bb, t].float()))
+        got.append(est[bb, t])
+    got, ref16, ref32 = torch.stack(got), torch.stack(ref16), torch.stack(ref32)
+    floor = rel_err(ref16, ref32)
+    log_case(f'full-length query credit: gpu {rel_err(got, ref32):.3e} floor {floor:.3e}')
+    assert rel_err(got, ref32) <= 2 * floor + 1e-3
