@@ -82,11 +82,13 @@ def attention(q, k, v, window, qk_norm=False):
     attention kernel: q and k bf16, v the bf16-rounded value in fp16 (the kernel's operand format), P in fp16,
     bf16 output. 8 heads; token count a multiple of 128. qk_norm declares RMS-normalised q, k rows (the
     credit reruns' processed heads), which lets the softmax skip its running maximum."""
-    for t, nm in ((q, 'q'), (k, 'k'), (v, 'v')):
-        _cuda(t, nm)
     B, T, H, hd = q.shape
     if hd != HD or H != 8 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError('q, k, v must be [batch, token, 8, 64] of one shape')
+    if T % 128:
+        raise ValueError(f'the attention kernel runs whole 128-token blocks: token count {T} is not a multiple of 128')
+    for t, nm in ((q, 'q'), (k, 'k'), (v, 'v')):
+        _cuda(t, nm)
     qkv = torch.empty(B * T, 3 * H * HD, device=q.device, dtype=torch.bfloat16)
     qkv[:, :H * HD] = q.reshape(B * T, H * HD).to(torch.bfloat16)
     qkv[:, H * HD:2 * H * HD] = k.reshape(B * T, H * HD).to(torch.bfloat16)
@@ -105,14 +107,16 @@ def rerun(kind, raw, a, sigma, cos, sin, fixed, values, window):
     runs with bounded scores (no running maximum)."""
     if kind not in ('q', 'k'):
         raise ValueError("kind must be 'q' or 'k'")
-    _cuda(raw, 'raw'), _cuda(a, 'a'), _cuda(fixed, 'fixed'), _cuda(values, 'values')
     n, b, T, H, hd = a.shape
     if hd != HD or H != 8 or tuple(raw.shape) != (b, T, H, HD):
         raise ValueError('a must be [n, b, t, 8, 64] and raw [b, t, 8, 64]')
     if tuple(fixed.shape) != (b, T, H, HD) or tuple(values.shape) != (b, T, H, HD):
         raise ValueError('fixed and values must be [b, t, 8, 64]')
+    if T % 128:
+        raise ValueError(f'the attention kernel runs whole 128-token blocks: t = {T} is not a multiple of 128')
     if a.dtype != torch.bfloat16:
         raise TypeError('a must be bfloat16')
+    _cuda(raw, 'raw'), _cuda(a, 'a'), _cuda(fixed, 'fixed'), _cuda(values, 'values')
     W = H * HD
     moved_slot, fixed_slot = (0, W) if kind == 'q' else (W, 0)
     qkv = torch.empty(n, b * T, 3 * W, device=a.device, dtype=torch.bfloat16)
@@ -132,10 +136,11 @@ def credit_chunk(kind, raw, a, sigma, cos, sin, fixed, values, window, baseline,
     """One chunk's contribution to the estimate of `query_key_errors` (train/val/run.py:617-625): rerun, score
     each query's output change against its target, for keys carry the scores back through the matched filter
     key_filter [b, h, t, t] (bf16 product, as the reference), then weight the draws: [b, t, h, 64] fp32."""
+    n, b, T, H, _ = a.shape
+    if kind == 'k' and (key_filter is None or tuple(key_filter.shape) != (b, H, T, T)):
+        raise ValueError(f'key credit needs the matched filter key_filter [{b}, {H}, {T}, {T}]')
     out = rerun(kind, raw, a, sigma, cos, sin, fixed, values, window)
     score = head_scores(out, baseline, target)
     if kind == 'k':
-        if key_filter is None:
-            raise ValueError('key credit needs the matched filter key_filter [b, h, t, t]')
         score = torch.matmul(key_filter.to(torch.bfloat16).contiguous(), score.to(torch.bfloat16).contiguous()).float()
     return code_estimate(score, a)

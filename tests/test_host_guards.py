@@ -56,3 +56,23 @@ def test_short_token_ids_and_outputs_are_refused(no_launch):
              logits=torch.zeros(B, T, 100))
     with pytest.raises(ValueError, match='buffers hold'):
         _run(buf, torch.zeros(B + 1), torch.zeros(T, dtype=torch.int64))
+
+
+def test_credit_wrappers_reject_bad_shapes_before_any_launch():
+    from noise_amd import credit
+    bf = torch.bfloat16
+    raw, fixed = torch.zeros(1, 100, 8, 64), torch.zeros(1, 100, 8, 64)
+    a = torch.zeros(2, 1, 100, 8, 64, dtype=bf)
+    with pytest.raises(ValueError, match="'q' or 'k'"):
+        credit.rerun('v', raw, a, 0.1, None, None, fixed, fixed, 50)
+    with pytest.raises(ValueError, match='multiple of 128'):
+        credit.rerun('q', raw, a, 0.1, None, None, fixed, fixed, 50)
+    with pytest.raises(ValueError, match='multiple of 128'):
+        credit.attention(raw, raw, raw, 50)
+    raw, a = torch.zeros(1, 128, 8, 64), torch.zeros(2, 1, 128, 8, 64, dtype=bf)
+    with pytest.raises(ValueError, match='fixed and values'):
+        credit.rerun('k', raw, a, 0.1, None, None, raw[:, :64], raw, 50)
+    with pytest.raises(ValueError, match='matched filter'):
+        credit.credit_chunk('k', raw, a, 0.1, None, None, raw, raw, 50, raw, raw, torch.zeros(1, 8, 128, 64))
+    with pytest.raises(ValueError, match='CUDA'):
+        credit.rerun('q', raw, a, 0.1, None, None, raw, raw, 50)
