@@ -24,6 +24,9 @@ def _cuda(t, name):
 
 def _tables(t, T):
     """cos / sin as fp32 [T, 32] from the reference's [1, >= T, 1, 32] (or [>= T, 32]) tables."""
+    if t.shape[-1] != 32 or t.numel() // 32 < T:
+        raise ValueError(f'rotary tables must hold at least {T} rows of 32 (got shape {tuple(t.shape)})')
+    _cuda(t, 'rotary table')
     t = t.reshape(-1, 32)[:T]
     return t.float().contiguous()
 
@@ -37,11 +40,12 @@ def moved_heads(raw, a, sigma, cos, sin):
         raise ValueError(f'raw must be [{b}, {T}, {H}, {HD}] and a [n, b, t, h, {HD}]')
     if a.dtype != torch.bfloat16:
         raise TypeError('a must be bfloat16 (the draws are stored in the model dtype)')
+    cos, sin = _tables(cos, T), _tables(sin, T)
     raw = raw.float().contiguous()
     a = a.contiguous()
     out = torch.empty(n * b, T, H, HD, device=a.device, dtype=torch.bfloat16)
-    _lib.call('noise_moved_heads', raw.data_ptr(), a.data_ptr(), float(sigma), _tables(cos, T).data_ptr(),
-              _tables(sin, T).data_ptr(), n, b, T, H, out.data_ptr(), H * HD, _stream())
+    _lib.call('noise_moved_heads', raw.data_ptr(), a.data_ptr(), float(sigma), cos.data_ptr(), sin.data_ptr(), n, b,
+              T, H, out.data_ptr(), H * HD, _stream())
     return out
 
 
@@ -116,6 +120,9 @@ def rerun(kind, raw, a, sigma, cos, sin, fixed, values, window):
         raise ValueError(f'the attention kernel runs whole 128-token blocks: t = {T} is not a multiple of 128')
     if a.dtype != torch.bfloat16:
         raise TypeError('a must be bfloat16')
+    if window < 0:
+        raise ValueError('window must be >= 0')
+    cos, sin = _tables(cos, T), _tables(sin, T)
     _cuda(raw, 'raw'), _cuda(a, 'a'), _cuda(fixed, 'fixed'), _cuda(values, 'values')
     W = H * HD
     moved_slot, fixed_slot = (0, W) if kind == 'q' else (W, 0)
@@ -124,8 +131,8 @@ def rerun(kind, raw, a, sigma, cos, sin, fixed, values, window):
     qkv[:, :, 2 * W:] = values.reshape(1, b * T, W).to(torch.bfloat16).half().view(torch.bfloat16)
     rawf, a = raw.float().contiguous(), a.contiguous()
     stream = _stream()
-    _lib.call('noise_moved_heads', rawf.data_ptr(), a.data_ptr(), float(sigma), _tables(cos, T).data_ptr(),
-              _tables(sin, T).data_ptr(), n, b, T, H, qkv.data_ptr() + 2 * moved_slot, 3 * W, stream)
+    _lib.call('noise_moved_heads', rawf.data_ptr(), a.data_ptr(), float(sigma), cos.data_ptr(), sin.data_ptr(), n, b,
+              T, H, qkv.data_ptr() + 2 * moved_slot, 3 * W, stream)
     y = torch.empty(n * b * T, W, device=a.device, dtype=torch.bfloat16)
     _lib.call('noise_attention', qkv.data_ptr(), n * b, T, int(window), 1, None, 0, y.data_ptr(), None, None, None,
               0, stream)

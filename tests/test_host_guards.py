@@ -74,5 +74,9 @@ def test_credit_wrappers_reject_bad_shapes_before_any_launch():
         credit.rerun('k', raw, a, 0.1, None, None, raw[:, :64], raw, 50)
     with pytest.raises(ValueError, match='matched filter'):
         credit.credit_chunk('k', raw, a, 0.1, None, None, raw, raw, 50, raw, raw, torch.zeros(1, 8, 128, 64))
+    with pytest.raises(ValueError, match='window'):
+        credit.rerun('q', raw, a, 0.1, None, None, raw, raw, -1)
+    with pytest.raises(ValueError, match='at least 128 rows'):
+        credit.rerun('q', raw, a, 0.1, torch.zeros(1, 100, 1, 32), torch.zeros(1, 100, 1, 32), raw, raw, 50)
     with pytest.raises(ValueError, match='CUDA'):
-        credit.rerun('q', raw, a, 0.1, None, None, raw, raw, 50)
+        credit.rerun('q', raw, a, 0.1, torch.zeros(1, 128, 1, 32), torch.zeros(1, 128, 1, 32), raw, raw, 50)
