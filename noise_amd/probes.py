@@ -34,6 +34,8 @@ def _run(base, C, rows, y, steps, sq, dots, dir_sq, width, per_token):
     if y.shape != (n,) or y.device.type != 'cuda':
         raise ValueError(f'y must be a CUDA tensor of shape ({n},)')
     if rows is not None:
+        if tuple(rows.shape) != (n, K) or rows.device.type != 'cuda':
+            raise ValueError(f'rows must be a CUDA tensor of shape ({n}, {K})')
         rows = rows.to(torch.int64).contiguous()
     out = torch.empty(n, K, device=base.device, dtype=torch.float32)
     _lib.call('noise_readout_probes', base.data_ptr(), V, C.data_ptr(), V, 0 if rows is None else rows.data_ptr(), K,

@@ -80,3 +80,11 @@ def test_credit_wrappers_reject_bad_shapes_before_any_launch():
         credit.rerun('q', raw, a, 0.1, torch.zeros(1, 100, 1, 32), torch.zeros(1, 100, 1, 32), raw, raw, 50)
     with pytest.raises(ValueError, match='CUDA'):
         credit.rerun('q', raw, a, 0.1, torch.zeros(1, 128, 1, 32), torch.zeros(1, 128, 1, 32), raw, raw, 50)
+
+
+def test_probe_rows_must_be_cuda():
+    from noise_amd import probes
+    z = torch.zeros
+    with pytest.raises(ValueError, match='CUDA'):
+        probes.row_derivatives(z(4, 256), z(8, 256), z(4, 2, dtype=torch.int64), z(4, dtype=torch.int64), z(4), z(4),
+                               z(4, 2), z(4, 2))
