@@ -85,18 +85,18 @@ class Eggroll:
         offsets = self.offsets(step)
         losses = torch.empty(per_rank, device=self.device)
         weights = Weights(self.params, self.model.config, self.pop.head)
-        chunk = min(self.pop.chunk, per_seq)
         lo, hi = self.rank * per_rank, (self.rank + 1) * per_rank
-        start = lo
-        while start < hi:
-            seq = start // per_seq
-            end = min(hi, start + chunk, (seq + 1) * per_seq)
-            directions = torch.arange(start, end, 2, device=self.device) % (2 * pairs) // 2
-            noise = self.noise(offsets, directions)
-            sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat((end - start) // 2)
-            losses[start - lo:end - lo] = self.pop.loss(self.params, noise, sign, x[seq], y[seq], pair_shift=1,
-                                                        weights=weights)
-            start = end
+        # every member of this rank in one call: member j reads sequence j // per_seq, so the population's
+        # chunks run across sequence boundaries (per-member token rows) instead of one pass per sequence
+        directions = torch.arange(lo, hi, 2, device=self.device) % (2 * pairs) // 2
+        noise = self.noise(offsets, directions)
+        sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat(per_rank // 2)
+        if len(x) == 1:
+            seq_x, seq_y = x[0], y[0]
+        else:
+            seq = torch.arange(lo, hi, device=self.device) // per_seq
+            seq_x, seq_y = x[seq], y[seq]
+        losses[:] = self.pop.loss(self.params, noise, sign, seq_x, seq_y, pair_shift=1, weights=weights)
         if self.world > 1:
             gathered = [torch.empty_like(losses) for _ in range(self.world)]
             torch.distributed.all_gather(gathered, losses)

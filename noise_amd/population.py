@@ -299,14 +299,18 @@ class Population:
 
     def loss(self, p, noise, sign, idx, targets, pair_shift=0, weights=None):
         """Per-member mean CE [m] fp32 (train/val/eggroll.py:66-103). noise rows are per member
-        (pair_shift 0, as population_loss receives them) or per antithetic pair (pair_shift 1)."""
-        m, T = sign.shape[0], idx.shape[0]
+        (pair_shift 0, as population_loss receives them) or per antithetic pair (pair_shift 1). idx and
+        targets are one sequence [T] shared by every member, or one row per member [m, T] (the members of
+        several sequences in one pass, as `Eggroll.step` spreads them, train/val/eggroll.py:133-143)."""
+        m, T = sign.shape[0], idx.shape[-1]
         dev = sign.device
         _need_cuda(sign, torch.float32, 'sign')
         _need_cuda(idx, torch.int64, 'idx')
         _need_cuda(targets, torch.int64, 'targets')
-        if targets.shape[0] != T:
-            raise ValueError('idx and targets must have the same length')
+        per_member = idx.dim() == 2
+        if idx.dim() not in (1, 2) or targets.shape != idx.shape or (per_member and idx.shape[0] != m):
+            raise ValueError(f'idx and targets must both be [T] or both [{m}, T]')
+        idx, targets = idx.contiguous(), targets.contiguous()
         if T % 128:
             raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')
         V = p['transformer.wte.weight'].shape[0]
@@ -325,8 +329,9 @@ class Population:
             c1 = min(m, c0 + step)
             r0, r1 = c0 >> pair_shift, (c1 + (1 << pair_shift) - 1) >> pair_shift
             chunk_noise = {n: _noise_rows(noise, n, r0, r1) for n in p}
-            forward_chunk(W, buf, chunk_noise, sign[c0:c1], idx, targets, pair_shift, out[c0:c1], cos, sin,
-                          self.windows)
+            ci, ct = (idx[c0:c1], targets[c0:c1]) if per_member else (idx, targets)
+            forward_chunk(W, buf, chunk_noise, sign[c0:c1], ci, ct, pair_shift, out[c0:c1], cos, sin,
+                          self.windows, tok_mstride=T if per_member else 0)
         return out
 
 

@@ -657,3 +657,51 @@ def test_fitness_update_adam_match_oracle():
                   1e-3 / (1 - 0.5 ** step), 0.5, 0.95, 1e-8, math.sqrt(1 - 0.95 ** step), s)
         torch.cuda.synchronize()
     assert torch.allclose(param.cpu(), ref_p, atol=1e-6, rtol=1e-6)
+
+
+def test_eggroll_step_two_sequences_matches_oracle():
+    """One whole `Eggroll.step` on the GPU (train/val/eggroll.py:130-168) with two sequences of 256 tokens and
+    4 antithetic pairs (8 members, 4 per sequence, all in one pass through per-member token rows) at the
+    reference's initialisation: member losses within 1e-4 of the bf16-mode oracle on the reference's noise
+    slices; then fitness, update and Adam from those losses against the oracle's composition
+    (torch.optim.AdamW semantics, weight decay 0)."""
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.optim import Adam
+    pairs, T, step = 4, 256, 3
+    model = make_model(DEV, 0)
+    before = {n: p.detach().cpu().clone() for n, p in model.named_parameters()}
+    shapes = {n: tuple(p.shape) for n, p in before.items()}
+    seqs = [zipf_tokens(T, seed=21), zipf_tokens(T, seed=22)]
+    x = torch.stack([s_[0] for s_ in seqs]).to(DEV)
+    y = torch.stack([s_[1] for s_ in seqs]).to(DEV)
+    es = Eggroll(model, pairs, chunk=8, noise_len=1 << 20, sigma=oe.SIGMA)
+    opt = Adam(model.parameters(), lr=oe.LR, betas=oe.BETAS, eps=oe.ADAM_EPS)
+    log_case(f'Eggroll.step pairs={pairs} sequences=2 T={T}')
+    es.step(x, y, opt, step)
+    torch.cuda.synchronize()
+    losses = es.last_losses.cpu()
+    buf = es.buffer.cpu()
+    # the step's offsets come from the device generator (train/val/eggroll.py:117-120): taken as given
+    offs = {n: o.cpu() for n, o in es.offsets(step).items()}
+    per_seq = 2 * pairs // 2  # members per sequence
+    for s_ in range(2):
+        dirs = oe.member_directions(s_ * per_seq, per_seq // 2, pairs)
+        g_ = oe.gather_noise(buf, offs, shapes, dirs)
+        noise = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
+                 for n, v in g_.items()}
+        sign = torch.tensor([oe.SIGMA, -oe.SIGMA]).repeat(per_seq // 2)
+        ref = om.population_loss(before, noise, sign, seqs[s_][0], seqs[s_][1], mode='bf16', head='fp32')
+        got = losses[s_ * per_seq:(s_ + 1) * per_seq]
+        assert (got - ref).abs().max() < 1e-4, (s_, got, ref)
+    f, w = oe.fitness(losses, pairs)
+    grads = oe.update(w, oe.gather_noise(buf, offs, shapes, torch.arange(pairs)), len(f))
+    for n, p in model.named_parameters():
+        g_ref = grads[n].reshape(p.shape)
+        g_got = p.grad.detach().cpu()
+        assert torch.allclose(g_got, g_ref, atol=1e-6 * float(g_ref.abs().max()) + 1e-12, rtol=1e-4), n
+        # Adam's first step moves every element by about lr sign(grad): a gradient within rounding of zero may
+        # take the other sign, so the parameters are compared element-wise on all but a few such elements
+        ref_p = oe.adam_step(before[n].clone(), g_ref, torch.zeros_like(g_ref), torch.zeros_like(g_ref), 1, oe.LR)
+        d = (p.detach().cpu() - ref_p).abs()
+        assert float((d <= 1e-6 + 1e-5 * ref_p.abs()).float().mean()) > 0.999, n
+        assert float(d.max()) <= 2.5 * oe.LR, n
