@@ -85,7 +85,9 @@ def attention(q, k, v, window, qk_norm=False):
     """Causal attention with a left window on [batch, token, head, 64] tensors (utils/model.py:24-31) on the
     attention kernel: q and k bf16, v the bf16-rounded value in fp16 (the kernel's operand format), P in fp16,
     bf16 output. 8 heads; token count a multiple of 128. qk_norm declares RMS-normalised q, k rows (the
-    credit reruns' processed heads), which lets the softmax skip its running maximum."""
+    credit reruns' processed heads), which lets the softmax skip its running maximum. fp16 holds every bf16
+    value of magnitude 2^-14 .. 65504 exactly; smaller ones lose low bits (absolute error < 2^-25) and larger
+    ones overflow, far outside the activations of this model."""
     B, T, H, hd = q.shape
     if hd != HD or H != 8 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError('q, k, v must be [batch, token, 8, 64] of one shape')
