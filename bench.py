@@ -351,7 +351,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: every box in this build has a single MI355X; --gpus {args.gpus} '
-              f'is not supported (members shard across GPUs by design; see DESIGN.md).', file=sys.stderr)
+              f'is not supported (the population would shard by members across GPUs, one loss all-gather per '
+              f'step; that path is not built here).', file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
