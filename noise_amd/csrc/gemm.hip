@@ -253,7 +253,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // Tile order: row block outer, column tile inner, except for the head (EPI_CE: 16 column tiles of a W that
   // does not fit an XCD's L2), which walks groups of CE_GROUP row blocks per column tile so each W column tile
   // is read once per group rather than once per row block (measured: config 3 15.4 -> 14.7 ms; groups of 4:
-  // 14.8, 32: 17.4).
+  // 14.8, 16: 15.3, 32: 17.4).
   constexpr int CE_GROUP = 8;
   auto tile_mn = [&](int t, int which) {
     if (EPI == EPI_CE) {
