@@ -304,12 +304,12 @@ class Population:
         several sequences in one pass, as `Eggroll.step` spreads them, train/val/eggroll.py:133-143)."""
         m, T = sign.shape[0], idx.shape[-1]
         dev = sign.device
-        _need_cuda(sign, torch.float32, 'sign')
-        _need_cuda(idx, torch.int64, 'idx')
-        _need_cuda(targets, torch.int64, 'targets')
         per_member = idx.dim() == 2
         if idx.dim() not in (1, 2) or targets.shape != idx.shape or (per_member and idx.shape[0] != m):
             raise ValueError(f'idx and targets must both be [T] or both [{m}, T]')
+        _need_cuda(sign, torch.float32, 'sign')
+        _need_cuda(idx, torch.int64, 'idx')
+        _need_cuda(targets, torch.int64, 'targets')
         idx, targets = idx.contiguous(), targets.contiguous()
         if T % 128:
             raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')

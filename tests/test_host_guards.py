@@ -88,3 +88,16 @@ def test_probe_rows_must_be_cuda():
     with pytest.raises(ValueError, match='CUDA'):
         probes.row_derivatives(z(4, 256), z(8, 256), z(4, 2, dtype=torch.int64), z(4, dtype=torch.int64), z(4), z(4),
                                z(4, 2), z(4, 2))
+
+
+def test_population_loss_rejects_mismatched_token_rows():
+    """idx / targets are one shared [T] sequence or one [m, T] row per member; anything else is refused
+    before any launch."""
+    pop = population.Population.__new__(population.Population)
+    sign = torch.zeros(4)
+    i64 = torch.int64
+    for idx, tgt in ((torch.zeros(3, 128, dtype=i64), torch.zeros(3, 128, dtype=i64)),   # 3 rows for 4 members
+                     (torch.zeros(4, 128, dtype=i64), torch.zeros(128, dtype=i64)),      # shapes differ
+                     (torch.zeros(1, 4, 128, dtype=i64), torch.zeros(1, 4, 128, dtype=i64))):
+        with pytest.raises(ValueError, match=r'both be \[T\]'):
+            pop.loss({}, {}, sign, idx, tgt)
