@@ -254,7 +254,7 @@ def run_attention(args):
         qk = qkv[:, :2 * D].view(P * T, 16, 64)
         qkv[:, :2 * D] = (qk * torch.rsqrt(qk.pow(2).mean(-1, keepdim=True) + 2 ** -23)).view(P * T, 2 * D)
     qkv16 = qkv.to(torch.bfloat16)
-    # v as fp16 holding the bf16 value, the format noise_qkv writes
+    # config 2's bf16 q, k (qk_f16 = 0 below); v travels as fp16 (here holding the bf16 value exactly)
     qkv16[:, 2 * D:] = qkv16[:, 2 * D:].half().view(torch.bfloat16)
     qkv = qkv16
     y = torch.empty(P * T, D, device=dev, dtype=torch.bfloat16)
@@ -265,7 +265,7 @@ def run_attention(args):
     s = torch.cuda.current_stream().cuda_stream
 
     def step():
-        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, int(args.qk_norm), bp.data_ptr(), 0, y.data_ptr(),
+        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, int(args.qk_norm), 0, bp.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), s)
     ms_step, ms_launch = _timed(step, args.steps, args.warmup)
     pairs = sum(min(q, window) + 1 for q in range(T))

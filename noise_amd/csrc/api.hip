@@ -255,7 +255,7 @@ int noise_attention_workspace_size(int members, int T, size_t* bytes) {
   return NOISE_OK;
 }
 
-int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, const float* b_proj,
+int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16, const float* b_proj,
                     int pair_shift, void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
@@ -277,6 +277,7 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
   g.H = NH;
   g.window = window;
   g.qk_norm = qk_norm != 0;
+  g.qk_f16 = qk_f16 != 0;
   g.b_proj = b_proj;
   g.b_ld = DM;
   g.pair_shift = pair_shift;

@@ -3,13 +3,14 @@
 #include <hip/hip_runtime.h>
 
 struct AttnArgs {
-  const __bf16* qkv;  // [members * T, ldq] rows; q at column h*64, k at koff + h*64, v at voff + h*64
+  const __bf16* qkv;  // [members * T, ldq] 16-bit rows; q at column h*64, k at koff + h*64, v (fp16) at voff + h*64
   long ldq;
   int koff, voff;
   __bf16* y;          // [members * T, ldy], head h at columns h*64 .. h*64+63
   long ldy;
   int members, T, H, window;
   int qk_norm;        // q and k rows are RMS-normalised (scores bounded by 8.03): no running maximum
+  int qk_f16;         // q and k are fp16 (the population path: written from fp32) rather than bf16
   // c_proj input-side dot partials: upart[row * upart_ld + h] = sum_d y[row, h*64+d] bf16(b_proj[dir, h*64+d])
   const float* b_proj;
   long b_ld;

@@ -3,8 +3,11 @@
 //
 // Reference: `attention` / `window_mask` (utils/model.py:14-31) called from population_loss
 // (train/val/eggroll.py:91): softmax(q k^T / sqrt(64)) v, a query at s seeing keys k with
-// s - window <= k <= s. q and k arrive bf16 (rotary and QK-norm already applied by the QKV GEMM), v arrives
-// as fp16 holding the bf16-rounded value exactly.
+// s - window <= k <= s. In the population forward q, k and v arrive as fp16 written from the fp32 values the
+// reference feeds flex (rotary and QK-norm already applied by the QKV kernels): an 11-bit significand, the
+// precision class of the TF32 attention the reference runs under set_float32_matmul_precision('high')
+// (train/val/eggroll.py:184). The credit reruns (train/val/run.py:594-634) run attention on bf16 q and k, as
+// the reference does there; the q/k element type is a template parameter, v is fp16 in both.
 //
 // One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; four workgroups per CU (122
 // VGPRs, 34 KiB of LDS each: 4 waves per SIMD hide the LDS and transcendental latencies).
@@ -12,7 +15,7 @@
 // (global_load_lds_dwordx4, issued from inline assembly so the compiler adds no LDS-wide waits): while block j
 // is computed, block j + 1 lands; one s_waitcnt vmcnt(0) + s_barrier per block (the loads are the only
 // vector memory operations in the loop). Nothing passes through registers on the way in.
-//   S^T = K Q^T (bf16 MFMA, A = K rows, B = Q rows): lane l holds 16 scores of query l % 16. The K rows
+//   S^T = K Q^T (fp16 or bf16 MFMA, A = K rows, B = Q rows): lane l holds 16 scores of query l % 16. The K rows
 //   of each 16-row MFMA block are interleaved at load time (block kb, row r <-> key
 //   32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4), so the scores' register layout IS the B operand of P V;
 //   P never leaves registers.
@@ -50,6 +53,14 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 __device__ __forceinline__ f32x4 mfma16x16x32_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+// The score MFMA on 8 16-bit q / k elements per lane, fp16 (F16) or bf16.
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_qk(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  if constexpr (F16)
+    return mfma16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c);
+  else
+    return mfma16x16x32(a, b, c);
+}
 
 // K tile [BKV keys][64 dims] bf16, 128-byte rows, 16-byte chunks XOR-swizzled by row.
 __device__ __forceinline__ int kswz(int r, int c) { return r * HD + ((c ^ (r & 7)) << 3); }
@@ -70,11 +81,12 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
   return *reinterpret_cast<unsigned*>(&p);
 }
 
-// QKN: q and k rows are RMS-normalised (||q||, ||k|| <= 8 up to bf16 rounding), so every score s = q.k / 8
+// QKN: q and k rows are RMS-normalised (||q||, ||k|| <= 8 up to 16-bit rounding), so every score s = q.k / 8
 // satisfies |s| <= 8.03 and 2^(s log2(e) / 8) <= 3.1e3: the probabilities need no running maximum (they stay
 // normal fp16 numbers and their sums stay far from fp32 overflow), which removes the max reduction, its
 // cross-lane shuffles and the rescaling from the loop. Softmax is shift-invariant, so the result is the same.
-template <bool QKN>
+// F16: q and k are fp16 (bf16 otherwise); they travel as raw 16-bit lanes and only the score MFMA reads their type.
+template <bool QKN, bool F16>
 __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   __shared__ __attribute__((aligned(1024))) bf16 sk[2][BKV * HD];
   __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
@@ -230,8 +242,8 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-        a = mfma16x16x32(k0, qf[qb][0], a);
-        s[qb][kb] = mfma16x16x32(k1, qf[qb][1], a);
+        a = mfma_qk<F16>(k0, qf[qb][0], a);
+        s[qb][kb] = mfma_qk<F16>(k1, qf[qb][1], a);
       }
     }
     // blocks away from the causal edge and the window edge need no mask
@@ -344,10 +356,14 @@ int attention_launch(const AttnArgs& g, hipStream_t s) {
   if (g.mom && !g.mom_out) return NOISE_EINVAL;
   const long grid = (long)(g.T / BQ) * g.H * g.members;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
-  if (g.qk_norm)
-    hipLaunchKernelGGL(attention_kernel<true>, dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  if (g.qk_norm && g.qk_f16)
+    hipLaunchKernelGGL((attention_kernel<true, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  else if (g.qk_norm)
+    hipLaunchKernelGGL((attention_kernel<true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  else if (g.qk_f16)
+    hipLaunchKernelGGL((attention_kernel<false, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else
-    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   NOISE_CHECK_LAUNCH();
   if (g.mom) {
     const long n = (long)g.members * g.H * 2 * HD;

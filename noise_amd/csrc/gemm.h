@@ -10,7 +10,7 @@ enum : int {
                   //                                         (weight-resident kernel of gemm_xs.hip, K = 512)
   EPI_RESID = 2,  // resid += lowrank(x)                     -> fp32 read-modify-write
   EPI_QKV = 3,    // q|k|v = lowrank(x) per 512-column segment; rotary + RMSNorm on q and k, gated value
-                  // embedding added to v                   -> bf16 store
+                  // embedding added to v                   -> fp16 store of the fp32 values
   EPI_CE = 4,     // z = 15 tanh(lowrank(x) / 15); per row partial sum of exp(z) over each wave's columns
                   // and z at the target column             -> fp32 partials
   EPI_DENSE = 5,  // y = bf16(x W^T) only: the rank-1 term and the residual add are left to the row kernel

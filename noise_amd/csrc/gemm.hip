@@ -110,10 +110,10 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
   return *reinterpret_cast<unsigned*>(&p);
 }
-// fp16 pair of the bf16-rounded values (exact: |v| < 65504 and bf16's 8-bit significand fits fp16's 11 bits;
-// magnitudes below 2^-14 become fp16 subnormals)
-__device__ __forceinline__ unsigned pack_f16_of_bf16(float a, float b) {
-  _Float16 __attribute__((ext_vector_type(2))) p = {(_Float16)bf16r(a), (_Float16)bf16r(b)};
+// fp16 pair (round to nearest even) of two fp32 values: q, k and v enter attention with an 11-bit significand,
+// the precision class of the reference's TF32 flex attention on fp32 operands (|v| must stay below 65504)
+__device__ __forceinline__ unsigned pack_f16(float a, float b) {
+  _Float16 __attribute__((ext_vector_type(2))) p = {(_Float16)a, (_Float16)b};
   return *reinterpret_cast<unsigned*>(&p);
 }
 
@@ -418,20 +418,12 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           for (int e = 0; e < CW; ++e) v[e] += gt * (wr[e] + sa * br[e]);
         }
         if (live) {
+          // q, k and v: fp16 of the fp32 values (the reference feeds flex fp32 operands, train/val/eggroll.py:91)
           bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
-          if (seg < 2) {
 #pragma unroll
-            for (int e = 0; e < CW; e += 8)
-              store_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]),
-                              pack_bf16(v[e + 4], v[e + 5]), pack_bf16(v[e + 6], v[e + 7]));
-          } else {
-            // v: the bf16-rounded value (the autocast rounding point) stored as fp16, which holds it exactly, so
-            // attention can feed it to fp16 MFMAs straight from memory
-#pragma unroll
-            for (int e = 0; e < CW; e += 8)
-              store_x4(o + e, pack_f16_of_bf16(v[e], v[e + 1]), pack_f16_of_bf16(v[e + 2], v[e + 3]),
-                              pack_f16_of_bf16(v[e + 4], v[e + 5]), pack_f16_of_bf16(v[e + 6], v[e + 7]));
-          }
+          for (int e = 0; e < CW; e += 8)
+            store_x4(o + e, pack_f16(v[e], v[e + 1]), pack_f16(v[e + 2], v[e + 3]), pack_f16(v[e + 4], v[e + 5]),
+                            pack_f16(v[e + 6], v[e + 7]));
         }
       } else {  // EPI_CE
         // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,

@@ -58,8 +58,8 @@ constexpr int SIGN_OFF = VEC - 8;
 enum : int {
   XS_RELU2 = 0,  // MLP c_fc: bf16(relu(lowrank)^2) + partial dots with b_next
   XS_DENSE = 1,  // c_proj dense product y = bf16(x W^T), row-major
-  XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, bf16
-  XS_V = 3,      // c_v without value embedding: lowrank, the bf16-rounded value stored as fp16
+  XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, fp16 of the fp32 result
+  XS_V = 3,      // c_v without value embedding: lowrank, fp16 of the fp32 result
 };
 // per wave and block: 4 x rows, then the mode's vectors (relu^2: a|b_next|u and the sign; q|k: a, and one
 // of cos / sin / u|sign / padding)
@@ -87,6 +87,11 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   return *reinterpret_cast<unsigned*>(&p);
 }
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned v) { return *reinterpret_cast<bf16x2*>(&v); }
+// fp16 pair (round to nearest even) of two fp32 values: q, k and v enter attention with an 11-bit significand
+__device__ __forceinline__ unsigned pack_f16(float a, float b) {
+  _Float16 __attribute__((ext_vector_type(2))) p = {(_Float16)a, (_Float16)b};
+  return *reinterpret_cast<unsigned*>(&p);
+}
 
 // q|k mode column map: slice s covers segment s / 2 (q, k), heads 4 (s % 2) .. + 3; wave w takes head
 // 4 (s % 2) + w / 2 and, of its 64 dims, half h = w % 2: local columns 0-15 are dims 16 h .. 16 h + 15 and
@@ -239,8 +244,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
     if constexpr (VV) {
-      // stages 0: vectors; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 as fp16 pairs
-      // holding the bf16-rounded value (exact); 5 / 10: the row half's store
+      // stages 0: vectors; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 (fp32, as the
+      // reference's lowrank output) as fp16 pairs; 5 / 10: the row half's store
       const QkVec& q = qv[pbuf];
       const int r = lane & 15;
       if (st == 0) {
@@ -260,8 +265,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
         const float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
         const float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
-        _Float16 __attribute__((ext_vector_type(2))) hp = {(_Float16)bf16r(v0), (_Float16)bf16r(v1)};
-        ev_h[i][sub] = *reinterpret_cast<unsigned*>(&hp);
+        ev_h[i][sub] = pack_f16(v0, v1);
       } else {
         store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       }
@@ -270,7 +274,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     if constexpr (QK) {
       // Iteration k runs, for block pk - 1 (held from iteration k - 1): stages 0 / 1, the head's RMSNorm
       // (utils/model.py:46-47, eps = 2^-23) of row half 0 / 1 from both waves' sums of squares, written
-      // to LDS last iteration and visible since this iteration's barrier, and the bf16 store; for block pk:
+      // to LDS last iteration and visible since this iteration's barrier, and the fp16 store; for block pk:
       // stage 2 the vectors, 3-6 / 8-11 v = bf16(dense) + s bf16(u) a of row half 0 / 1, 7 / 12 rotary
       // (utils/model.py:55-58) and the wave's sum of squares into LDS.
       const QkVec& q = qv[pbuf];
@@ -282,7 +286,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         const float rn = rsqrtf(tot * (1.f / 64.f) + 1.1920928955078125e-07f);
         u32x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = pack_bf16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
+        for (int e = 0; e < 4; ++e) o[e] = pack_f16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
         store_half(blk_of(pk - 1), i, o);
         return;
       }

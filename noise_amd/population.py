@@ -221,7 +221,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         ap, bp = noise[pre + 'attn.c_proj.weight']
         t0 = tm.mark('attention')
         # q and k come out of noise_qkv RMS-normalised
-        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], int(QK_NORM), _p(bp), ps, _p(buf.y), _p(buf.u_attn),
+        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], int(QK_NORM), 1, _p(bp), ps, _p(buf.y), _p(buf.u_attn),
                   0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')

@@ -11,8 +11,8 @@ Two rounding modes:
 * ``mode='bf16'`` -- the rounding points of the reference under CUDA bf16 autocast
   (`train/val/eggroll.py:144`): every GEMM (including the rank-1 GEMV ``x @ b``) rounds both operands
   to bf16, accumulates in fp32 and rounds its output to bf16; the rank-1 correction and the residual
-  stream stay fp32. One rounding point is the MI355X kernel's own choice, not the reference's:
-  q, k and v are rounded to bf16 before attention (flex runs on fp32 q/k/v in the reference).
+  stream stay fp32. q, k and v stay fp32 into attention, as in the reference (flex attention is not
+  covered by autocast); the attention output y is rounded to bf16 where the c_proj GEMM casts it.
 
 ``head='fp32'`` evaluates the lm_head GEMM in float32 (the north star's fp32 head); ``head='bf16'`` is
 the reference's autocast head.
@@ -162,8 +162,8 @@ def population_loss(p, noise, sign, idx, targets, mode='fp32', head='fp32', cos=
             gate = 2 * torch.sigmoid(linear('attn.ve_gate.weight', h[..., :32]))
             v = v + gate.unsqueeze(-1) * ve
         q, k = norm(apply_rotary(q, cos, sin)), norm(apply_rotary(k, cos, sin))
-        if mode == 'bf16':
-            q, k, v = bf(q), bf(k), bf(v)
+        # q, k, v reach attention in fp32 (the fp32 rank-1 term promotes lowrank's output; flex runs on fp32
+        # operands at TF32 under set_float32_matmul_precision('high'), train/val/eggroll.py:58, :90-91, :184)
         y = attention(q, k, v, windows[i]).reshape(m, length, -1)
         if mode == 'bf16':
             y = bf(y)

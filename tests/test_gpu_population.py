@@ -148,12 +148,15 @@ def test_block_entry_and_qkv_match_oracle():
     c, sn = cos[:T], sin[:T]
     qr = om.norm(om.apply_rotary(q.view(m, T, 8, 64), c, sn))
     kr = om.norm(om.apply_rotary(kk_.view(m, T, 8, 64), c, sn))
-    got = qkv.cpu().float().view(m, T, 3, 8, 64)
-    # the v segment is written as fp16 (the bf16-rounded value, exactly)
-    got[:, :, 2] = qkv[:, 1024:].cpu().view(torch.float16).float().view(m, T, 8, 64)
+    # q, k and v are written as fp16 of the fp32 values (11-bit significand): the error is fp16 rounding plus
+    # the dense product's bf16 rounding, which a different fp32 summation order can move by one bf16 step
+    got = qkv.cpu().view(torch.float16).float().view(m, T, 3, 8, 64)
     for k, ref in enumerate((qr, kr, vv)):
-        assert rel_err(got[:, :, k], om.bf(ref)) < 5e-3, k
+        assert rel_err(got[:, :, k], ref) < 2e-3, k
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
+    # fp16, not bf16: rounding the fp32 result to fp16 changes it by at most 2^-11 relative, and the GPU's
+    # values agree with that rounding far better than bf16 rounding would allow
+    assert rel_err(got[:, :, 0], qr.half().float()) < rel_err(om.bf(qr), qr)
     # a block without value embedding (gate null): the same q | k, v = lowrank only
     log_case(f'qkv without value embedding m={m} T={T}')
     qkv2 = torch.empty_like(qkv)
@@ -164,7 +167,7 @@ def test_block_entry_and_qkv_match_oracle():
     assert torch.equal(qkv2[:, :1024].cpu(), qkv[:, :1024].cpu())
     v2 = qkv2[:, 1024:].cpu().view(torch.float16).float().view(m, T, 512)
     vref = lin(wv, av, 2)
-    assert rel_err(v2, om.bf(vref)) < 5e-3
+    assert rel_err(v2, vref) < 2e-3
     assert (v2 - vref).abs().max() <= 2 ** -7 * vref.abs().max() + 1e-3
 
 
@@ -277,29 +280,31 @@ def test_mlp_hidden_tile16_matches_rows():
     assert ((ya.cpu().float() - refa).abs() <= refa.abs() * 2 ** -7 + 1e-6).all()
 
 
-@pytest.mark.parametrize('qk_norm', [0, 1])
-def test_attention_matches_oracle_and_moments(qk_norm):
+@pytest.mark.parametrize('qk_norm,qk_f16', [(0, 0), (1, 0), (1, 1), (0, 1)])
+def test_attention_matches_oracle_and_moments(qk_norm, qk_f16):
     """qk_norm = 0: any q, k (running-maximum softmax); qk_norm = 1: q, k RMS-normalised per head as the
-    model's QK-norm leaves them (bounded scores, no running maximum), including rows scaled to the bound."""
+    model's QK-norm leaves them (bounded scores, no running maximum), including rows scaled to the bound.
+    qk_f16 = 1: q and k fp16 (the population forward's format), 0: bf16 (the credit reruns'); v fp16."""
     g = torch.Generator().manual_seed(2)
     m, T = 2, 256
+    dt = torch.float16 if qk_f16 else torch.bfloat16
     for window in (T, 100):
-        log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm}')
-        q, k, v = (torch.randn(m, T, 8, 64, generator=g).bfloat16() for _ in range(3))
+        log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm} qk_f16={qk_f16}')
+        q, k, v = (torch.randn(m, T, 8, 64, generator=g) for _ in range(3))
         if qk_norm:
-            q, k = om.norm(q.float()).bfloat16(), om.norm(k.float()).bfloat16()
+            q, k = om.norm(q), om.norm(k)
             # extreme case: every key of the first head equal to its query direction (scores at the bound)
             k[:, :, 0] = q[:, :, 0]
-        # v travels as fp16 holding the bf16 value (the format noise_qkv writes)
-        v16 = v.half().view(torch.bfloat16)
-        qkv = torch.cat([q.reshape(m * T, 512), k.reshape(m * T, 512), v16.reshape(m * T, 512)], 1).to(DEV)
+        q, k, v = q.to(dt), k.to(dt), v.half()
+        qkv = torch.cat([q.reshape(m * T, 512).view(torch.bfloat16), k.reshape(m * T, 512).view(torch.bfloat16),
+                         v.reshape(m * T, 512).view(torch.bfloat16)], 1).to(DEV)
         y = torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
         bp = torch.randn(m, 512, generator=g)
         bpd = bp.to(DEV)
         up = torch.empty(m * T, 8, device=DEV)
         mom = torch.empty(m, 8, 2, 64, device=DEV)
         ws = torch.empty(_lib.size_query('noise_attention_workspace_size', m, T), device=DEV, dtype=torch.uint8)
-        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, bpd.data_ptr(), 0, y.data_ptr(),
+        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, qk_f16, bpd.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
@@ -386,20 +391,21 @@ def _population_case(model, params, P, T, sigma, seed, head='fp32'):
     return got, noise, sign, idx, tgt
 
 
-def _oracle_with_floor(params, noise, sign, idx, tgt):
+def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False):
     """bf16-mode oracle losses, and how far they move under three equally valid changes of rounding: every
-    GEMM accumulating in fp64 instead of fp32, attention computed in fp64, and attention probabilities
-    rounded to fp16. The largest move (per loss and per antithetic difference) is the floor: at trained-scale
+    GEMM accumulating in fp64 instead of fp32, attention computed in fp64, and attention at TF32-class
+    precision (q, k, v and the probabilities rounded to fp16, the reference's TF32 flex attention's
+    significand). The largest move (per loss and per antithetic difference) is the floor: at trained-scale
     weights the bf16 path is chaotic, and one alternative alone under-samples how far valid roundings diverge
     (the CPU oracle's own results also shift with the host's summation order)."""
     ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
     orig_attn = om.attention
 
     def attention_p16(q, k, v, window, dtype=torch.float32):
-        # probabilities rounded to fp16 before P V (11-bit significand, the precision class of the
+        # q, k, v and the probabilities rounded to fp16 (11-bit significand, the precision class of the
         # reference's TF32 flex attention); normalised by the sum of the rounded probabilities
         B, T, H, D = q.shape
-        qh, kh, vh = (t.transpose(1, 2).float() for t in (q, k, v))
+        qh, kh, vh = (t.transpose(1, 2).half().float() for t in (q, k, v))
         scores = qh @ kh.transpose(-1, -2) / math.sqrt(D)
         pos = torch.arange(T)
         mask = (pos[:, None] >= pos[None, :]) & (pos[:, None] - pos[None, :] <= window)
@@ -431,6 +437,8 @@ def _oracle_with_floor(params, noise, sign, idx, tgt):
         om.lowrank = orig
     floor = max(float((a - ref).abs().max()) for a in (alt, *alts))
     pair_floor = max(float(((a[1::2] - a[0::2]) - (ref[1::2] - ref[0::2])).abs().max()) for a in (alt, *alts))
+    if return_alts:
+        return ref, floor, pair_floor, [alt, *alts]
     return ref, floor, pair_floor
 
 
@@ -531,8 +539,12 @@ def test_population_loss_pair_shift_equals_per_member(trained):
 
 
 def test_population_loss_golden_reference_fp32(golden):
-    """The kernels against the reference's own fp32 CPU losses (tests/golden): the difference is the
-    bf16 rounding of the autocast path, bounded well inside the antithetic signal's scale."""
+    """The kernels against the reference's own fp32 CPU losses (tests/golden) at trained-scale weights: the
+    difference is the bf16 rounding of the autocast GEMMs. Bound: twice the gap between the bf16 rounding class
+    and those fp32 losses, plus 1e-4. The gap is measured here as the largest distance from the golden losses of
+    the bf16-mode oracle (fp32 attention operands, as the reference) and of its three alternative roundings
+    (2.0e-3 .. 2.5e-3 on losses, 1.8e-3 .. 2.2e-3 on antithetic differences on the build host; the CPU's own
+    summation order moves each by ~1e-3)."""
     model = trained_like(make_model('cpu', 0))
     params = {n: p.detach().clone() for n, p in model.named_parameters()}
     P, T = 2 * golden['pairs'], golden['T']
@@ -546,7 +558,76 @@ def test_population_loss_golden_reference_fp32(golden):
     got = Population(gm, chunk=P).loss(dict(gm.named_parameters()), _dev(noise), sign.to(DEV), idx.to(DEV),
                                        tgt.to(DEV)).cpu()
     ref = torch.tensor(golden['losses_trained'])
-    assert (got - ref).abs().max() < 2e-2, (got, ref)
+    b16, _, _, alts = _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=True)
+    dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
+    gap = max(float((x - ref).abs().max()) for x in (b16, *alts))
+    pair_gap = max(float(((x[1::2] - x[0::2]) - dr).abs().max()) for x in (b16, *alts))
+    assert gap < 5e-3 and pair_gap < 5e-3, (gap, pair_gap)
+    assert (got - ref).abs().max() <= 2 * gap + 1e-4, (got, ref, gap)
+    assert (dg - dr).abs().max() <= 2 * pair_gap + 1e-4, (dg, dr, pair_gap)
+
+
+def _spearman(a, b):
+    ra = torch.argsort(torch.argsort(a)).double()
+    rb = torch.argsort(torch.argsort(b)).double()
+    ra, rb = ra - ra.mean(), rb - rb.mean()
+    return float((ra @ rb) / (ra.norm() * rb.norm()))
+
+
+@pytest.mark.timeout(600)
+def test_es_signal_survives_at_trained_scale(trained):
+    """At trained-scale weights a 1e-4 bar on losses cannot hold (equally valid roundings move them by ~3e-3), so
+    this checks what the update consumes (train/val/eggroll.py:151-163): 64 antithetic pairs at T = 256.
+    - The pair differences L(theta - sE) - L(theta + sE) rank like the oracle's: 1 - Spearman(GPU, oracle) at
+      most 1.5x the oracle's own disagreement with its alternative roundings (fp64 GEMM accumulation; TF32-class
+      fp16 attention).
+    - Every pair whose oracle difference exceeds twice the pair floor has the same sign on the GPU.
+    - The update -sum_j w_j a_j b_j^T / n built on the GPU (z-score fitness + grouped outer products) from the GPU
+      losses points where the oracle's does from the oracle losses: cosine >= 0.99 for lm_head and a c_fc."""
+    from noise_amd.population import Population
+    from oracle import eggroll as oe_
+    model, params = trained
+    pairs, T = 64, 256
+    P = 2 * pairs
+    log_case(f'ES signal pairs={pairs} T={T} trained-scale weights')
+    shapes = {n: tuple(t.shape) for n, t in params.items()}
+    per_dir = population_noise(shapes, pairs, seed=41, per_member=False)
+    per_mem = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
+               for n, v in per_dir.items()}
+    sign = antithetic_signs(P, 1e-3)
+    idx, tgt = zipf_tokens(T, seed=42)
+    gm = _gpu_model(model)
+    dnoise = _dev(per_dir)
+    got = Population(gm, chunk=P).loss(dict(gm.named_parameters()), dnoise, sign.to(DEV), idx.to(DEV),
+                                       tgt.to(DEV), pair_shift=1)
+    s = torch.cuda.current_stream().cuda_stream
+    fit = torch.empty(pairs, device=DEV)
+    w = torch.empty(pairs, device=DEV)
+    _lib.call('noise_fitness', got.data_ptr(), P, pairs, _lib.FITNESS_ZSCORE, fit.data_ptr(), w.data_ptr(), s)
+    names = ['lm_head.weight', 'transformer.h.3.mlp.c_fc.weight']
+    upd = {}
+    for n in names:
+        a, b = dnoise[n]
+        upd[n] = torch.empty(a.shape[1], b.shape[1], device=DEV)
+        _lib.call('noise_outer_update', a.data_ptr(), a.shape[1], b.data_ptr(), b.shape[1], w.data_ptr(), pairs,
+                  a.shape[1], b.shape[1], -1.0 / pairs, upd[n].data_ptr(), s)
+    torch.cuda.synchronize()
+    got = got.cpu()
+    log_case('ES signal: oracle and its alternative roundings')
+    ref, _, pair_floor, alts = _oracle_with_floor(params, per_mem, sign, idx, tgt, return_alts=True)
+    dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
+    rho = _spearman(dg, dr)
+    rho_alt = [_spearman(a[1::2] - a[0::2], dr) for a in alts]
+    assert 1 - rho <= 1.5 * max(1 - r for r in rho_alt) + 1e-4, (rho, rho_alt)
+    big = dr.abs() > 2 * pair_floor
+    assert int(big.sum()) >= pairs // 2, (int(big.sum()), pair_floor)
+    assert torch.equal(torch.sign(dg[big]), torch.sign(dr[big]))
+    _, w_ref = oe_.fitness(ref, pairs)
+    ref_upd = oe_.update(w_ref, {n: per_dir[n] for n in names}, pairs)
+    for n in names:
+        a_, b_ = upd[n].cpu().flatten(), ref_upd[n].flatten()
+        cos = float(a_ @ b_ / (a_.norm() * b_.norm()))
+        assert cos >= 0.99, (n, cos)
 
 
 # ---------------------------------------------------------------- update path
