@@ -170,6 +170,18 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
                     int pair_shift, void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream);
 
+/* noise_attention without a workspace argument: no counterpart in the reference. It is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The moments' partials go to a library-owned device array of NOISE_ATTENTION_NOALLOC_MAX_PARTIALS floats
+ * (16 MiB, one copy per GPU, held until the process ends), so with mom != null the call needs
+ * members * (T / 128) * 8 * 128 <= NOISE_ATTENTION_NOALLOC_MAX_PARTIALS (P = 256 members at T = 2048 fits) and
+ * returns NOISE_ENOSPC beyond it, before any GPU work. It calls no hipMalloc / hipFree. Calls that overlap on one
+ * GPU share that array and race: serialise them (one stream, or events). Results equal noise_attention's. */
+#define NOISE_ATTENTION_NOALLOC_MAX_PARTIALS (4 * 1024 * 1024)
+int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16,
+                            const float* b_proj, int pair_shift, void* y, float* upart, float* mom,
+                            noise_stream_t stream);
+
 /* resid += lowrank(x, w) with the input-side dot of row r given as u_parts partial sums
  * u[r * u_row_stride + q * u_part_stride]: the attention c_proj (u from noise_attention: row stride 8,
  * part stride 1) and the MLP c_proj (u from noise_mlp_fc: row stride 1, part stride members*T).

@@ -34,6 +34,7 @@ SIGNATURES = {
     'noise_qkv': [P, P, P, P, P, P, P, I, I, I, P, P, P, P, L, P, P, P, L, P, P],
     'noise_attention_workspace_size': [I, I, SP],
     'noise_attention': [P, I, I, I, I, I, P, I, P, P, P, P, S, P],
+    'noise_attention_noalloc': [P, I, I, I, I, I, P, I, P, P, P, P],
     'noise_lowrank_resid': [P, P, I, I, P, P, I, L, L, P, I, I, I, P, P],
     'noise_norm_dot': [P, P, P, P, P, I, I, I, P, I, P],
     'noise_dense_bf16': [P, I, I, I, P, I, I, P, P],

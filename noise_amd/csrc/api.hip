@@ -1,4 +1,5 @@
 // extern "C" entry points of libnoise_hip.so (declared in include/noise_hip.h).
+#include <mutex>
 #include <vector>
 
 #include "../../include/noise_hip.h"
@@ -13,6 +14,13 @@
 static_assert(NOISE_CE_MEMBER_MEAN == CE_MEMBER_MEAN && NOISE_CE_NONE == CE_NONE && NOISE_CE_SUM == CE_SUM &&
                   NOISE_CE_MEAN == CE_MEAN,
               "reduction codes");
+
+// The moment partials of noise_attention_noalloc live in this library-owned device array: every GPU the library
+// runs on holds its own copy (16 MiB) until the process ends. In host code `scratch` only names the symbol, not a
+// device address: its address on the current GPU comes from hipGetSymbolAddress, looked up once per device
+// (scratch_address below), and only that address is passed to kernels.
+static_assert(NOISE_ATTENTION_NOALLOC_MAX_PARTIALS % 64 == 0, "scratch size");
+static __device__ __align__(256) float scratch[NOISE_ATTENTION_NOALLOC_MAX_PARTIALS];
 
 namespace {
 
@@ -64,6 +72,26 @@ int copy_pending(const noise_pending_t* src, int npend, Pending* dst) {
 
 bool bad_members(int members, int T, int pair_shift) {
   return members <= 0 || T <= 0 || pair_shift < 0 || pair_shift > 1 || (long)members * T > 0x7fffffffL;
+}
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_dev[MAX_DEVICES];
+
+// The device address of `scratch` on the current device (looked up on this device's first call).
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+  if (dev < 0 || dev >= MAX_DEVICES) return NOISE_ENOTSUP;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
+    if (!p) return NOISE_ENOTSUP;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return NOISE_OK;
 }
 
 }  // namespace
@@ -286,6 +314,23 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
   g.mom = mom ? static_cast<float*>(mom_work) : nullptr;
   g.mom_out = mom;
   return attention_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16,
+                            const float* b_proj, int pair_shift, void* y, float* upart, float* mom,
+                            noise_stream_t stream) {
+  if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
+  void* work = nullptr;
+  size_t bytes = 0;
+  if (mom) {
+    // the size check comes first: a rejected call touches no GPU state
+    noise_attention_workspace_size(members, T, &bytes);
+    if (bytes > sizeof(float) * (size_t)NOISE_ATTENTION_NOALLOC_MAX_PARTIALS) return NOISE_ENOSPC;
+    if (int rc = scratch_address(&work)) return rc;
+  }
+  // the same kernels as noise_attention; every partial is written before it is read, so nothing is cleared
+  return noise_attention(qkv, members, T, window, qk_norm, qk_f16, b_proj, pair_shift, y, upart, mom, work, bytes,
+                         stream);
 }
 
 int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,

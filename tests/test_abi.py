@@ -75,6 +75,9 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_fitness(1, 8, 4, 5, 1, 1, None) == EINVAL        # unknown mode
     assert lib.noise_adam(None, None, None, None, 10, 1e-3, .5, .95, 1e-8, 1.0, None) == EINVAL
     assert lib.noise_attention(1, 1, 100, 50, 0, 1, None, 0, 1, None, None, None, 0, None) == EINVAL  # T % 128
+    # the allocation-free attention refuses moments beyond its fixed array (1024 x 2048 needs 16 Mi partials)
+    assert lib.noise_attention_noalloc(1, 1024, 2048, 2048, 1, 1, None, 0, 1, None, 1, None) == ENOSPC
+    assert lib.noise_attention_noalloc(1, 0, 2048, 2048, 1, 1, None, 0, 1, None, 1, None) == EINVAL
     head = lambda tgt, stride, red, loss, logits: lib.noise_head_ce(  # noqa: E731
         1, 0, None, 1, 4096, 1, 1, 1, 1, tgt, stride, 1, 256, 0, red, loss, logits, None, 0, None, 0, None)
     assert head(1, 0, 0, 1, None) == ENOSPC
