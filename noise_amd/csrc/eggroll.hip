@@ -10,17 +10,16 @@
 
 namespace {
 
-// One workgroup: f_j = L[2j+1] - L[2j]; z-score mode divides by (unbiased std + 1e-8) with no
-// centering (:151-152); rank mode maps f to centred ranks in [-0.5, 0.5] (ties broken by index).
-// weight[d] = sum of f_j over j = d mod pairs in increasing j (:153-154).
-__global__ void __launch_bounds__(1024) fitness_kernel(const float* __restrict__ losses, int nf, int pairs, int mode,
-                                                       float* __restrict__ fit, float* __restrict__ weight) {
+// Z-score fitness in one workgroup (O(n) work): f_j = L[2j+1] - L[2j], divided by (unbiased std + 1e-8) with no
+// centering (:151-152).
+__global__ void __launch_bounds__(1024) zscore_fitness_kernel(const float* __restrict__ losses, int nf,
+                                                              float* __restrict__ fit) {
   __shared__ float red[1024];
   __shared__ float stat;
   const int tid = threadIdx.x;
   for (int j = tid; j < nf; j += 1024) fit[j] = losses[2 * j + 1] - losses[2 * j];
   __syncthreads();
-  if (mode == NOISE_FITNESS_ZSCORE) {
+  {
     float s = 0.f;
     for (int j = tid; j < nf; j += 1024) s += fit[j];
     red[tid] = s;
@@ -46,24 +45,43 @@ __global__ void __launch_bounds__(1024) fitness_kernel(const float* __restrict__
     __syncthreads();
     const float den = stat;
     for (int j = tid; j < nf; j += 1024) fit[j] = fit[j] / den;
-  } else {
-    // centred rank of f_j: #{i : f_i < f_j or (f_i == f_j and i < j)} / (nf - 1) - 0.5
-    for (int j = tid; j < nf; j += 1024) {
-      const float fj = losses[2 * j + 1] - losses[2 * j];
-      int r = 0;
-      for (int i = 0; i < nf; ++i) {
-        const float fi = losses[2 * i + 1] - losses[2 * i];
-        r += (fi < fj) || (fi == fj && i < j);
-      }
-      fit[j] = nf > 1 ? (float)r / (float)(nf - 1) - 0.5f : 0.f;
+  }
+}
+
+// Rank fitness (config-4 option; no reference function), spread over the GPU: thread j owns f_j and counts
+// #{i : f_i < f_j or (f_i == f_j and i < j)} over every f_i, which the workgroup stages through LDS RTILE at a
+// time (every lane reads the same LDS word: a broadcast). fit_j = rank / (n - 1) - 0.5, ties broken by index.
+// n^2 comparisons in n / 256 workgroups: 131,072 pairs (the reference's population) are 512 workgroups of 131,072
+// broadcast-compare steps each.
+constexpr int RTILE = 2048;
+__global__ void __launch_bounds__(256) rank_fitness_kernel(const float* __restrict__ losses, int nf,
+                                                           float* __restrict__ fit) {
+  __shared__ float tile[RTILE];
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const float fj = j < nf ? losses[2 * j + 1] - losses[2 * j] : 0.f;
+  int r = 0;
+  for (int i0 = 0; i0 < nf; i0 += RTILE) {
+    const int n = min(RTILE, nf - i0);
+    __syncthreads();  // the previous tile has been read by every thread
+    for (int i = threadIdx.x; i < n; i += 256) tile[i] = losses[2 * (i0 + i) + 1] - losses[2 * (i0 + i)];
+    __syncthreads();
+    const int lt = j - i0;  // tile entries i < lt have index i0 + i < j
+    for (int i = 0; i < n; ++i) {
+      const float fi = tile[i];
+      r += (fi < fj) || (fi == fj && i < lt);
     }
   }
-  __syncthreads();
-  for (int d = tid; d < pairs; d += 1024) {
-    float s = 0.f;
-    for (int j = d; j < nf; j += pairs) s += fit[j];
-    weight[d] = s;
-  }
+  if (j < nf) fit[j] = nf > 1 ? (float)r / (float)(nf - 1) - 0.5f : 0.f;
+}
+
+// weight[d] = sum of fit_j over j = d mod pairs, in increasing j (:153-154): one thread per direction.
+__global__ void __launch_bounds__(256) fold_fitness_kernel(const float* __restrict__ fit, int nf, int pairs,
+                                                           float* __restrict__ weight) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= pairs) return;
+  float s = 0.f;
+  for (int j = d; j < nf; j += pairs) s += fit[j];
+  weight[d] = s;
 }
 
 // G[o, i] = scale * sum_j (w_j a_j[o]) b_j[i] over ndir directions (a null: a_j[o] = 1, out = 1), for up
@@ -186,7 +204,14 @@ int fitness_launch(const float* losses, int n, int pairs, int mode, float* fit, 
   if (!losses || !fit || !weight || n < 4 || n % 2 || pairs <= 0 ||
       (mode != NOISE_FITNESS_ZSCORE && mode != NOISE_FITNESS_RANK))
     return NOISE_EINVAL;
-  hipLaunchKernelGGL(fitness_kernel, dim3(1), dim3(1024), 0, s, losses, n / 2, pairs, mode, fit, weight);
+  const int nf = n / 2;
+  if (mode == NOISE_FITNESS_ZSCORE)
+    hipLaunchKernelGGL(zscore_fitness_kernel, dim3(1), dim3(1024), 0, s, losses, nf, fit);
+  else
+    hipLaunchKernelGGL(rank_fitness_kernel, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, s, losses, nf, fit);
+  NOISE_CHECK_LAUNCH();
+  hipLaunchKernelGGL(fold_fitness_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, fit, nf, pairs,
+                     weight);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }

@@ -3,6 +3,10 @@
 Perturbation bookkeeping (the fixed N(0, 1) buffer, per-step offsets, the member -> direction and
 member -> sequence layout) follows the reference exactly; the population forward, the fitness, the
 gradient estimate and (with noise_amd.optim.Adam) the optimizer step run in libnoise_hip.so.
+
+Noise rows are gathered per kernel pass (the members one forward pass evaluates), never for the whole
+population at once: a pass of m members holds m / 2 directions x 101,552 floats (624 MB at m = 3072),
+whatever the population size.
 """
 import torch
 
@@ -21,18 +25,33 @@ NOISE = 2 ** 28
 FITNESS = {'zscore': _lib.FITNESS_ZSCORE, 'rank': _lib.FITNESS_RANK}
 
 
+def member_sequences(lo, hi, per_seq, chunk_pairs=CHUNK, device=None):
+    """Sequence index of members lo .. hi - 1. The reference walks a rank's members in chunks of 2 * CHUNK and
+    evaluates each whole chunk on sequence start // per_seq (train/val/eggroll.py:139-145): when per_seq is not a
+    multiple of 2 * CHUNK, a chunk runs on the sequence its first member falls in and some sequences host no
+    member at all."""
+    j = torch.arange(lo, hi, device=device)
+    return (j // (2 * chunk_pairs)) * (2 * chunk_pairs) // per_seq
+
+
 class Eggroll:
     """Perturbation bookkeeping + the population step (train/val/eggroll.py:106-168).
 
-    chunk   -- members per forward pass of the kernels (a multiple of 2; bounded by activation memory);
-    head    -- 'fp32' or 'bf16' head (see noise_amd.population.Population);
-    fitness -- 'zscore' (the reference, :151-152) or 'rank' (centred ranks);
+    chunk       -- members per forward pass of the kernels (a multiple of 2; bounded by activation memory); the
+                   noise rows are gathered per pass;
+    chunk_pairs -- the reference's CHUNK (pairs per batched forward, :34): it fixes which sequence each member
+                   is evaluated on and that every rank hosts whole chunks (:139-145, the check of :187-188);
+    head        -- 'fp32' or 'bf16' head (see noise_amd.population.Population);
+    fitness     -- 'zscore' (the reference, :151-152) or 'rank' (centred ranks);
     sigma, noise_len -- SIGMA and NOISE of the reference by default."""
 
     def __init__(self, model, pairs, rank=0, world=1, chunk=512, head='fp32', fitness='zscore', sigma=SIGMA,
-                 noise_len=NOISE):
+                 noise_len=NOISE, chunk_pairs=CHUNK):
         if chunk % 2:
             raise ValueError('chunk must be even (antithetic pairs stay together)')
+        if chunk_pairs <= 0:
+            raise ValueError('chunk_pairs must be positive')
+        self.chunk_pairs = chunk_pairs
         self.model, self.pairs, self.rank, self.world = model, pairs, rank, world
         self.device = next(model.parameters()).device
         self.params = dict(model.named_parameters())
@@ -77,26 +96,32 @@ class Eggroll:
     def step(self, x, y, optimizer, step):
         """Evaluate this rank's share of the population, gather the losses, rebuild the update
         (train/val/eggroll.py:130-168). Returns the mean population loss."""
-        pairs = self.pairs
+        pairs, cp = self.pairs, self.chunk_pairs
         members = max(2 * pairs, 2 * len(x))
         per_seq, per_rank = members // len(x), members // self.world
-        if per_seq % 2 or per_rank % 2 or members % len(x) or members % self.world:
-            raise ValueError('every sequence and every rank must host whole antithetic pairs')
+        if members % self.world or per_rank % (2 * cp):
+            # the reference's own requirement: every rank evaluates whole chunks of 2 * CHUNK members (:187-188)
+            raise ValueError(f'each rank must evaluate whole chunks of {2 * cp} members (chunk_pairs = {cp})')
         offsets = self.offsets(step)
         losses = torch.empty(per_rank, device=self.device)
         weights = Weights(self.params, self.model.config, self.pop.head)
         lo, hi = self.rank * per_rank, (self.rank + 1) * per_rank
-        # every member of this rank in one call: member j reads sequence j // per_seq, so the population's
-        # chunks run across sequence boundaries (per-member token rows) instead of one pass per sequence
-        directions = torch.arange(lo, hi, 2, device=self.device) % (2 * pairs) // 2
-        noise = self.noise(offsets, directions)
-        sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat(per_rank // 2)
-        if len(x) == 1:
-            seq_x, seq_y = x[0], y[0]
-        else:
-            seq = torch.arange(lo, hi, device=self.device) // per_seq
-            seq_x, seq_y = x[seq], y[seq]
-        losses[:] = self.pop.loss(self.params, noise, sign, seq_x, seq_y, pair_shift=1, weights=weights)
+        sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat(self.pop.chunk // 2)
+        # one kernel pass per `chunk` members, each with only its own directions' noise rows; the members of a
+        # pass may span several of the reference's chunks and so several sequences (per-member token rows)
+        for c0 in range(lo, hi, self.pop.chunk):
+            c1 = min(hi, c0 + self.pop.chunk)
+            directions = torch.arange(c0, c1, 2, device=self.device) % (2 * pairs) // 2
+            noise = self.noise(offsets, directions)
+            seq = member_sequences(c0, c1, per_seq, cp, device=self.device)
+            first, last = (c0 // (2 * cp)) * (2 * cp) // per_seq, ((c1 - 1) // (2 * cp)) * (2 * cp) // per_seq
+            if first == last:
+                seq_x, seq_y = x[first], y[first]
+            else:
+                seq_x, seq_y = x[seq], y[seq]
+            losses[c0 - lo:c1 - lo] = self.pop.loss(self.params, noise, sign[:c1 - c0], seq_x, seq_y, pair_shift=1,
+                                                    weights=weights)
+            del noise
         if self.world > 1:
             gathered = [torch.empty_like(losses) for _ in range(self.world)]
             torch.distributed.all_gather(gathered, losses)

@@ -1,7 +1,8 @@
 """CPU restatement of EGGROLL's perturbation bookkeeping, fitness, update and Adam (TEST INFRASTRUCTURE
 ONLY). Follows `train/val/eggroll.py:106-168` and `:205`, `:208-212`.
 
-Parity pins (tests/test_oracle.py, tests/test_golden.py): offsets / gathered noise against golden streams
+Parity pins (tests/test_oracle.py, tests/test_golden.py): chunk_sequences against the hand-worked layout of
+pairs = 1536 on 8 sequences (chunks of 512 members on sequences 0, 1, 2, 4, 5, 6); offsets / gathered noise against golden streams
 written by importing the reference in the build container; fitness against a hand-computed closed form
 (unbiased std, no centering); rank_fitness (no reference function) against hand-ranked vectors with ties; update against the explicit sum_j w_j a_j b_j^T; Adam against
 torch.optim.AdamW (library routine); a whole reference step (losses, new weights) against the golden
@@ -42,6 +43,18 @@ def member_directions(start, chunk, pairs):
     """Directions of the members start .. start+2*chunk (train/val/eggroll.py:140): members 2j, 2j+1 share
     direction j (mod pairs); member 2j has +sigma and 2j+1 has -sigma (:138)."""
     return torch.arange(start, start + 2 * chunk, 2) % (2 * pairs) // 2
+
+
+def chunk_sequences(members, per_seq, chunk, world=1):
+    """Sequence of every member of the population, as the reference's loop assigns them: each rank walks its
+    members in chunks of 2 * chunk starting at rank * per_rank, and a whole chunk runs on sequence
+    start // per_seq (train/val/eggroll.py:137-145)."""
+    per_rank = members // world
+    seq = torch.full((members,), -1, dtype=torch.int64)
+    for rank in range(world):
+        for start in range(rank * per_rank, (rank + 1) * per_rank, 2 * chunk):
+            seq[start:start + 2 * chunk] = start // per_seq
+    return seq
 
 
 def fitness(losses, pairs):

@@ -639,7 +639,7 @@ def test_noise_gather_rows_equal_buffer_slices():
     from noise_amd.eggroll import Eggroll
     model = make_model(DEV, 0)
     pairs = 6
-    es = Eggroll(model, pairs, chunk=4, noise_len=1 << 20)
+    es = Eggroll(model, pairs, chunk=4, noise_len=1 << 20, chunk_pairs=1)
     offs = es.offsets(3)
     dirs = torch.tensor([0, 5, 2, 2, 4], device=DEV)
     log_case('noise gather rows')
@@ -740,6 +740,79 @@ def test_fitness_update_adam_match_oracle():
     assert torch.allclose(param.cpu(), ref_p, atol=1e-6, rtol=1e-6)
 
 
+def test_fitness_at_the_reference_population():
+    """noise_fitness at the reference's population (131,072 pairs, train/val/eggroll.py:30): rank mode (spread over
+    the GPU) equals the oracle's centred ranks bit for bit, with many ties (losses on a coarse grid); z-score mode
+    matches the oracle's within fp32 summation order."""
+    from oracle import eggroll as oe_
+    pairs = 131072
+    g = torch.Generator().manual_seed(17)
+    losses = 5 + torch.randint(0, 2000, (2 * pairs,), generator=g).float() * 1e-3  # a 1e-3 grid: ties
+    ld = losses.to(DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    fit = torch.empty(pairs, device=DEV)
+    w = torch.empty(pairs, device=DEV)
+    log_case(f'rank fitness pairs={pairs}')
+    _lib.call('noise_fitness', ld.data_ptr(), 2 * pairs, pairs, _lib.FITNESS_RANK, fit.data_ptr(), w.data_ptr(), s)
+    torch.cuda.synchronize()
+    fr, wr = oe_.rank_fitness(losses, pairs)
+    assert torch.equal(fit.cpu(), fr)
+    assert torch.equal(w.cpu(), wr)
+    log_case(f'zscore fitness pairs={pairs}, folded onto {pairs // 4} directions')
+    w4 = torch.empty(pairs // 4, device=DEV)
+    _lib.call('noise_fitness', ld.data_ptr(), 2 * pairs, pairs // 4, _lib.FITNESS_ZSCORE, fit.data_ptr(),
+              w4.data_ptr(), s)
+    torch.cuda.synchronize()
+    fz, wz = oe_.fitness(losses, pairs // 4)
+    assert torch.allclose(fit.cpu(), fz, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(w4.cpu(), wz, rtol=1e-5, atol=1e-5)
+
+
+def test_eggroll_step_eight_sequences_reference_chunk_layout():
+    """Eggroll.step with BATCH = 8 sequences (train/val/eggroll.py:28) and the reference's chunk layout scaled
+    down: 24 pairs, CHUNK = 4 pairs, so per_seq = 6 members and the chunks of 8 members start at 0, 8, ..., 40 and
+    run on sequences 0, 1, 2, 4, 5, 6 (:139-145), as 1536 pairs in chunks of 256 do at full size. Kernel passes of
+    16 members (each gathering only its own directions' noise) cut across those chunks. Every member's loss within
+    1e-4 of the bf16-mode oracle on its chunk's sequence and the reference's noise slices; the gradient estimate
+    from those losses against the oracle's."""
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.optim import Adam
+    pairs, batch, cp, T, step = 24, 8, 4, 128, 5
+    model = make_model(DEV, 0)
+    before = {n: p.detach().cpu().clone() for n, p in model.named_parameters()}
+    shapes = {n: tuple(p.shape) for n, p in before.items()}
+    seqs = [zipf_tokens(T, seed=40 + i) for i in range(batch)]
+    x = torch.stack([s_[0] for s_ in seqs]).to(DEV)
+    y = torch.stack([s_[1] for s_ in seqs]).to(DEV)
+    es = Eggroll(model, pairs, chunk=16, noise_len=1 << 20, sigma=oe.SIGMA, chunk_pairs=cp)
+    opt = Adam(model.parameters(), lr=oe.LR, betas=oe.BETAS, eps=oe.ADAM_EPS)
+    log_case(f'Eggroll.step pairs={pairs} sequences={batch} chunk_pairs={cp} T={T}')
+    es.step(x, y, opt, step)
+    torch.cuda.synchronize()
+    losses = es.last_losses.cpu()
+    members = 2 * pairs
+    seq_of = oe.chunk_sequences(members, members // batch, cp)
+    assert sorted(set(seq_of.tolist())) == [0, 1, 2, 4, 5, 6]
+    buf = es.buffer.cpu()
+    offs = {n: o.cpu() for n, o in es.offsets(step).items()}
+    for start in range(0, members, 2 * cp):
+        sq = int(seq_of[start])
+        dirs = oe.member_directions(start, cp, pairs)
+        g_ = oe.gather_noise(buf, offs, shapes, dirs)
+        noise = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
+                 for n, v in g_.items()}
+        sign = torch.tensor([oe.SIGMA, -oe.SIGMA]).repeat(cp)
+        ref = om.population_loss(before, noise, sign, seqs[sq][0], seqs[sq][1], mode='bf16', head='fp32')
+        got = losses[start:start + 2 * cp]
+        assert (got - ref).abs().max() < 1e-4, (start, sq, got, ref)
+    f, w = oe.fitness(losses, pairs)
+    grads = oe.update(w, oe.gather_noise(buf, offs, shapes, torch.arange(pairs)), len(f))
+    for n, p in model.named_parameters():
+        g_ref = grads[n].reshape(p.shape)
+        assert torch.allclose(p.grad.detach().cpu(), g_ref, atol=1e-6 * float(g_ref.abs().max()) + 1e-12,
+                              rtol=1e-4), n
+
+
 def test_eggroll_step_two_sequences_matches_oracle():
     """One whole `Eggroll.step` on the GPU (train/val/eggroll.py:130-168) with two sequences of 256 tokens and
     4 antithetic pairs (8 members, 4 per sequence, all in one pass through per-member token rows) at the
@@ -755,7 +828,7 @@ def test_eggroll_step_two_sequences_matches_oracle():
     seqs = [zipf_tokens(T, seed=21), zipf_tokens(T, seed=22)]
     x = torch.stack([s_[0] for s_ in seqs]).to(DEV)
     y = torch.stack([s_[1] for s_ in seqs]).to(DEV)
-    es = Eggroll(model, pairs, chunk=8, noise_len=1 << 20, sigma=oe.SIGMA)
+    es = Eggroll(model, pairs, chunk=8, noise_len=1 << 20, sigma=oe.SIGMA, chunk_pairs=2)
     opt = Adam(model.parameters(), lr=oe.LR, betas=oe.BETAS, eps=oe.ADAM_EPS)
     log_case(f'Eggroll.step pairs={pairs} sequences=2 T={T}')
     es.step(x, y, opt, step)

@@ -224,6 +224,20 @@ def test_member_directions():
     assert oe.member_directions(8, 4, 4).tolist() == [0, 1, 2, 3]
 
 
+def test_chunk_sequences_hand_worked_layout():
+    """pairs = 1536 on BATCH = 8 sequences: 3072 members, per_seq = 384, chunks of 2 * 256 = 512 members start at
+    0, 512, ..., 2560 and run on sequences 0 // 384 = 0, 1, 2, 4, 5, 6 (3 and 7 host no member)."""
+    seq = oe.chunk_sequences(3072, 384, 256)
+    want = torch.tensor([0, 1, 2, 4, 5, 6]).repeat_interleave(512)
+    assert torch.equal(seq, want)
+    # when per_seq is a multiple of 2 * CHUNK every sequence hosts exactly per_seq members
+    seq = oe.chunk_sequences(8 * 1024, 1024, 256)
+    assert torch.equal(seq, torch.arange(8).repeat_interleave(1024))
+    # two ranks: each walks its own half from rank * per_rank
+    seq = oe.chunk_sequences(24, 12, 2, world=2)
+    assert seq.tolist() == [0] * 12 + [1] * 12
+
+
 def test_rank_fitness_hand_ranked_with_ties():
     # pair differences: [2, -1, 2, 0.5] -> ranks with ties by index: -1 -> 0, 0.5 -> 1, 2 (j=0) -> 2, 2 (j=2) -> 3
     losses = torch.tensor([1.0, 3.0, 2.0, 1.0, 0.0, 2.0, 4.0, 4.5])
