@@ -254,7 +254,7 @@ def run_attention(args):
         qk = qkv[:, :2 * D].view(P * T, 16, 64)
         qkv[:, :2 * D] = (qk * torch.rsqrt(qk.pow(2).mean(-1, keepdim=True) + 2 ** -23)).view(P * T, 2 * D)
     qkv16 = qkv.to(torch.bfloat16)
-    # config 2's bf16 q, k (qk_f16 = 0 below); v travels as fp16 (here holding the bf16 value exactly)
+    # config 2's bf16 q, k (NOISE_QK_BF16 below); v travels as fp16 (here holding the bf16 value exactly)
     qkv16[:, 2 * D:] = qkv16[:, 2 * D:].half().view(torch.bfloat16)
     qkv = qkv16
     y = torch.empty(P * T, D, device=dev, dtype=torch.bfloat16)

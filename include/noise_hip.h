@@ -145,8 +145,9 @@ int noise_block_entry(const float* x_in, const float* x0, float* x_out, void* h,
  * null, v += gate * (ve_w[idx] + s a_ve[idx] b_ve) (train/val/eggroll.py:85-89), member p reading the
  * token ids idx[p * idx_mstride .. + T] (0: one shared sequence; T: a sequence per member). Output
  * [members*T, 1536] fp16 (q | k | v, head h at columns h*64 of each segment), each rounded once from the
- * fp32 value the reference feeds flex attention (train/val/eggroll.py:58, :90-91): the operand format of
- * noise_attention with qk_f16 = 1. |v| must stay below 65504 (fp16's largest finite value).
+ * fp32 value the reference feeds flex attention (train/val/eggroll.py:58, :90-91), q multiplied by
+ * log2(e) / 8 first (the softmax's score scale in base-2 units): the operand format NOISE_QK_F16_Q_LOG2 of
+ * noise_attention. |v| must stay below 65504 (fp16's largest finite value).
  *   w_qkv    bf16 [1536, 512] = c_q ; c_k ; c_v
  *   rot_cos / rot_sin  bf16 [>= T, 32] (utils/model.py:177-183) */
 /*   u_qkv    [members*T, 4] as noise_block_entry writes it (dots with b_q, b_k, b_v; the member's sign) */
@@ -155,8 +156,13 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
               const void* rot_sin, const float* gate, const float* ve_w, long vocab, const float* ve_a,
               const float* ve_b, const int64_t* idx, long idx_mstride, void* qkv, noise_stream_t stream);
 
-/* Windowed causal attention on q | k | v rows of [members*T, 1536] 16-bit values (8 heads x 64): q and k fp16
- * (qk_f16 != 0, as noise_qkv writes them) or bf16 (qk_f16 == 0, the credit reruns' moved heads); v fp16.
+/* q | k formats of noise_attention. */
+#define NOISE_QK_BF16 0       /* q, k bf16 (the credit reruns' moved heads, train/val/run.py:186-189) */
+#define NOISE_QK_F16 1        /* q, k fp16 */
+#define NOISE_QK_F16_Q_LOG2 2 /* q, k fp16 with q pre-multiplied by log2(e) / 8, as noise_qkv writes them (qk_norm != 0) */
+
+/* Windowed causal attention on q | k | v rows of [members*T, 1536] 16-bit values (8 heads x 64): q and k in
+ * qk_format (NOISE_QK_*); v fp16.
  * y bf16 [members*T, 512]; a query at s
  * sees keys s - window .. s (utils/model.py:14-31). When b_proj is not null, writes the c_proj
  * input-side dot partials upart [members*T, 8]. When mom is not null, writes per-(member, head)
@@ -166,7 +172,7 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
  * as noise_qkv writes them): every score is then bounded by 8.03 and the softmax runs without a running
  * maximum; qk_norm == 0 accepts any q, k. */
 int noise_attention_workspace_size(int members, int T, size_t* bytes);
-int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16, const float* b_proj,
+int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, int qk_format, const float* b_proj,
                     int pair_shift, void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream);
 
@@ -178,7 +184,7 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
  * returns NOISE_ENOSPC beyond it, before any GPU work. It calls no hipMalloc / hipFree. Calls that overlap on one
  * GPU share that array and race: serialise them (one stream, or events). Results equal noise_attention's. */
 #define NOISE_ATTENTION_NOALLOC_MAX_PARTIALS (4 * 1024 * 1024)
-int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16,
+int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_format,
                             const float* b_proj, int pair_shift, void* y, float* upart, float* mom,
                             noise_stream_t stream);
 

@@ -17,6 +17,7 @@ ERRORS = {-1: 'NOISE_EINVAL (rejected argument)', -2: 'NOISE_ENOSPC (workspace t
           -3: 'NOISE_ENOTSUP (shape outside the kernel tiling)'}
 
 FITNESS_ZSCORE, FITNESS_RANK = 0, 1
+QK_BF16, QK_F16, QK_F16_Q_LOG2 = 0, 1, 2
 LAYOUT_ROWS, LAYOUT_TILE16 = 0, 1
 CE_MEMBER_MEAN, CE_NONE, CE_SUM, CE_MEAN = 0, 1, 2, 3
 

@@ -100,8 +100,8 @@ def attention(q, k, v, window, qk_norm=False):
     qkv[:, H * HD:2 * H * HD] = k.reshape(B * T, H * HD).to(torch.bfloat16)
     qkv[:, 2 * H * HD:] = v.reshape(B * T, H * HD).to(torch.bfloat16).half().view(torch.bfloat16)
     y = torch.empty(B * T, H * HD, device=q.device, dtype=torch.bfloat16)
-    _lib.call('noise_attention', qkv.data_ptr(), B, T, int(window), int(bool(qk_norm)), 0, None, 0, y.data_ptr(), None,
-              None, None, 0, _stream())
+    _lib.call('noise_attention', qkv.data_ptr(), B, T, int(window), int(bool(qk_norm)), _lib.QK_BF16, None, 0,
+              y.data_ptr(), None, None, None, 0, _stream())
     return y.view(B, T, H, HD)
 
 
@@ -136,8 +136,8 @@ def rerun(kind, raw, a, sigma, cos, sin, fixed, values, window):
     _lib.call('noise_moved_heads', rawf.data_ptr(), a.data_ptr(), float(sigma), cos.data_ptr(), sin.data_ptr(), n, b,
               T, H, qkv.data_ptr() + 2 * moved_slot, 3 * W, stream)
     y = torch.empty(n * b * T, W, device=a.device, dtype=torch.bfloat16)
-    _lib.call('noise_attention', qkv.data_ptr(), n * b, T, int(window), 1, 0, None, 0, y.data_ptr(), None, None, None,
-              0, stream)
+    _lib.call('noise_attention', qkv.data_ptr(), n * b, T, int(window), 1, _lib.QK_BF16, None, 0, y.data_ptr(), None,
+              None, None, 0, stream)
     return y.view(n, b, T, H, HD)
 
 

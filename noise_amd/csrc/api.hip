@@ -11,6 +11,8 @@
 #include "probes.h"
 #include "rowops.h"
 
+static_assert(NOISE_QK_BF16 == QK_BF16 && NOISE_QK_F16 == QK_F16 && NOISE_QK_F16_Q_LOG2 == QK_F16_Q_LOG2,
+              "q/k format codes");
 static_assert(NOISE_CE_MEMBER_MEAN == CE_MEMBER_MEAN && NOISE_CE_NONE == CE_NONE && NOISE_CE_SUM == CE_SUM &&
                   NOISE_CE_MEAN == CE_MEAN,
               "reduction codes");
@@ -283,7 +285,7 @@ int noise_attention_workspace_size(int members, int T, size_t* bytes) {
   return NOISE_OK;
 }
 
-int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16, const float* b_proj,
+int noise_attention(const void* qkv, int members, int T, int window, int qk_norm, int qk_format, const float* b_proj,
                     int pair_shift, void* y, float* upart, float* mom, void* mom_work, size_t mom_work_bytes,
                     noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
@@ -305,7 +307,7 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
   g.H = NH;
   g.window = window;
   g.qk_norm = qk_norm != 0;
-  g.qk_f16 = qk_f16 != 0;
+  g.qk_format = qk_format;
   g.b_proj = b_proj;
   g.b_ld = DM;
   g.pair_shift = pair_shift;
@@ -316,7 +318,7 @@ int noise_attention(const void* qkv, int members, int T, int window, int qk_norm
   return attention_launch(g, static_cast<hipStream_t>(stream));
 }
 
-int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_f16,
+int noise_attention_noalloc(const void* qkv, int members, int T, int window, int qk_norm, int qk_format,
                             const float* b_proj, int pair_shift, void* y, float* upart, float* mom,
                             noise_stream_t stream) {
   if (bad_members(members, T, pair_shift)) return NOISE_EINVAL;
@@ -329,7 +331,7 @@ int noise_attention_noalloc(const void* qkv, int members, int T, int window, int
     if (int rc = scratch_address(&work)) return rc;
   }
   // the same kernels as noise_attention; every partial is written before it is read, so nothing is cleared
-  return noise_attention(qkv, members, T, window, qk_norm, qk_f16, b_proj, pair_shift, y, upart, mom, work, bytes,
+  return noise_attention(qkv, members, T, window, qk_norm, qk_format, b_proj, pair_shift, y, upart, mom, work, bytes,
                          stream);
 }
 

@@ -2,6 +2,9 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+// Formats of the q and k columns (values of the C ABI's qk_format).
+enum : int { QK_BF16 = 0, QK_F16 = 1, QK_F16_Q_LOG2 = 2 };
+
 struct AttnArgs {
   const __bf16* qkv;  // [members * T, ldq] 16-bit rows; q at column h*64, k at koff + h*64, v (fp16) at voff + h*64
   long ldq;
@@ -10,7 +13,7 @@ struct AttnArgs {
   long ldy;
   int members, T, H, window;
   int qk_norm;        // q and k rows are RMS-normalised (scores bounded by 8.03): no running maximum
-  int qk_f16;         // q and k are fp16 (the population path: written from fp32) rather than bf16
+  int qk_format;      // QK_BF16, QK_F16 or QK_F16_Q_LOG2 (fp16, q pre-multiplied by log2(e) / 8: noise_qkv's output)
   // c_proj input-side dot partials: upart[row * upart_ld + h] = sum_d y[row, h*64+d] bf16(b_proj[dir, h*64+d])
   const float* b_proj;
   long b_ld;

@@ -86,8 +86,11 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
 // normal fp16 numbers and their sums stay far from fp32 overflow), which removes the max reduction, its
 // cross-lane shuffles and the rescaling from the loop. Softmax is shift-invariant, so the result is the same.
 // F16: q and k are fp16 (bf16 otherwise); they travel as raw 16-bit lanes and only the score MFMA reads their type.
-template <bool QKN, bool F16>
+// QL2: q arrives pre-multiplied by log2(e) / 8 (noise_qkv writes it so), so the MFMA returns scores in base-2 units
+// and the softmax takes exp2 of them directly: one VALU multiply per score less (with QKN no max is subtracted).
+template <bool QKN, bool F16, bool QL2>
 __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
+  static_assert(!QL2 || QKN, "pre-scaled q is the population forward's QK-normalised format");
   __shared__ __attribute__((aligned(1024))) bf16 sk[2][BKV * HD];
   __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
   __shared__ float smom[NWAVE][2][HD];
@@ -138,7 +141,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
       dma_x4_s(kv0, voffs[q], reinterpret_cast<const char*>(sv[buf]) + (DH * wave + q) * 1024);
   };
 
-  const float c2 = 0.125f * 1.4426950408889634f;  // scores -> log2 units: 1/sqrt(64) * log2(e)
+  const float c2 = QL2 ? 1.f : 0.125f * 1.4426950408889634f;  // scores -> log2 units: 1/sqrt(64) * log2(e)
   float mref[2] = {-1e30f, -1e30f};  // running max (score units)
   // O^T accumulators, and the row sums of the fp16 probabilities actually used in P V, accumulated on the
   // MFMA pipe (an all-ones A operand: every element of osum[qb] in lane l is the sum for query l % 16)
@@ -220,7 +223,8 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
       for (int hlf = 0; hlf < 2; ++hlf)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          pf[qb][c][4 * hlf + e] = (f16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * c + hlf][e], c2, -mc));
+          pf[qb][c][4 * hlf + e] =
+              (f16)__builtin_amdgcn_exp2f(QL2 ? s[qb][2 * c + hlf][e] : fmaf(s[qb][2 * c + hlf][e], c2, -mc));
   };
 
   issue(j0, 0);
@@ -354,16 +358,20 @@ int attention_launch(const AttnArgs& g, hipStream_t s) {
     return NOISE_EINVAL;
   if (g.upart && (!g.b_proj || g.upart_ld < g.H || g.b_ld < g.H * HD)) return NOISE_EINVAL;
   if (g.mom && !g.mom_out) return NOISE_EINVAL;
+  if (g.qk_format < QK_BF16 || g.qk_format > QK_F16_Q_LOG2 || (g.qk_format == QK_F16_Q_LOG2 && !g.qk_norm))
+    return NOISE_EINVAL;
   const long grid = (long)(g.T / BQ) * g.H * g.members;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
-  if (g.qk_norm && g.qk_f16)
-    hipLaunchKernelGGL((attention_kernel<true, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  if (g.qk_format == QK_F16_Q_LOG2)
+    hipLaunchKernelGGL((attention_kernel<true, true, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  else if (g.qk_norm && g.qk_format == QK_F16)
+    hipLaunchKernelGGL((attention_kernel<true, true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else if (g.qk_norm)
-    hipLaunchKernelGGL((attention_kernel<true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
-  else if (g.qk_f16)
-    hipLaunchKernelGGL((attention_kernel<false, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<true, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  else if (g.qk_format == QK_F16)
+    hipLaunchKernelGGL((attention_kernel<false, true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else
-    hipLaunchKernelGGL((attention_kernel<false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<false, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   NOISE_CHECK_LAUNCH();
   if (g.mom) {
     const long n = (long)g.members * g.H * 2 * HD;

@@ -404,7 +404,8 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
           }
           // QK RMSNorm over the head's 64 dims (eps = 2^-23, utils/model.py:46-47)
           ss = sum_rows4(ss);
-          const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f);
+          // q (segment 0) leaves pre-multiplied by log2(e) / 8, the attention's score scale in base-2 units
+          const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f) * (seg ? 1.f : 0.18033688011112042f);
 #pragma unroll
           for (int e = 0; e < CW; ++e) v[e] *= r;
         } else if (g.gate) {

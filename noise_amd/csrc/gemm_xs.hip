@@ -58,7 +58,8 @@ constexpr int SIGN_OFF = VEC - 8;
 enum : int {
   XS_RELU2 = 0,  // MLP c_fc: bf16(relu(lowrank)^2) + partial dots with b_next
   XS_DENSE = 1,  // c_proj dense product y = bf16(x W^T), row-major
-  XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, fp16 of the fp32 result
+  XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, fp16 of the fp32 result (q times
+                 // log2(e) / 8)
   XS_V = 3,      // c_v without value embedding: lowrank, fp16 of the fp32 result
 };
 // per wave and block: 4 x rows, then the mode's vectors (relu^2: a|b_next|u and the sign; q|k: a, and one
@@ -283,7 +284,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         if (pk < 1) return;
         const int i = st;
         const float tot = ev_ss[i] + ssq[(pk - 1) & 1][16 * i + r][wave ^ 1];
-        const float rn = rsqrtf(tot * (1.f / 64.f) + 1.1920928955078125e-07f);
+        // q (segment 0) leaves pre-multiplied by log2(e) / 8, the attention's score scale in base-2 units
+        const float rn = rsqrtf(tot * (1.f / 64.f) + 1.1920928955078125e-07f) * (seg ? 1.f : 0.18033688011112042f);
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = pack_f16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);

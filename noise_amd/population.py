@@ -221,8 +221,8 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         ap, bp = noise[pre + 'attn.c_proj.weight']
         t0 = tm.mark('attention')
         # q and k come out of noise_qkv RMS-normalised
-        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], int(QK_NORM), 1, _p(bp), ps, _p(buf.y), _p(buf.u_attn),
-                  0, 0, 0, s)
+        _lib.call('noise_attention', _p(buf.qkv), m, T, windows[i], int(QK_NORM), _lib.QK_F16_Q_LOG2, _p(bp), ps,
+                  _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
         _lib.call('noise_dense_bf16', _p(buf.y), _lib.LAYOUT_ROWS, D, D, _p(W.proj[i]), m, T, _p(buf.y_ap), s)

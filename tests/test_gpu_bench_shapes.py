@@ -6,7 +6,7 @@ oracle on sampled members.
   antithetic differences within 1e-4) and at trained-scale weights (within twice the oracle's own rounding
   floor, measured in the test, plus 1e-4).
 - Config 2: windowed causal attention + credit moments on [256 members, 8 heads, 2048 tokens, 64], windows 2048
-  and 1024, with N(0, 1) bf16 q/k (running-maximum softmax) and with RMS-normalised fp16 q/k (the population
+  and 1024, with N(0, 1) bf16 q/k (running-maximum softmax) and with RMS-normalised fp16 q/k, q pre-scaled (the population
   forward's bounded-score softmax).
 - Config 3: RMSNorm with gain -> fp32 head with rank-1 perturbation -> soft cap -> CE on [512, 2048, 512] bf16.
 """
@@ -78,36 +78,40 @@ def test_config4_one_pass_at_trained_scale():
     assert (dg - dr).abs().max() <= 2 * pair_floor + 1e-4, (dg, dr, pair_floor)
 
 
-def _attention_case(P, T, qk_norm, qk_f16, seed):
+def _attention_case(P, T, qk_norm, qk_format, seed):
+    """q, k, v and their q | k | v rows; with qk_format 2 the rows hold q * log2(e) / 8 (noise_qkv's format) and
+    the returned q is that fp16 value back in score units (fp32)."""
     g = torch.Generator(device=DEV).manual_seed(seed)
-    dt = torch.float16 if qk_f16 else torch.bfloat16
+    dt = torch.float16 if qk_format else torch.bfloat16
     q, k, v = (torch.randn(P, T, 8, 64, device=DEV, generator=g) for _ in range(3))
     if qk_norm:
         q, k = (t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 2 ** -23) for t in (q, k))
-    q, k, v = q.to(dt), k.to(dt), v.bfloat16().half()
-    qkv = torch.cat([t.reshape(P * T, 512).view(torch.bfloat16) for t in (q, k, v)], 1)
+    q_in = (q * (math.log2(math.e) / 8)).to(dt) if qk_format == 2 else q.to(dt)
+    q = q_in.float() / (math.log2(math.e) / 8) if qk_format == 2 else q_in
+    k, v = k.to(dt), v.bfloat16().half()
+    qkv = torch.cat([t.reshape(P * T, 512).view(torch.bfloat16) for t in (q_in, k, v)], 1)
     return q, k, v, qkv
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize('qk_norm,qk_f16', [(0, 0), (1, 1)])
-def test_config2_attention_moments_full_size(qk_norm, qk_f16):
+@pytest.mark.parametrize('qk_norm,qk_format', [(0, 0), (1, 2)])
+def test_config2_attention_moments_full_size(qk_norm, qk_format):
     """P = 256, 8 heads, T = 2048, windows 2048 and 1024, one launch each. Sampled members' outputs within 1e-2
     relative of the fp32 oracle on the same 16-bit inputs; every member's moments within 1e-5 of the moments of
     the kernel's own bf16 output (the reduction), the sampled members' within the bf16 output rounding of the
     oracle's moments."""
     P, T = 256, 2048
-    q, k, v, qkv = _attention_case(P, T, qk_norm, qk_f16, seed=5 + qk_norm)
+    q, k, v, qkv = _attention_case(P, T, qk_norm, qk_format, seed=5 + qk_norm)
     s = torch.cuda.current_stream().cuda_stream
     sample = [0, 1, 131, 255]
     bp = torch.randn(P, 512, device=DEV, generator=torch.Generator(device=DEV).manual_seed(9))
     ws = torch.empty(_lib.size_query('noise_attention_workspace_size', P, T), device=DEV, dtype=torch.uint8)
     for window in (2048, 1024):
-        log_case(f'config2 attention P={P} T={T} window={window} qk_norm={qk_norm} qk_f16={qk_f16}')
+        log_case(f'config2 attention P={P} T={T} window={window} qk_norm={qk_norm} qk_format={qk_format}')
         y = torch.empty(P * T, 512, device=DEV, dtype=torch.bfloat16)
         up = torch.empty(P * T, 8, device=DEV)
         mom = torch.empty(P, 8, 2, 64, device=DEV)
-        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, qk_norm, qk_f16, bp.data_ptr(), 0, y.data_ptr(),
+        _lib.call('noise_attention', qkv.data_ptr(), P, T, window, qk_norm, qk_format, bp.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), s)
         torch.cuda.synchronize()
         yv = y.view(P, T, 8, 64)

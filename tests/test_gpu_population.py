@@ -148,15 +148,17 @@ def test_block_entry_and_qkv_match_oracle():
     c, sn = cos[:T], sin[:T]
     qr = om.norm(om.apply_rotary(q.view(m, T, 8, 64), c, sn))
     kr = om.norm(om.apply_rotary(kk_.view(m, T, 8, 64), c, sn))
-    # q, k and v are written as fp16 of the fp32 values (11-bit significand): the error is fp16 rounding plus
-    # the dense product's bf16 rounding, which a different fp32 summation order can move by one bf16 step
+    # q, k and v are written as fp16 of the fp32 values (11-bit significand), q multiplied by log2(e) / 8 first:
+    # the error is fp16 rounding plus the dense product's bf16 rounding, which a different fp32 summation order
+    # can move by one bf16 step
     got = qkv.cpu().view(torch.float16).float().view(m, T, 3, 8, 64)
+    got[:, :, 0] /= math.log2(math.e) / 8
     for k, ref in enumerate((qr, kr, vv)):
         assert rel_err(got[:, :, k], ref) < 2e-3, k
         assert (got[:, :, k] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, k
     # fp16, not bf16: rounding the fp32 result to fp16 changes it by at most 2^-11 relative, and the GPU's
     # values agree with that rounding far better than bf16 rounding would allow
-    assert rel_err(got[:, :, 0], qr.half().float()) < rel_err(om.bf(qr), qr)
+    assert rel_err(got[:, :, 1], kr.half().float()) < rel_err(om.bf(kr), kr)
     # a block without value embedding (gate null): the same q | k, v = lowrank only
     log_case(f'qkv without value embedding m={m} T={T}')
     qkv2 = torch.empty_like(qkv)
@@ -280,23 +282,27 @@ def test_mlp_hidden_tile16_matches_rows():
     assert ((ya.cpu().float() - refa).abs() <= refa.abs() * 2 ** -7 + 1e-6).all()
 
 
-@pytest.mark.parametrize('qk_norm,qk_f16', [(0, 0), (1, 0), (1, 1), (0, 1)])
-def test_attention_matches_oracle_and_moments(qk_norm, qk_f16):
+@pytest.mark.parametrize('qk_norm,qk_format', [(0, 0), (1, 0), (1, 1), (0, 1), (1, 2)])
+def test_attention_matches_oracle_and_moments(qk_norm, qk_format):
     """qk_norm = 0: any q, k (running-maximum softmax); qk_norm = 1: q, k RMS-normalised per head as the
     model's QK-norm leaves them (bounded scores, no running maximum), including rows scaled to the bound.
-    qk_f16 = 1: q and k fp16 (the population forward's format), 0: bf16 (the credit reruns'); v fp16."""
+    qk_format 0: q and k bf16 (the credit reruns'), 1: fp16, 2: fp16 with q pre-multiplied by log2(e) / 8 (the
+    population forward's, as noise_qkv writes it); v fp16."""
     g = torch.Generator().manual_seed(2)
     m, T = 2, 256
-    dt = torch.float16 if qk_f16 else torch.bfloat16
+    dt = torch.float16 if qk_format else torch.bfloat16
     for window in (T, 100):
-        log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm} qk_f16={qk_f16}')
+        log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm} qk_format={qk_format}')
         q, k, v = (torch.randn(m, T, 8, 64, generator=g) for _ in range(3))
         if qk_norm:
             q, k = om.norm(q), om.norm(k)
             # extreme case: every key of the first head equal to its query direction (scores at the bound)
             k[:, :, 0] = q[:, :, 0]
         q, k, v = q.to(dt), k.to(dt), v.half()
-        qkv = torch.cat([q.reshape(m * T, 512).view(torch.bfloat16), k.reshape(m * T, 512).view(torch.bfloat16),
+        q_in = (q.float() * (math.log2(math.e) / 8)).half() if qk_format == 2 else q
+        if qk_format == 2:
+            q = q_in.float() / (math.log2(math.e) / 8)  # the q the kernel sees, back in score units (fp32)
+        qkv = torch.cat([q_in.reshape(m * T, 512).view(torch.bfloat16), k.reshape(m * T, 512).view(torch.bfloat16),
                          v.reshape(m * T, 512).view(torch.bfloat16)], 1).to(DEV)
         y = torch.empty(m * T, 512, device=DEV, dtype=torch.bfloat16)
         bp = torch.randn(m, 512, generator=g)
@@ -304,7 +310,7 @@ def test_attention_matches_oracle_and_moments(qk_norm, qk_f16):
         up = torch.empty(m * T, 8, device=DEV)
         mom = torch.empty(m, 8, 2, 64, device=DEV)
         ws = torch.empty(_lib.size_query('noise_attention_workspace_size', m, T), device=DEV, dtype=torch.uint8)
-        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, qk_f16, bpd.data_ptr(), 0, y.data_ptr(),
+        _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, qk_format, bpd.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
@@ -777,7 +783,7 @@ def test_eggroll_step_eight_sequences_reference_chunk_layout():
     from those losses against the oracle's."""
     from noise_amd.eggroll import Eggroll
     from noise_amd.optim import Adam
-    pairs, batch, cp, T, step = 24, 8, 4, 128, 5
+    pairs, batch, cp, T, step = 24, 8, 4, 256, 5
     model = make_model(DEV, 0)
     before = {n: p.detach().cpu().clone() for n, p in model.named_parameters()}
     shapes = {n: tuple(p.shape) for n, p in before.items()}
