@@ -317,6 +317,21 @@ int noise_gather_rows(const float* buffer, long buffer_len, const noise_gather_p
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
                float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream);
 
+/* noise_adam for every tensor of an optimizer step in one launch (torch.optim.AdamW's per-parameter loop,
+ * train/val/eggroll.py:167): tensors is a host array, read before the call returns; each entry carries its own
+ * step_size and bc2_sqrt (its own step count). Same arithmetic per element as noise_adam. */
+typedef struct noise_adam_tensor {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  long n;
+  float step_size;
+  float bc2_sqrt;
+} noise_adam_tensor_t;
+int noise_adam_batch(const noise_adam_tensor_t* tensors, int n, float beta1, float beta2, float eps,
+                     noise_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,7 @@ SIGNATURES = {
     'noise_head_scores': [P, L, P, P, I, I, I, I, P, P],
     'noise_code_estimate': [P, P, I, I, I, I, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
+    'noise_adam_batch': [P, I, F, F, F, P],
 }
 
 
@@ -76,6 +77,19 @@ def gather_params(items):
     """A host array of noise_gather_param_t from (offsets, a, b, out, in) tuples of device pointers: returns
     (pointer, count, array) -- keep the array alive until the call is enqueued."""
     arr = (GatherParam * len(items))(*[GatherParam(*it) for it in items])
+    return ctypes.cast(arr, P), len(items), arr
+
+
+class AdamTensor(ctypes.Structure):
+    """noise_adam_tensor_t of include/noise_hip.h."""
+    _fields_ = [('param', P), ('grad', P), ('exp_avg', P), ('exp_avg_sq', P), ('n', L), ('step_size', F),
+                ('bc2_sqrt', F)]
+
+
+def adam_tensors(items):
+    """A host array of noise_adam_tensor_t from (param, grad, exp_avg, exp_avg_sq, n, step_size, bc2_sqrt) tuples:
+    returns (pointer, count, array) -- keep the array alive until the call is enqueued."""
+    arr = (AdamTensor * len(items))(*[AdamTensor(*it) for it in items])
     return ctypes.cast(arr, P), len(items), arr
 
 

@@ -502,6 +502,16 @@ int noise_code_estimate(const float* credited, const void* a, int draws, int bat
   return code_estimate_launch(g, static_cast<hipStream_t>(stream));
 }
 
+int noise_adam_batch(const noise_adam_tensor_t* tensors, int n, float beta1, float beta2, float eps,
+                     noise_stream_t stream) {
+  if (n <= 0 || !tensors) return NOISE_EINVAL;
+  std::vector<AdamTensor> t(n);
+  for (int k = 0; k < n; ++k)
+    t[k] = AdamTensor{tensors[k].param, tensors[k].grad, tensors[k].exp_avg, tensors[k].exp_avg_sq, tensors[k].n,
+                      tensors[k].step_size, tensors[k].bc2_sqrt, 0};
+  return adam_batch_launch(t.data(), n, beta1, beta2, eps, static_cast<hipStream_t>(stream));
+}
+
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
                float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream) {
   AdamArgs g{param, grad, exp_avg, exp_avg_sq, n, step_size, beta1, beta2, eps, bc2_sqrt};

@@ -67,3 +67,22 @@ struct AdamArgs {
 int fitness_launch(const float* losses, int n, int pairs, int mode, float* fit, float* weight, hipStream_t s);
 int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int ndir, float scale, hipStream_t s);
 int adam_launch(const AdamArgs& g, hipStream_t s);
+
+// Several tensors' Adam steps in one launch: up to ADAM_MAX tensors per launch, passed by value, with the running
+// total of 256-element blocks (block b belongs to the first tensor whose block_end exceeds b).
+constexpr int ADAM_MAX = 64;
+struct AdamTensor {
+  float* param;
+  const float* grad;
+  float* m;
+  float* v;
+  long n;
+  float step_size, bc2_sqrt;
+  long block_end;
+};
+struct AdamBatchArgs {
+  AdamTensor t[ADAM_MAX];
+  int n;
+  float beta1, beta2, eps;
+};
+int adam_batch_launch(const AdamTensor* tensors, int n, float beta1, float beta2, float eps, hipStream_t s);

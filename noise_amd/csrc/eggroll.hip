@@ -184,18 +184,33 @@ __global__ void __launch_bounds__(256) outer_update_kernel(const OuterBatchArgs 
 
 // torch.optim.AdamW (single-tensor path) with weight_decay = 0:
 // m = lerp(m, g, 1 - b1); v = b2 v + (1 - b2) g^2; p -= (lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps).
+__device__ __forceinline__ void adam_element(float* param, const float* grad, float* mp, float* vp, long i,
+                                             float step_size, float bc2_sqrt, float beta1, float beta2, float eps) {
+  const float gr = grad[i];
+  float m = mp[i], v = vp[i];
+  const float w = 1.f - beta1;
+  m = w < 0.5f ? m + w * (gr - m) : gr - (gr - m) * (1.f - w);
+  v = v * beta2 + (1.f - beta2) * gr * gr;
+  mp[i] = m;
+  vp[i] = v;
+  const float denom = sqrtf(v) / bc2_sqrt + eps;
+  param[i] = param[i] + (-step_size) * (m / denom);
+}
 __global__ void __launch_bounds__(256) adam_kernel(AdamArgs g) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= g.n) return;
-  const float gr = g.grad[i];
-  float m = g.m[i], v = g.v[i];
-  const float w = 1.f - g.beta1;
-  m = w < 0.5f ? m + w * (gr - m) : gr - (gr - m) * (1.f - w);
-  v = v * g.beta2 + (1.f - g.beta2) * gr * gr;
-  g.m[i] = m;
-  g.v[i] = v;
-  const float denom = sqrtf(v) / g.bc2_sqrt + g.eps;
-  g.param[i] = g.param[i] + (-g.step_size) * (m / denom);
+  adam_element(g.param, g.grad, g.m, g.v, i, g.step_size, g.bc2_sqrt, g.beta1, g.beta2, g.eps);
+}
+// Every tensor of an optimizer step in one launch (the same arithmetic per element as adam_kernel): block b
+// serves the tensor whose range of 256-element blocks holds it (a uniform scan over the running totals).
+__global__ void __launch_bounds__(256) adam_batch_kernel(const AdamBatchArgs g) {
+  const long b = blockIdx.x;
+  int k = 0;
+  while (k + 1 < g.n && b >= g.t[k].block_end) ++k;
+  const AdamTensor& t = g.t[k];
+  const long i = (b - (k ? g.t[k - 1].block_end : 0)) * 256 + threadIdx.x;
+  if (i >= t.n) return;
+  adam_element(t.param, t.grad, t.m, t.v, i, t.step_size, t.bc2_sqrt, g.beta1, g.beta2, g.eps);
 }
 
 }  // namespace
@@ -276,6 +291,27 @@ int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int 
       m.tile_end = (int)tiles;
     }
     hipLaunchKernelGGL(outer_update_kernel, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+  }
+  return NOISE_OK;
+}
+
+int adam_batch_launch(const AdamTensor* tensors, int n, float beta1, float beta2, float eps, hipStream_t s) {
+  if (n <= 0 || !tensors) return NOISE_EINVAL;
+  for (int base = 0; base < n; base += ADAM_MAX) {
+    AdamBatchArgs g{};
+    g.n = std::min(ADAM_MAX, n - base);
+    g.beta1 = beta1, g.beta2 = beta2, g.eps = eps;
+    long blocks = 0;
+    for (int k = 0; k < g.n; ++k) {
+      const AdamTensor& t = tensors[base + k];
+      if (!t.param || !t.grad || !t.m || !t.v || t.n <= 0 || !(t.bc2_sqrt > 0.f)) return NOISE_EINVAL;
+      g.t[k] = t;
+      blocks += (t.n + 255) / 256;
+      g.t[k].block_end = blocks;
+    }
+    if (blocks > 0x7fffffffL) return NOISE_ENOTSUP;
+    hipLaunchKernelGGL(adam_batch_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g);
     NOISE_CHECK_LAUNCH();
   }
   return NOISE_OK;

@@ -5,8 +5,16 @@ split (utils/eval.py:24-53).
 `init_weights` stores the token and value embeddings in bfloat16 before the state dict is copied in
 (utils/model.py:171-175, utils/eval.py:24-31): the tables here keep fp32 storage holding the
 bf16-rounded values, which is what the kernels read. `evaluate` runs `GPT.forward(..., 'sum')` over
-batches of rows, with the reference's autocast rounding points (head='bf16' by default; 'fp32' for the
+batches of rows on the population kernels at sigma = 0 (head='bf16' by default; 'fp32' for the
 fp32-accurate head), accumulates in fp64 and returns the mean over all predictions.
+
+Rounding differs from utils/eval.py. The reference runs GPT.forward under CUDA autocast with bf16 embeddings, so
+its whole residual stream is bf16: x0, every residual add and mix, the norms' outputs, rotary's products, the value
+gate and the attention probabilities round to bf16 (rms_norm and the 0-dim lambda products keep their input's
+bf16 dtype). The kernels keep the population path's rounding points instead: an fp32 residual stream and fp32
+norms, bf16 GEMM operands and outputs, fp16 attention operands. On a trained-scale synthetic model the two streams'
+mean losses differ by about 2e-3 (a CPU estimate on 2 x 256 tokens), so a score from `evaluate` is not
+interchangeable with the reference's at that level.
 """
 from pathlib import Path
 

@@ -21,16 +21,19 @@ class Adam(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, closure=None):
+        """One step of every parameter with a gradient: each param group's tensors in one noise_adam_batch launch."""
         loss = closure() if closure is not None else None
         stream = torch.cuda.current_stream().cuda_stream
         for group in self.param_groups:
             b1, b2 = group['betas']
+            items, keep = [], []
             for p in group['params']:
                 if p.grad is None:
                     continue
                 if p.device.type != 'cuda' or p.dtype != torch.float32 or not p.is_contiguous():
                     raise ValueError('Adam (HIP) needs contiguous fp32 CUDA parameters')
                 grad = p.grad.contiguous()
+                keep.append(grad)
                 st = self.state[p]
                 if not st:
                     st['step'] = 0
@@ -38,8 +41,9 @@ class Adam(torch.optim.Optimizer):
                     st['exp_avg_sq'] = torch.zeros_like(p)
                 st['step'] += 1
                 t = st['step']
-                step_size = group['lr'] / (1 - b1 ** t)
-                bc2_sqrt = math.sqrt(1 - b2 ** t)
-                _lib.call('noise_adam', p.data_ptr(), grad.data_ptr(), st['exp_avg'].data_ptr(),
-                          st['exp_avg_sq'].data_ptr(), p.numel(), step_size, b1, b2, group['eps'], bc2_sqrt, stream)
+                items.append((p.data_ptr(), grad.data_ptr(), st['exp_avg'].data_ptr(), st['exp_avg_sq'].data_ptr(),
+                              p.numel(), group['lr'] / (1 - b1 ** t), math.sqrt(1 - b2 ** t)))
+            if items:
+                ptr, count, _arr = _lib.adam_tensors(items)
+                _lib.call('noise_adam_batch', ptr, count, b1, b2, group['eps'], stream)
         return loss

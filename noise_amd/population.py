@@ -351,8 +351,9 @@ def clean_forward(model, idx, targets=None, loss_reduction='mean', head='fp32', 
     member b reading its own sequence (token stride T), with zero signs, so every rank-1 term and every
     lambda perturbation vanishes exactly. With targets, the loss is F.cross_entropy of the capped logits with
     ignore_index = -1 and `loss_reduction` 'mean' / 'sum' (0-dim) or 'none' ([B * T]); without, the capped
-    fp32 logits [B, T, vocab] are returned. The GEMMs keep the autocast rounding points of the population
-    path; head='fp32' keeps the head fp32-accurate, 'bf16' rounds it as autocast does."""
+    fp32 logits [B, T, vocab] are returned. The kernels keep the rounding points of the population path (fp32
+    residual stream and norms, bf16 GEMMs, fp16 attention operands), not the all-bf16 stream GPT.forward has under
+    autocast with bf16 embeddings; head='fp32' keeps the head fp32-accurate, 'bf16' rounds it as autocast does."""
     if loss_reduction not in REDUCTIONS:
         raise ValueError(f"loss_reduction must be one of {tuple(REDUCTIONS)}, got {loss_reduction!r}")
     _need_cuda(idx, torch.int64, 'idx')

@@ -745,6 +745,27 @@ def test_fitness_update_adam_match_oracle():
         torch.cuda.synchronize()
     assert torch.allclose(param.cpu(), ref_p, atol=1e-6, rtol=1e-6)
 
+    log_case('adam_batch')
+    # several tensors (one above the 64-tensor launch limit, ragged sizes) in one call equal noise_adam per tensor
+    sizes = [1000, 1, 257, 4096 * 3 + 5] + [33] * 62
+    ps = [torch.randn(n, generator=g) for n in sizes]
+    gs = [torch.randn(n, generator=g) for n in sizes]
+    single = [(p_.clone().to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)) for p_, n in zip(ps, sizes)]
+    batch = [(p_.clone().to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)) for p_, n in zip(ps, sizes)]
+    gd = [g_.to(DEV) for g_ in gs]
+    for step in range(1, 3):
+        ss, bc = 1e-3 / (1 - 0.5 ** step), math.sqrt(1 - 0.95 ** step)
+        for (pp, mm, vv), g_, n in zip(single, gd, sizes):
+            _lib.call('noise_adam', pp.data_ptr(), g_.data_ptr(), mm.data_ptr(), vv.data_ptr(), n, ss, 0.5, 0.95, 1e-8,
+                      bc, s)
+        ptr, count, _keep = _lib.adam_tensors([(pp.data_ptr(), g_.data_ptr(), mm.data_ptr(), vv.data_ptr(), n, ss, bc)
+                                               for (pp, mm, vv), g_, n in zip(batch, gd, sizes)])
+        _lib.call('noise_adam_batch', ptr, count, 0.5, 0.95, 1e-8, s)
+    torch.cuda.synchronize()
+    for a_, b_ in zip(single, batch):
+        for x_, y_ in zip(a_, b_):
+            assert torch.equal(x_.cpu(), y_.cpu())
+
 
 def test_fitness_at_the_reference_population():
     """noise_fitness at the reference's population (131,072 pairs, train/val/eggroll.py:30): rank mode (spread over
