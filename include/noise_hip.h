@@ -266,6 +266,11 @@ int noise_head_scores(const void* out, long out_ld, const float* baseline, const
                       int heads, float* score, noise_stream_t stream);
 int noise_code_estimate(const float* credited, const void* a, int draws, int batch, int T, int heads, float* est,
                         noise_stream_t stream);
+/* noise_key_filter: the key scores of query_key_errors (train/val/run.py:622-623), (K.to(bf16) @ score.to(bf16)).float()
+ *   per (b, h): out[b, h, t, j] = bf16(sum_s bf16(K[b, h, t, s]) bf16(score[b, h, s, j])) with fp32 accumulation;
+ *   filter bf16 [batch, heads, T, T] (16-byte aligned), score and out fp32 [batch, heads, T, draws]; T % 64 == 0. */
+int noise_key_filter(const void* filter, const float* score, int batch, int heads, int T, int draws, float* out,
+                     noise_stream_t stream);
 
 /* ---------------------------------------------------------------- EGGROLL update */
 

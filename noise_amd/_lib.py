@@ -51,6 +51,7 @@ SIGNATURES = {
     'noise_moved_heads': [P, P, F, P, P, I, I, I, I, P, L, P],
     'noise_head_scores': [P, L, P, P, I, I, I, I, P, P],
     'noise_code_estimate': [P, P, I, I, I, I, P, P],
+    'noise_key_filter': [P, P, I, I, I, I, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
     'noise_adam_batch': [P, I, F, F, F, P],
 }

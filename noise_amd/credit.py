@@ -81,6 +81,22 @@ def code_estimate(credited, a):
     return est
 
 
+def key_scores(filt, score):
+    """The key scores of `query_key_errors` (train/val/run.py:622-623): (K.to(bf16) @ score.to(bf16)).float() per
+    (b, h), K [b, h, t, t] (the matched filter), score [b, h, t, n] -> [b, h, t, n] fp32 holding bf16 values."""
+    _cuda(filt, 'key filter'), _cuda(score, 'score')
+    b, H, T, n = score.shape
+    if tuple(filt.shape) != (b, H, T, T):
+        raise ValueError(f'the key filter must be [{b}, {H}, {T}, {T}] for scores of shape {tuple(score.shape)}')
+    if T % 64:
+        raise ValueError(f'the key filter kernel runs whole 64-token blocks: t = {T} is not a multiple of 64')
+    filt = filt.to(torch.bfloat16).contiguous()
+    score = score.float().contiguous()
+    out = torch.empty(b, H, T, n, device=score.device, dtype=torch.float32)
+    _lib.call('noise_key_filter', filt.data_ptr(), score.data_ptr(), b, H, T, n, out.data_ptr(), _stream())
+    return out
+
+
 def attention(q, k, v, window, qk_norm=False):
     """Causal attention with a left window on [batch, token, head, 64] tensors (utils/model.py:24-31) on the
     attention kernel: q and k bf16, v the bf16-rounded value in fp16 (the kernel's operand format), P in fp16,
@@ -144,12 +160,13 @@ def rerun(kind, raw, a, sigma, cos, sin, fixed, values, window):
 def credit_chunk(kind, raw, a, sigma, cos, sin, fixed, values, window, baseline, target, key_filter=None):
     """One chunk's contribution to the estimate of `query_key_errors` (train/val/run.py:617-625): rerun, score
     each query's output change against its target, for keys carry the scores back through the matched filter
-    key_filter [b, h, t, t] (bf16 product, as the reference), then weight the draws: [b, t, h, 64] fp32."""
+    key_filter [b, h, t, t] (bf16 MFMA product, as the reference's bf16 matmul), then weight the draws:
+    [b, t, h, 64] fp32."""
     n, b, T, H, _ = a.shape
     if kind == 'k' and (key_filter is None or tuple(key_filter.shape) != (b, H, T, T)):
         raise ValueError(f'key credit needs the matched filter key_filter [{b}, {H}, {T}, {T}]')
     out = rerun(kind, raw, a, sigma, cos, sin, fixed, values, window)
     score = head_scores(out, baseline, target)
     if kind == 'k':
-        score = torch.matmul(key_filter.to(torch.bfloat16).contiguous(), score.to(torch.bfloat16).contiguous()).float()
+        score = key_scores(key_filter, score)
     return code_estimate(score, a)

@@ -496,6 +496,13 @@ int noise_head_scores(const void* out, long out_ld, const float* baseline, const
   return head_scores_launch(g, static_cast<hipStream_t>(stream));
 }
 
+int noise_key_filter(const void* filter, const float* score, int batch, int heads, int T, int draws, float* out,
+                     noise_stream_t stream) {
+  if (batch <= 0 || heads <= 0 || (long)batch * heads > 0x7fffffffL) return NOISE_EINVAL;
+  const KeyFilterArgs g{static_cast<const bf16*>(filter), score, out, batch * heads, T, draws};
+  return key_filter_launch(g, static_cast<hipStream_t>(stream));
+}
+
 int noise_code_estimate(const float* credited, const void* a, int draws, int batch, int T, int heads, float* est,
                         noise_stream_t stream) {
   const CodeEstimateArgs g{credited, static_cast<const bf16*>(a), est, draws, T, heads, (long)batch * T * heads * 64};

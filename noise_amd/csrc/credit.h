@@ -32,6 +32,14 @@ struct CodeEstimateArgs {
   long elems;              // B * T * H * 64
 };
 
+struct KeyFilterArgs {
+  const __bf16* filt;      // [BH, T, T] matched filter (attention map transposed and row-normalised)
+  const float* score;      // [BH, T, n] query scores
+  float* out;              // [BH, T, n] bf16-rounded key scores, as fp32
+  int BH, T, n;
+};
+
 int moved_heads_launch(const MovedHeadsArgs& g, hipStream_t s);
+int key_filter_launch(const KeyFilterArgs& g, hipStream_t s);
 int head_scores_launch(const HeadScoresArgs& g, hipStream_t s);
 int code_estimate_launch(const CodeEstimateArgs& g, hipStream_t s);

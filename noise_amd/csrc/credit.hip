@@ -8,6 +8,9 @@
 //   (l, l + 32), so the rotation needs no exchange and the norm is one 32-lane sum.
 // head_scores: score[b, h, t, j] = sum_d (out[j, b, t, h, d] - baseline[b, t, h, d]) hub[b, t, h, d].
 // code_estimate: est[b, t, h, d] = sum_j credited[b, h, t, j] a[j, b, t, h, d], draws in order.
+// key_filter: the key scores of `query_key_errors` (:622-623), (K.to(bf16) @ score.to(bf16)).float(): per (b, h), the
+//   matched filter K [T, T] times the query scores [T, n] on bf16 MFMA with fp32 accumulation, rounded to bf16 as
+//   the reference's bf16 matmul returns it.
 #include "common.h"
 #include "credit.h"
 
@@ -73,6 +76,67 @@ __global__ void __launch_bounds__(256) code_estimate_kernel(const CodeEstimateAr
 }
 
 }  // namespace
+
+namespace {
+// One workgroup = 64 rows t x 64 draws j of one (b, h); 4 waves of 16 rows. The contraction over s walks 32 at a
+// time through LDS: the K tile [64 t][32 s] as loaded (16-byte rows of 8), the scores [32 s][64 j] rounded to bf16
+// and stored transposed [64 j][32 s] so both MFMA operands are 16-byte reads along s. Lane l of wave w ends with
+// rows 16 w + 4 (l / 16) + e, column l % 16 of each 16-column block.
+constexpr int KF_LD = 32 + 8;  // LDS row pitch (bf16): 80 bytes, so 16 rows of a fragment read hit distinct banks
+__global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16 sa[64 * KF_LD];
+  __shared__ __attribute__((aligned(16))) bf16 sb[64 * KF_LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * 64, j0 = blockIdx.y * 64, bh = blockIdx.z;
+  const bf16* filt = g.filt + (long)bh * g.T * g.T;
+  const float* score = g.score + (long)bh * g.T * g.n;
+  f32x4 acc[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
+                  f32x4{0.f, 0.f, 0.f, 0.f}};
+  // loaders: K row tid / 4, s chunk tid % 4 (8 values); scores row s = tid / 8, columns 8 (tid % 8) .. + 7
+  const int ar = tid >> 2, ac = (tid & 3) * 8, bs = tid >> 3, bc = (tid & 7) * 8;
+  for (int s0 = 0; s0 < g.T; s0 += 32) {
+    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(filt + (long)(t0 + ar) * g.T + s0 + ac);
+    float sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = j0 + bc + e;
+      sv[e] = j < g.n ? score[(long)(s0 + bs) * g.n + j] : 0.f;
+    }
+    __syncthreads();  // the previous chunk's fragments have been read
+    *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac]) = kv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sb[(bc + e) * KF_LD + bs] = to_bf16(sv[e]);
+    __syncthreads();
+    const bf16x8 af = *reinterpret_cast<const bf16x8*>(&sa[(16 * wave + (lane & 15)) * KF_LD + 8 * (lane >> 4)]);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sb[(16 * cb + (lane & 15)) * KF_LD + 8 * (lane >> 4)]);
+      acc[cb] = mfma16x16x32(af, bfr, acc[cb]);
+    }
+  }
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int j = j0 + 16 * cb + (lane & 15);
+    if (j >= g.n) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = t0 + 16 * wave + 4 * (lane >> 4) + e;
+      g.out[((long)bh * g.T + t) * g.n + j] = bf16r(acc[cb][e]);
+    }
+  }
+}
+}  // namespace
+
+int key_filter_launch(const KeyFilterArgs& g, hipStream_t s) {
+  if (!g.filt || !g.score || !g.out || g.BH <= 0 || g.T <= 0 || g.n <= 0 || g.T % 64 ||
+      ((uintptr_t)g.filt & 15))
+    return NOISE_EINVAL;
+  if (g.BH > 65535 || (g.n + 63) / 64 > 65535) return NOISE_ENOTSUP;
+  hipLaunchKernelGGL(key_filter_kernel, dim3((unsigned)(g.T / 64), (unsigned)((g.n + 63) / 64), (unsigned)g.BH),
+                     dim3(256), 0, s, g);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
 
 int moved_heads_launch(const MovedHeadsArgs& g, hipStream_t s) {
   if (!g.raw || !g.a || !g.cos || !g.sin || !g.out || g.n <= 0 || g.B <= 0 || g.T <= 0 || g.H <= 0 ||

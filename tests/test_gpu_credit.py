@@ -75,6 +75,22 @@ def test_attention_wrapper_matches_oracle():
     assert (got - ref).abs().max() < 2e-2
 
 
+@pytest.mark.parametrize('n', [24, 70])
+def test_key_scores_match_the_bf16_product(n):
+    """The key scores (train/val/run.py:622-623) on the HIP kernel: bf16(K) @ bf16(score) with fp32 accumulation,
+    rounded to bf16; within one bf16 step of the fp32 product of the same bf16 operands (the summation order may
+    move the rounding), for draw counts that are not multiples of the kernel's 64-column blocks."""
+    g = torch.Generator().manual_seed(27)
+    b, h, T = 2, 8, 256
+    filt = torch.rand(b, h, T, T, generator=g).tril().bfloat16()
+    score = torch.randn(b, h, T, n, generator=g)
+    log_case(f'key_scores b={b} h={h} T={T} n={n}')
+    got = credit.key_scores(filt.to(DEV), score.to(DEV)).cpu()
+    exact = filt.double() @ score.bfloat16().double()
+    assert torch.equal(got, got.bfloat16().float())  # bf16 values
+    assert ((got.double() - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6).all()
+
+
 @pytest.mark.parametrize('kind', ['q', 'k'])
 def test_credit_chunk_matches_oracle(kind):
     """One chunk of query / key credit: GPU estimate within twice the oracle's own bf16-output floor (oracle

@@ -375,3 +375,41 @@ def test_query_credit_with_basis_draws_is_the_gradient():
     baseline = out_of(raw)
     est = oc.credit_chunk('q', raw, a, sigma, cos, sin, kp, v, window, baseline, hub, round_out=False)
     assert torch.allclose(est.double() / sigma, q.grad, rtol=2e-2, atol=2e-3 * float(q.grad.abs().max()))
+
+
+def test_key_credit_through_a_permutation_filter_sums_key_gradients():
+    """Keys (train/val/run.py:617-625): with the 64 draws a_j = e_j at every (b, t, h), every key of the sequence
+    moves by the same draw, so query u's score for draw j is sigma * sum_s d(target_u . out_u) / d raw_k[s, j]. A
+    matched filter that is a cyclic shift of the positions (t <- t + 1, not symmetric) carries query t + 1's score to
+    key position t, so the estimate / sigma at t is sum_s d(target_{t+1} . out_{t+1}) / d raw_k[s]: fp64 autograd one
+    query at a time. A transposed filter product would land on t - 1 instead."""
+    from oracle import credit as oc
+    g = torch.Generator().manual_seed(13)
+    b, t, h, window, sigma = 1, 6, 2, 3, 1e-3
+    raw = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    qp = om.norm(torch.randn(b, t, h, 64, generator=g, dtype=torch.float64))
+    v = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    hub = torch.randn(b, t, h, 64, generator=g, dtype=torch.float64)
+    ang = torch.rand(t, 32, generator=g, dtype=torch.float64) * 6
+    cos, sin = ang.cos(), ang.sin()
+    a = torch.eye(64, dtype=torch.float64)[:, None, None, None, :].expand(64, b, t, h, 64).contiguous()
+
+    def out_of(k_raw):
+        x1, x2 = k_raw[..., :32], k_raw[..., 32:]
+        c, s = cos[None, :, None, :], sin[None, :, None, :]
+        y = torch.cat([x1 * c + x2 * s, -x1 * s + x2 * c], -1)
+        y = y * torch.rsqrt((y * y).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)
+        return om.attention(qp, y, v, window, dtype=torch.float64)
+
+    shift = torch.zeros(t, t, dtype=torch.float64)
+    for u in range(t):
+        shift[u, (u + 1) % t] = 1.0   # key row u reads query (u + 1) % t
+    filt = shift[None, None].expand(b, h, t, t).contiguous()
+    est = oc.credit_chunk('k', raw, a, sigma, cos, sin, qp, v, window, out_of(raw), hub, key_filter=filt,
+                          round_out=False)
+    ref = torch.zeros(b, t, h, 64, dtype=torch.float64)
+    for u in range(t):
+        k = raw.clone().requires_grad_(True)
+        (out_of(k)[:, (u + 1) % t] * hub[:, (u + 1) % t]).sum().backward()
+        ref[:, u] = k.grad.sum(1)
+    assert torch.allclose(est.double() / sigma, ref, rtol=2e-2, atol=2e-3 * float(ref.abs().max()))
