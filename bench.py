@@ -14,7 +14,9 @@ synthetic and resident in HBM before the timed region.
 `--workload mlp` times BASELINE config 1 alone (the rank-1-perturbed relu^2 MLP, P = 256, T = 2048,
 shared x); `--workload attention` config 2 (windowed causal attention + per-head moments, P = 256,
 8 heads, T = 2048); `--workload head` config 3 (RMSNorm with gain + fp32 head + soft-capped CE,
-P = 512, T = 2048). Prints one JSON line.
+P = 512, T = 2048). `--workload stream` measures the HBM ceilings of the row kernels' read / write mixes with the
+library's own streaming kernel; `--workload library` times the vendor GEMM on the fused MLP's shapes (a reference
+point); `--workload copy` calibrates the PMC traffic counters. Prints one JSON line.
 """
 import argparse
 import json
@@ -336,12 +338,76 @@ def run_copy(args):
                          'frac': achieved / 8000.0, 'traffic': nbytes, 'kernel': 'torch copy_'}}
 
 
+def run_stream(args):
+    """HBM ceilings of the row kernels' read / write mixes, measured with the library's own streaming kernel
+    (noise_hbm_stream: one wave per row, 16-byte vector accesses) over the config-4 row count (3072 x 2048 rows):
+    block entry (4 KiB read, 3 KiB written per row), MLP entry (3 / 1), a copy (2 / 2), read-heavy (2 / 1) and
+    write-heavy (1 / 2). value = the block-entry mix."""
+    from noise_amd import _lib
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    rows = 3072 * T
+    src = torch.zeros(rows * 4096 // 4, device=dev, dtype=torch.int32)
+    dst = torch.empty(rows * 3072 // 4, device=dev, dtype=torch.int32)
+    s = torch.cuda.current_stream().cuda_stream
+    mixes = {'block_entry_4r_3w': (4, 3), 'mlp_entry_3r_1w': (3, 1), 'copy_2r_2w': (2, 2), 'read_heavy_2r_1w': (2, 1),
+             'write_heavy_1r_2w': (1, 2)}
+    out = {}
+    for name, (ri, wo) in mixes.items():
+        ms_step, ms_launch = _timed(lambda: _lib.call('noise_hbm_stream', src.data_ptr(), ri, dst.data_ptr(), wo, rows, s),
+                                    args.steps, args.warmup)
+        out[name] = {'ms': ms_launch, 'TB/s': (ri + wo) * 1024 * rows / (ms_launch * 1e-3) / 1e12}
+    be = out['block_entry_4r_3w']
+    return {'metric': 'HBM streaming ceiling of the row-kernel mixes', 'value': be['TB/s'] * 1e3, 'unit': 'GB/s',
+            'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': be['ms'], 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'u32', 'data': 'synthetic',
+            'config': {'workload': 'hbm_stream', 'rows': rows, 'mixes': out},
+            'roofline': {'bound': 'hbm', 'achieved': be['TB/s'] * 1e3, 'peak': 8000.0, 'unit': 'GB/s',
+                         'frac': be['TB/s'] * 1e3 / 8000.0, 'traffic': 7 * 1024 * rows, 'kernel': 'hbm_stream_kernel'}}
+
+
+def run_library(args):
+    """The vendor library (torch.matmul -> hipBLASLt / rocBLAS) on plain bf16 GEMMs of the fused MLP's shapes at
+    config 4 (M = 3072 x 2048 rows: c_fc [M, 512] x [512, 2048], c_proj [M, 2048] x [2048, 512]) and on an 8192^3 GEMM:
+    a reference point for the MLP pair's fraction of the nominal 2.5 PFLOP/s (plain products, no rank-1 terms, relu^2
+    or dot partials). value = the pair's TFLOP/s."""
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    M = 3072 * T
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M, D, device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(F, D, device=dev, generator=g) * D ** -0.5).to(torch.bfloat16)
+    w2 = (torch.randn(D, F, device=dev, generator=g) * F ** -0.5).to(torch.bfloat16)
+    h = torch.empty(M, F, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
+    _, t_fc = _timed(lambda: torch.matmul(x, w1.t(), out=h), args.steps, args.warmup)
+    _, t_proj = _timed(lambda: torch.matmul(h, w2.t(), out=y), args.steps, args.warmup)
+    del x, h, y
+    a = torch.randn(8192, 8192, device=dev, generator=g).to(torch.bfloat16)
+    b = torch.randn(8192, 8192, device=dev, generator=g).to(torch.bfloat16)
+    _, t_sq = _timed(lambda: a @ b, args.steps, args.warmup)
+    f_mlp = 2 * M * D * F
+    tf = lambda f, ms: f / (ms * 1e-3) / 1e12  # noqa: E731
+    pair = tf(2 * f_mlp, t_fc + t_proj)
+    return {'metric': 'vendor bf16 GEMM on the fused-MLP shapes (reference point)', 'value': pair, 'unit': 'TFLOP/s',
+            'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': t_fc + t_proj,
+            'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+            'config': {'workload': 'library_gemm', 'M': M,
+                       'c_fc': {'ms': t_fc, 'TFLOP/s': tf(f_mlp, t_fc), 'frac': tf(f_mlp, t_fc) / PEAK_BF16_TFLOPS},
+                       'c_proj': {'ms': t_proj, 'TFLOP/s': tf(f_mlp, t_proj), 'frac': tf(f_mlp, t_proj) / PEAK_BF16_TFLOPS},
+                       'square_8192': {'ms': t_sq, 'TFLOP/s': tf(2 * 8192 ** 3, t_sq),
+                                       'frac': tf(2 * 8192 ** 3, t_sq) / PEAK_BF16_TFLOPS}},
+            'roofline': {'bound': 'mfma', 'achieved': pair, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
+                         'frac': pair / PEAK_BF16_TFLOPS, 'traffic': None, 'kernel': 'torch.matmul (vendor library)'}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=3)
     ap.add_argument('--warmup', type=int, default=1)
-    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy'), default='step')
+    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy', 'stream', 'library'),
+                    default='step')
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
     ap.add_argument('--qk-norm', action='store_true', help='config 2 with RMS-normalised q, k rows (the model case)')
     ap.add_argument('--pairs', type=int, default=1536)
@@ -360,8 +426,8 @@ def main():
         print('bench.py needs a GPU', file=sys.stderr)
         sys.exit(2)
     result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head,
-              'copy': run_copy}[args.workload](args)
-    if not args.no_cpu_baseline and args.workload != 'copy':
+              'copy': run_copy, 'stream': run_stream, 'library': run_library}[args.workload](args)
+    if not args.no_cpu_baseline and args.workload not in ('copy', 'stream', 'library'):
         result['cpu_baseline'] = cpu_baseline_mlp() if args.workload == 'mlp' else cpu_baseline_step()
     print(json.dumps(result), flush=True)
 

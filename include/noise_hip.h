@@ -322,6 +322,11 @@ int noise_gather_rows(const float* buffer, long buffer_len, const noise_gather_p
 int noise_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, long n, float step_size,
                float beta1, float beta2, float eps, float bc2_sqrt, noise_stream_t stream);
 
+/* HBM streaming calibration (no counterpart in the reference): each of `rows` rows reads in_kib KiB of src and writes
+ * out_kib KiB of dst (1..4 KiB each, 16-byte aligned buffers), one wave per row with the row kernels' 16-byte vector
+ * accesses. It measures the bandwidth ceiling of a row kernel's read / write mix (bench.py --workload stream). */
+int noise_hbm_stream(const void* src, int in_kib, void* dst, int out_kib, long rows, noise_stream_t stream);
+
 /* noise_adam for every tensor of an optimizer step in one launch (torch.optim.AdamW's per-parameter loop,
  * train/val/eggroll.py:167): tensors is a host array, read before the call returns; each entry carries its own
  * step_size and bc2_sqrt (its own step count). Same arithmetic per element as noise_adam. */

@@ -54,6 +54,7 @@ SIGNATURES = {
     'noise_key_filter': [P, P, I, I, I, I, P, P],
     'noise_adam': [P, P, P, P, L, F, F, F, F, F, P],
     'noise_adam_batch': [P, I, F, F, F, P],
+    'noise_hbm_stream': [P, I, P, I, L, P],
 }
 
 

@@ -509,6 +509,10 @@ int noise_code_estimate(const float* credited, const void* a, int draws, int bat
   return code_estimate_launch(g, static_cast<hipStream_t>(stream));
 }
 
+int noise_hbm_stream(const void* src, int in_kib, void* dst, int out_kib, long rows, noise_stream_t stream) {
+  return hbm_stream_launch(src, in_kib, dst, out_kib, rows, static_cast<hipStream_t>(stream));
+}
+
 int noise_adam_batch(const noise_adam_tensor_t* tensors, int n, float beta1, float beta2, float eps,
                      noise_stream_t stream) {
   if (n <= 0 || !tensors) return NOISE_EINVAL;

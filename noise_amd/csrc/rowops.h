@@ -107,6 +107,8 @@ struct CeFinalizeArgs {
 };
 
 int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s);
+// HBM streaming calibration: rows of in_kib KiB read and out_kib KiB written (1..4 each), one wave per row.
+int hbm_stream_launch(const void* src, int in_kib, void* dst, int out_kib, long rows, hipStream_t s);
 int block_entry_launch(const BlockEntryArgs& g, hipStream_t s);
 int norm_dot_launch(const NormDotArgs& g, hipStream_t s);
 int head_norm_launch(const HeadNormArgs& g, hipStream_t s);

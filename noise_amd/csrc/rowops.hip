@@ -358,6 +358,41 @@ __global__ void __launch_bounds__(256) cast_kernel(const float* __restrict__ in,
 
 int grid_rows(long M) { return (int)((M + 3) / 4); }
 
+// HBM calibration: one wave per row reads in_kib KiB of the row's source and writes out_kib KiB, with the row
+// kernels' 16-byte vector loads and stores (ordinary stores for the full lines). The written values are a function
+// of the read ones, so no load is dead.
+template <int IN, int OUT>
+__global__ void __launch_bounds__(256) hbm_stream_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                         long rows) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const u32x4* s = src + row * IN * 64 + lane;
+  u32x4 v[IN];
+#pragma unroll
+  for (int k = 0; k < IN; ++k) v[k] = s[k * 64];  // every load issued before any is used
+  u32x4 acc = v[0];
+#pragma unroll
+  for (int k = 1; k < IN; ++k) acc ^= v[k];
+  u32x4* d = dst + row * OUT * 64 + lane;
+#pragma unroll
+  for (int k = 0; k < OUT; ++k) d[k * 64] = acc + u32x4{(unsigned)k, 0u, 0u, 0u};
+}
+template <int IN>
+int hbm_stream_out(const void* src, void* dst, int out_kib, long rows, hipStream_t s) {
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  const u32x4* a = static_cast<const u32x4*>(src);
+  u32x4* b = static_cast<u32x4*>(dst);
+  switch (out_kib) {
+    case 1: hipLaunchKernelGGL((hbm_stream_kernel<IN, 1>), grid, dim3(256), 0, s, a, b, rows); break;
+    case 2: hipLaunchKernelGGL((hbm_stream_kernel<IN, 2>), grid, dim3(256), 0, s, a, b, rows); break;
+    case 3: hipLaunchKernelGGL((hbm_stream_kernel<IN, 3>), grid, dim3(256), 0, s, a, b, rows); break;
+    default: hipLaunchKernelGGL((hbm_stream_kernel<IN, 4>), grid, dim3(256), 0, s, a, b, rows); break;
+  }
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
 bool bad_pending(const Pending* pend, int npend) {
   if (npend < 0 || npend > MAX_PENDING) return true;
   for (int k = 0; k < npend; ++k) {
@@ -370,6 +405,18 @@ bool bad_pending(const Pending* pend, int npend) {
 }
 
 }  // namespace
+
+int hbm_stream_launch(const void* src, int in_kib, void* dst, int out_kib, long rows, hipStream_t s) {
+  if (!src || !dst || in_kib < 1 || in_kib > 4 || out_kib < 1 || out_kib > 4 || rows <= 0 || (rows + 3) / 4 > 0x7fffffffL ||
+      (((uintptr_t)src | (uintptr_t)dst) & 15))
+    return NOISE_EINVAL;
+  switch (in_kib) {
+    case 1: return hbm_stream_out<1>(src, dst, out_kib, rows, s);
+    case 2: return hbm_stream_out<2>(src, dst, out_kib, rows, s);
+    case 3: return hbm_stream_out<3>(src, dst, out_kib, rows, s);
+    default: return hbm_stream_out<4>(src, dst, out_kib, rows, s);
+  }
+}
 
 int embed_norm_launch(const EmbedNormArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.T <= 0 || !g.w || !g.a || !g.b || !g.sign || !g.idx || !g.x0 || g.V <= 0) return NOISE_EINVAL;
