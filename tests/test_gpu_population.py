@@ -840,6 +840,60 @@ def test_eggroll_step_eight_sequences_reference_chunk_layout():
                               rtol=1e-4), n
 
 
+@pytest.mark.timeout(900)
+def test_eggroll_step_at_the_reference_population():
+    """One whole Eggroll.step at the reference's own population (train/val/eggroll.py:28-34): PAIRS = 131,072 antithetic
+    pairs (262,144 members), BATCH = 8 sequences, CHUNK = 256, the full 2^28 noise buffer, at T = 128 tokens (the
+    population machinery is what this exercises; T only scales the forward). 16 kernel passes of 16,384 members, each
+    gathering its own noise rows; the update walks the directions 256 at a time. Checks: every loss finite and near
+    ln 4096 at the reference init; sampled members of several chunks and sequences within 1e-4 of the oracle on their
+    chunk's sequence; the z-score fitness of all 131,072 pairs and the gradients of the mixing scalars and of one
+    ve_gate weight against the oracle's composition from the same losses and noise."""
+    from noise_amd.eggroll import Eggroll, PAIRS, BATCH, CHUNK
+    from noise_amd.optim import Adam
+    pairs, T, step = PAIRS, 128, 7
+    model = make_model(DEV, 0)
+    before = {n: p.detach().cpu().clone() for n, p in model.named_parameters()}
+    shapes = {n: tuple(p.shape) for n, p in before.items()}
+    seqs = [zipf_tokens(T, seed=60 + i) for i in range(BATCH)]
+    x = torch.stack([s_[0] for s_ in seqs]).to(DEV)
+    y = torch.stack([s_[1] for s_ in seqs]).to(DEV)
+    es = Eggroll(model, pairs, chunk=16384, sigma=oe.SIGMA)
+    opt = Adam(model.parameters(), lr=oe.LR, betas=oe.BETAS, eps=oe.ADAM_EPS)
+    log_case(f'Eggroll.step pairs={pairs} sequences={BATCH} T={T} (reference population)')
+    es.step(x, y, opt, step)
+    torch.cuda.synchronize()
+    losses = es.last_losses.cpu()
+    members = 2 * pairs
+    assert losses.shape == (members,) and torch.isfinite(losses).all()
+    # the init's head keeps every member near ln 4096 (262,144 draws reach ~0.08 away at sigma = 2e-3)
+    assert (losses - math.log(4096)).abs().max() < 0.25
+    seq_of = oe.chunk_sequences(members, members // BATCH, CHUNK)
+    offs = {n: o.cpu() for n, o in es.offsets(step).items()}
+    log_case('reference population: oracle on sampled members')
+    buf = es.buffer.cpu()
+    for m in (0, 1, 2 * CHUNK + 6, members // 2 + 3, members - 2):
+        m0 = m - m % 2
+        dirs = oe.member_directions(m0, 1, pairs)
+        g_ = oe.gather_noise(buf, offs, shapes, dirs)
+        noise = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
+                 for n, v in g_.items()}
+        sq = int(seq_of[m0])
+        ref = om.population_loss(before, noise, torch.tensor([oe.SIGMA, -oe.SIGMA]), seqs[sq][0], seqs[sq][1],
+                                 mode='bf16', head='fp32')
+        assert (losses[m0:m0 + 2] - ref).abs().max() < 1e-4, (m0, sq, losses[m0:m0 + 2], ref)
+    f, w = oe.fitness(losses, pairs)
+    small = {n: s_ for n, s_ in shapes.items() if n in ('resid_lambdas', 'x0_lambdas', 'transformer.h.1.attn.ve_gate.weight')}
+    grads = oe.update(w, oe.gather_noise(buf, {n: offs[n] for n in small}, small, torch.arange(pairs)), len(f))
+    params = dict(model.named_parameters())
+    for n in small:
+        g_ref = grads[n].reshape(params[n].shape)
+        g_got = params[n].grad.detach().cpu()
+        assert torch.allclose(g_got, g_ref, atol=1e-4 * float(g_ref.abs().max()) + 1e-9, rtol=1e-3), n
+    del es
+    torch.cuda.empty_cache()
+
+
 def test_eggroll_step_two_sequences_matches_oracle():
     """One whole `Eggroll.step` on the GPU (train/val/eggroll.py:130-168) with two sequences of 256 tokens and
     4 antithetic pairs (8 members, 4 per sequence, all in one pass through per-member token rows) at the
