@@ -95,12 +95,13 @@ __device__ __forceinline__ unsigned pack_f16(float a, float b) {
 }
 
 // q|k mode column map: slice s covers segment s / 2 (q, k), heads 4 (s % 2) .. + 3; wave w takes head
-// 4 (s % 2) + w / 2 and, of its 64 dims, half h = w % 2: local columns 0-15 are dims 16 h .. 16 h + 15 and
-// 16-31 are dims 32 + 16 h .. 47 + 16 h, so every rotary pair (d, d + 32) lies in one lane pair l, l ^ 32
-// and the head's RMSNorm needs only the partner wave w ^ 1.
+// 4 (s % 2) + w / 2 and, of its 64 dims, the 16 rotary pairs (d, d + 32) with d in 16 h .. 16 h + 15, h = w % 2.
+// Local column 8 g + 4 j + e (lane group g, MFMA column block j, element e) is dim 32 j + 16 h + 4 g + e: a lane's
+// 8 columns are dims d0 .. d0 + 3 and their partners d0 + 32 .. d0 + 35 (d0 = 16 h + 4 g), so the rotation stays
+// inside the lane, and the head's RMSNorm needs only the partner wave w ^ 1.
 __device__ __forceinline__ int qk_col(int nslice, int wave, int lc) {
   const int seg = nslice >> 1, head = 4 * (nslice & 1) + (wave >> 1), half = wave & 1;
-  const int dim = lc < 16 ? 16 * half + lc : 32 + 16 * half + (lc - 16);
+  const int dim = 32 * ((lc >> 2) & 1) + 16 * half + 4 * (lc >> 3) + (lc & 3);
   return seg * 512 + head * 64 + dim;
 }
 
@@ -179,13 +180,12 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       return;
     }
     if constexpr (QK) {
-      // a over the wave's columns (lanes 0-7: two 64-byte runs of dims); then wave 0-3: cos / sin rows
-      // (1 KiB each), wave 4: the block's u_qkv rows, waves 5-7: the same rows into a padding area (every
-      // wave issues DMA_PER_BLOCK loads per block)
-      // lanes 0-3: dims qk_col(.., 0 .. 15), lanes 4-7: qk_col(.., 16 .. 31) = the first run + 32
+      // a over the wave's columns (lanes 0-7: local columns 4 L .. 4 L + 3 = dims 16 h + 4 (L / 2) + 32 (L % 2)
+      // .. + 3); then wave 0-3: cos / sin rows (1 KiB each), wave 4: the block's u_qkv rows, waves 5-7: the same rows
+      // into a padding area (every wave issues DMA_PER_BLOCK loads per block)
       const int seg = nslice >> 1;
       if (lane < 8)
-        dma_x4_s(g.ra[seg] + (long)dir * g.ra_ld + qk_col(nslice, wave, 0) - seg * 512, 128u * (lane >> 2) + 16u * (lane & 3),
+        dma_x4_s(g.ra[seg] + (long)dir * g.ra_ld + qk_col(nslice, wave, 0) - seg * 512, 128u * (lane & 1) + 16u * (lane >> 1),
                  &qv[buf].av[wave][0]);
       if (wave < 4) {
         const bf16* tab = (wave >> 1) ? g.rot_sin : g.rot_cos;
@@ -226,17 +226,24 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   float ev_a[8], ev_u[2], ev_dot[2];
   unsigned ev_bp[4], ev_h[2][4];
   float ev_v[2][8], ev_ss[2];   // q|k: rotated values and the wave's sums of squares per row half
-  bf16x8 ev_cs[2][2];           // q|k: cos / sin of the lane's 8 dims for rows r, r + 16
+  bf16x4 ev_cs[2][2];           // q|k: cos / sin of the lane's 4 rotary pairs for rows r, r + 16
   const int qk_ocol = QK ? qk_col(nslice, wave, 8 * grp) : 0;  // the lane's first output column
   // Stores of a row half go to a uniform base (the half's first row, the wave's first column) plus a per-lane
   // byte offset fixed for the kernel: row lane % 16, the lane's 8 columns.
   const int col0 = QK ? qk_col(nslice, wave, 0) : fw;
   const unsigned st_off = 2u * (unsigned)((lane & 15) * g.ldo + (QK ? qk_ocol - col0 : 8 * grp));
+
   // TILE16 (c_fc h): the half's 1 KiB tile of the wave's 32 columns, 16-byte unit 4 r + (grp ^ ((r / 2) % 4))
   const unsigned tile_off = 16u * (unsigned)(4 * (lane & 15) + (grp ^ (((lane & 15) >> 1) & 3)));
   auto half_base = [&](int blk, int i) { return g.out_bf16 + ((long)blk * R + 16 * i) * g.ldo + col0; };
   auto store_half = [&](int blk, int i, u32x4 v) {
     *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(half_base(blk, i)) + st_off) = v;
+  };
+  // q|k: the lane's dims d0 .. d0 + 3 at st_off, their partners d0 + 32 .. at st_off + 64 bytes
+  auto store_half_qk = [&](int blk, int i, u32x4 v) {
+    char* b = reinterpret_cast<char*>(half_base(blk, i)) + st_off;
+    *reinterpret_cast<uint2*>(b) = make_uint2(v[0], v[1]);
+    *reinterpret_cast<uint2*>(b + 64) = make_uint2(v[2], v[3]);
   };
 
   // Stage st (0 .. 15) of the epilogue of block pk (ring slot pbuf) from acc:
@@ -289,7 +296,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = pack_f16(ev_v[i][2 * e] * rn, ev_v[i][2 * e + 1] * rn);
-        store_half(blk_of(pk - 1), i, o);
+        store_half_qk(blk_of(pk - 1), i, o);
         return;
       }
       if (pk < 0 || st > 12) return;
@@ -302,12 +309,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
         ev_u[0] = u0.w * bf16r(seg ? u0.y : u0.x);
         ev_u[1] = u1.w * bf16r(seg ? u1.y : u1.x);
-        const int dd = (qk_ocol & 63) & 31;  // the lane's first dim modulo 32
+        const int dd = (qk_ocol & 63) & 31;  // the lane's first dim d0 (< 32): 4 dims, half of a 16-byte chunk
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int c = 0; c < 2; ++c)
-            ev_cs[i][c] = *reinterpret_cast<const bf16x8*>(&q.cs[c][16 * i + r][8 * ((dd >> 3) ^ ((r >> 2) & 3))]);
+            ev_cs[i][c] = *reinterpret_cast<const bf16x4*>(
+                &q.cs[c][16 * i + r][8 * ((dd >> 3) ^ ((r >> 2) & 3)) + (dd & 7)]);
         return;
       }
       const int i = st < 8 ? 0 : 1, sub = st - (i ? 8 : 3);
@@ -316,16 +324,16 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         ev_v[i][c] = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
         ev_v[i][c + 1] = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
       } else {
-        // dims d < 32 (lane groups 0, 1): x_d cos + x_{d+32} sin; d >= 32: x_d cos - x_{d-32} sin
-        const bool first = grp < 2;
+        // pair (d, d + 32) = (x1, x2) of elements e, e + 4: [x1 cos + x2 sin, -x1 sin + x2 cos]
         float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const f32pair hv = halves32(ev_v[i][e]);  // dims d (lane groups 0, 1) and d + 32 (groups 2, 3)
+        for (int e = 0; e < 4; ++e) {
+          const float x1 = ev_v[i][e], x2 = ev_v[i][e + 4];
           const float cv = (float)ev_cs[i][0][e], sv = (float)ev_cs[i][1][e];
-          const float y = first ? hv.lo * cv + hv.hi * sv : hv.hi * cv - hv.lo * sv;
-          ev_v[i][e] = y;
-          ss += y * y;
+          const float y1 = x1 * cv + x2 * sv, y2 = x2 * cv - x1 * sv;
+          ev_v[i][e] = y1;
+          ev_v[i][e + 4] = y2;
+          ss += y1 * y1 + y2 * y2;
         }
         ss = sum_rows4(ss);
         ev_ss[i] = ss;
