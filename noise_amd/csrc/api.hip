@@ -262,8 +262,8 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
   g.idx = idx;
   g.tok_mstride = idx_mstride;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // q | k on the weight-resident kernel (rotary and the head RMSNorm in its epilogue), v (with the value
-  // embedding) on the tile GEMM; both read the same h
+  // q | k and v on the weight-resident kernel (rotary and the head RMSNorm, or the gated value embedding, in
+  // its epilogue); both launches read the same h
   LowrankGemmArgs gqk = g;
   gqk.N = 2 * DM;
   if (xs_qk_supported(gqk)) {
@@ -274,6 +274,7 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
     gv.W = g.W + (long)2 * DM * DM;
     gv.out_bf16 = g.out_bf16 + 2 * DM;
     if (xs_v_supported(gv)) return xs_v_launch(gv, s);
+    if (xs_ve_supported(gv)) return xs_ve_launch(gv, s);
     return lowrank_gemm_launch(EPI_QKV, gv, s);
   }
   return lowrank_gemm_launch(EPI_QKV, g, s);

@@ -104,3 +104,6 @@ int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream);
 // ... and for c_v without value embedding (N = 512, W and out already offset to the v segment; a = ra[2]).
 bool xs_v_supported(const LowrankGemmArgs& g);
 int xs_v_launch(const LowrankGemmArgs& g, hipStream_t stream);
+// ... and for c_v with the gated value embedding (gate, ve_w, ve_a, ve_b, idx set; T a multiple of 32).
+bool xs_ve_supported(const LowrankGemmArgs& g);
+int xs_ve_launch(const LowrankGemmArgs& g, hipStream_t stream);

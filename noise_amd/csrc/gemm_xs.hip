@@ -61,11 +61,29 @@ enum : int {
   XS_QK = 2,     // c_q | c_k: lowrank + rotary + RMSNorm over each 64-dim head, fp16 of the fp32 result (q times
                  // log2(e) / 8)
   XS_V = 3,      // c_v without value embedding: lowrank, fp16 of the fp32 result
+  XS_VE = 4,     // c_v with the gated value embedding: lowrank + gate (ve_w[tok] + s ve_a[tok] ve_b), fp16
 };
+// LDS ring depth per mode: the value-embedding mode gives one ring slot to its gathered embedding rows
+template <int MODE>
+constexpr int RING = MODE == XS_VE ? 3 : NBUF;
 // per wave and block: 4 x rows, then the mode's vectors (relu^2: a|b_next|u and the sign; q|k: a, and one
 // of cos / sin / u|sign / padding)
 template <int MODE>
 constexpr int DMA_PER_BLOCK = MODE == XS_DENSE ? 4 : 6;
+constexpr int VE_DMA = 6;  // value embedding: loads of one block's gather per wave (4 rows of W, b, a[tok])
+
+// value-embedding mode: the per-block vectors of one ring slot, and one wave's gathered embedding block.
+struct VeVec {
+  float av[NW][32];   // a_v over each wave's 32 columns
+  float uq[R][4];     // u_qkv rows: bf16 dots with b_q, b_k, b_v and the member's sign
+  float gate[R][8];   // the block's gate rows, 2 sigmoid(ve_gate(h[:32])) per head
+  int64_t tok[R];     // token ids of the NEXT block's rows (they address that block's embedding gather)
+};
+struct VeRows {
+  float w[R][32];     // ve_w[tok] over the wave's 32 columns, one row per block row
+  float b[32];        // ve_b[dir] over the wave's 32 columns
+  float a[R];         // ve_a[dir, tok] per block row
+};
 
 // q|k mode: the per-block vectors shared by the workgroup's 8 waves (5.5 KiB per ring slot).
 struct QkVec {
@@ -108,14 +126,18 @@ __device__ __forceinline__ int qk_col(int nslice, int wave, int lc) {
 // DENSE: the c_proj dense product y = bf16(x W^T) only (no rank-1 term, no vectors, no partial dots), row-major.
 template <int MODE>
 __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
-  constexpr bool DENSE = MODE == XS_DENSE, QK = MODE == XS_QK, VV = MODE == XS_V;
+  constexpr bool DENSE = MODE == XS_DENSE, QK = MODE == XS_QK, VV = MODE == XS_V, VE = MODE == XS_VE;
+  constexpr int NB = RING<MODE>;
   constexpr int FIRST_STORE = QK ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) char smem[NBUF * XBYTES];
-  __shared__ __attribute__((aligned(16))) char svec[NBUF][NW][VEC];
+  __shared__ __attribute__((aligned(16))) char smem[NB * XBYTES];
+  __shared__ __attribute__((aligned(16))) char svec[NB][NW][VEC];
   __shared__ __attribute__((aligned(16))) float red[2][R][NW];
-  __shared__ __attribute__((aligned(16))) QkVec qv[NBUF];
+  __shared__ __attribute__((aligned(16))) QkVec qv[NB];
   __shared__ __attribute__((aligned(16))) float ssq[2][R][NW];  // q|k: per-row partial sums of squares
   __shared__ __attribute__((aligned(16))) float qpad[R][4];     // q|k: landing area of the padding loads
+  __shared__ __attribute__((aligned(16))) VeVec vv[NB];         // value embedding: per-block vectors
+  __shared__ __attribute__((aligned(16))) VeRows ver[NW];       // value embedding: each wave's gathered rows
+  __shared__ float vpad[NW];                                    // value embedding: landing area of padding loads
 
   // the wave index is uniform: keeping it in an SGPR keeps every per-wave address on the scalar unit
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), grp = lane >> 4;
@@ -149,7 +171,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 
   auto blk_of = [&](int k) { return lo + stream + k * streams; };
 
-  // ---- loads of block k into ring slot k % NBUF. Wave w fills x rows 4 w + q: lane L loads k 8 L .. 8 L + 7.
+  // ---- loads of block k into ring slot k % NB. Wave w fills x rows 4 w + q: lane L loads k 8 L .. 8 L + 7.
   // Lanes 0-7 load a_p, 8-15 b_next over the wave's 32 columns, 16-23 the block's 32 input-side dots; lane 0
   // the member's sign.
   // Blocks are issued in order k = 0, 1, 2, ...: the next one's first row, member and token advance by
@@ -159,7 +181,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   const int step_rows = streams * R;
   const unsigned lane16 = 16u * lane;  // the lane's byte offset in a 1 KiB row load
   auto issue = [&](int k) {
-    const int buf = k % NBUF, row0 = nx_row, p = nx_p, t0 = nx_t0, dir = p >> g.pair_shift;
+    const int buf = k % NB, row0 = nx_row, p = nx_p, t0 = nx_t0, dir = p >> g.pair_shift;
     nx_row += step_rows;
     nx_t0 += step_rows;
     while (nx_t0 >= g.T) {
@@ -177,6 +199,22 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       // into a padding area (every wave issues DMA_PER_BLOCK loads per block)
       if (lane < 8) dma_x4_s(g.ra[2] + (long)dir * g.ra_ld + fw, lane16, &qv[buf].av[wave][0]);
       if (lane < R) dma_x4_s(urows, lane16, wave == 4 ? &qv[buf].uq[0][0] : &qpad[0][0]);
+      return;
+    }
+    if constexpr (VE) {
+      // a over the wave's 32 columns (lanes 0-7); one more load per wave: wave 4 the block's u_qkv rows, wave 5
+      // its gate rows, wave 6 the token ids of the next block (when there is one), the others 4 padding bytes
+      // (every wave issues DMA_PER_BLOCK loads per block)
+      if (lane < 8) dma_x4_s(g.ra[2] + (long)dir * g.ra_ld + fw, lane16, &vv[buf].av[wave][0]);
+      if (wave == 4) {
+        if (lane < R) dma_x4_s(urows, lane16, &vv[buf].uq[0][0]);
+      } else if (wave == 5) {
+        dma_x4_s(g.gate + (long)row0 * 8, lane16, &vv[buf].gate[0][0]);
+      } else if (wave == 6 && k + 1 < nb) {
+        if (lane < R / 2) dma_x4_s(g.idx + (long)nx_p * g.tok_mstride + nx_t0, lane16, &vv[buf].tok[0]);
+      } else if (lane == 0) {
+        dma_x1(g.u, &vpad[wave]);
+      }
       return;
     }
     if constexpr (QK) {
@@ -226,6 +264,51 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   float ev_a[8], ev_u[2], ev_dot[2];
   unsigned ev_bp[4], ev_h[2][4];
   float ev_v[2][8], ev_ss[2];   // q|k: rotated values and the wave's sums of squares per row half
+  // value embedding: block k's term gate (W[idx] + s a[idx] b) per lane, read in iteration k (after its gather
+  // landed) and added by block k's epilogue in iteration k + 1: ve_x = W[idx] + s a[idx] b over the lane's 8
+  // columns of rows r and r + 16, ve_g = the rows' gates for the wave's head
+  float ve_x[2][8], ve_g[2];
+
+  // The gather of block k's embedding rows into this wave's VeRows (VE_DMA loads): tk[q] is the token of block
+  // row 8 q + lane / 8 (lane % 8 loads columns 4 (lane % 8) .. + 3 of the wave's 32), tka the token of row
+  // lane % 32 (lanes 0-31 load a[dir, tok]).
+  auto ve_issue = [&](int k, const int64_t(&tk)[4], int64_t tka) {
+    const int p = blk_of(k) * R / g.T, dir = p >> g.pair_shift;
+    VeRows& vr = ver[wave];
+    const int c4 = fw + 4 * (lane & 7);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_x4(g.ve_w + tk[q] * 512 + c4, &vr.w[8 * q][0]);
+    if (lane < 8) dma_x4_s(g.ve_b + (long)dir * 512 + fw, lane16, &vr.b[0]);
+    if (lane < R) dma_x1(g.ve_a + (long)dir * g.ve_v + tka, &vr.a[0]);
+  };
+  // ... of block k + 1, from the token ids that arrived with block k
+  auto ve_next = [&](int k) {
+    const int64_t* tt = vv[k % NB].tok;
+    int64_t tk[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tk[q] = tt[8 * q + (lane >> 3)];
+    ve_issue(k + 1, tk, tt[lane & 31]);
+  };
+  // block k's term from its landed gather and its gate / sign rows (EPI_QKV's arithmetic, per element)
+  auto ve_read = [&](int k) {
+    const VeVec& q = vv[k % NB];
+    const VeRows& vr = ver[wave];
+    const int r = lane & 15, head = fw >> 6;
+    const float4 b0 = *reinterpret_cast<const float4*>(&vr.b[8 * grp]);
+    const float4 b1 = *reinterpret_cast<const float4*>(&vr.b[8 * grp + 4]);
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = 16 * i + r;
+      const float sa = q.uq[row][3] * vr.a[row];
+      ve_g[i] = q.gate[row][head];
+      const float4 w0 = *reinterpret_cast<const float4*>(&vr.w[row][8 * grp]);
+      const float4 w1 = *reinterpret_cast<const float4*>(&vr.w[row][8 * grp + 4]);
+      const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ve_x[i][c] = ww[c] + sa * bb[c];
+    }
+  };
   bf16x4 ev_cs[2][2];           // q|k: cos / sin of the lane's 4 rotary pairs for rows r, r + 16
   const int qk_ocol = QK ? qk_col(nslice, wave, 8 * grp) : 0;  // the lane's first output column
   // Stores of a row half go to a uniform base (the half's first row, the wave's first column) plus a per-lane
@@ -251,18 +334,27 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   //   6 / 12: second shuffle and the wave partial into LDS.
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
-    if constexpr (VV) {
+    if constexpr (VV || VE) {
       // stages 0: vectors; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 (fp32, as the
-      // reference's lowrank output) as fp16 pairs; 5 / 10: the row half's store
-      const QkVec& q = qv[pbuf];
+      // reference's lowrank output), plus the gated embedding term in VE mode, as fp16 pairs; 5 / 10: the row
+      // half's store
+      const float* avw;
+      const float(*uqr)[4];
+      if constexpr (VE) {
+        avw = &vv[pbuf].av[wave][0];
+        uqr = vv[pbuf].uq;
+      } else {
+        avw = &qv[pbuf].av[wave][0];
+        uqr = qv[pbuf].uq;
+      }
       const int r = lane & 15;
       if (st == 0) {
-        const float4 a0 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp]);
-        const float4 a1 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp + 4]);
+        const float4 a0 = *reinterpret_cast<const float4*>(avw + 8 * grp);
+        const float4 a1 = *reinterpret_cast<const float4*>(avw + 8 * grp + 4);
         ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
         ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
-        const float4 u0 = *reinterpret_cast<const float4*>(&q.uq[r][0]);
-        const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
+        const float4 u0 = *reinterpret_cast<const float4*>(&uqr[r][0]);
+        const float4 u1 = *reinterpret_cast<const float4*>(&uqr[16 + r][0]);
         ev_u[0] = u0.w * bf16r(u0.z);
         ev_u[1] = u1.w * bf16r(u1.z);
         return;
@@ -271,8 +363,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       const int i = st < 6 ? 0 : 1, sub = st - (i ? 6 : 1);
       if (sub < 4) {
         const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
-        const float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
-        const float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+        float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
+        float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+        if constexpr (VE) {
+          // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
+          v0 += ve_g[i] * ve_x[i][c];
+          v1 += ve_g[i] * ve_x[i][c + 1];
+        }
         ev_h[i][sub] = pack_f16(v0, v1);
       } else {
         store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
@@ -408,15 +505,30 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   };
 
   // One iteration: wait for block k, MFMAs of block k into acc, interleaved step by step with the epilogue
-  // of block k - 1 (epi) and the partial sums of block k - 2 (sum); then the loads of block k + NBUF - 1
+  // of block k - 1 (epi) and the partial sums of block k - 2 (sum); then the loads of block k + NB - 1
   // into the slot block k - 1 used.
   auto iter = [&](f32x4 (&acc)[2][2], const f32x4 (&prev)[2][2], int k, bool epi, bool sum) {
     // stores are issued in iterations j >= FIRST_STORE (q|k stores block j - 2's rows, the others block j - 1's)
-    wait_block(min(NBUF - 2, nb - 1 - k), min(2, max(0, k - FIRST_STORE)));
+    if constexpr (VE) {
+      // Block k has landed once the operations issued after its loads are the only ones outstanding: in
+      // iteration k - 1 the two stores of block k - 2's epilogue (k >= 2), block k's gather (VE_DMA) and block
+      // k + 1's loads (when issued); block k's gather then has landed too.
+      constexpr int D = DMA_PER_BLOCK<MODE>, E = VE_DMA;
+      const bool xn = k + 1 < nb;
+      if (k == 0) {
+        if (xn) wait_vm_lgkm0<D>(); else wait_vm_lgkm0<0>();
+      } else if (k == 1) {
+        if (xn) wait_vm_lgkm0<E + D>(); else wait_vm_lgkm0<E>();
+      } else {
+        if (xn) wait_vm_lgkm0<2 + E + D>(); else wait_vm_lgkm0<2 + E>();
+      }
+    } else {
+      wait_block(min(NB - 2, nb - 1 - k), min(2, max(0, k - FIRST_STORE)));
+    }
     __builtin_amdgcn_s_barrier();
-    const int pbuf = (k + NBUF - 1) % NBUF;
+    const int pbuf = (k + NB - 1) % NB;
     // lane (row r = lane & 15, group grp): row-half i at LDS row 16 i + r, step s at chunk 16 grp + s
-    const char* xsb = smem + (k % NBUF) * XBYTES + (lane & 15) * XROW + 256 * grp;
+    const char* xsb = smem + (k % NB) * XBYTES + (lane & 15) * XROW + 256 * grp;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -437,16 +549,38 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma16x16x32(wr[j][s], xc[i], acc[i][j]);
       if (epi) epi_stage(prev, k - 1, pbuf, s);
+      if constexpr (VE) {
+        if (s == 11) {
+          // block k's gather (issued in iteration k - 1, or before the ring for k = 0) has landed once block
+          // k + 1's loads (when issued) and this iteration's two stores are the only later operations left
+          if (k >= 1) {
+            if (k + 1 < nb) wait_vm_lgkm0<DMA_PER_BLOCK<MODE> + 2>(); else wait_vm_lgkm0<2>();
+          }
+          ve_read(k);
+        } else if (s == 12 && k + 1 < nb) {
+          // this wave's reads of its gathered rows are complete before the next gather overwrites them
+          wait_vm_lgkm0<63>();
+          ve_next(k);
+        }
+      }
       if constexpr (MODE == XS_RELU2) {
         if (s == 13 && sum) sum_partials(k - 2);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (k + NBUF - 1 < nb) issue(k + NBUF - 1);
+    if (k + NB - 1 < nb) issue(k + NB - 1);
   };
 
+  if constexpr (VE) {
+    // block 0's embedding gather goes out before the ring's loads, from token ids read straight from memory
+    const int64_t* tt = g.idx + (long)nx_p * g.tok_mstride + nx_t0;
+    int64_t tk[4];
 #pragma unroll
-  for (int k = 0; k < NBUF - 1; ++k)
+    for (int q = 0; q < 4; ++q) tk[q] = tt[8 * q + (lane >> 3)];
+    ve_issue(0, tk, tt[lane & 31]);
+  }
+#pragma unroll
+  for (int k = 0; k < NB - 1; ++k)
     if (k < nb) issue(k);
 
   iter(accA, accB, 0, false, false);
@@ -468,8 +602,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   }
 #pragma unroll
   for (int st = 0; st < KS; ++st) {
-    if (last == k) epi_stage(accB, last, last % NBUF, st);
-    else epi_stage(accA, last, last % NBUF, st);
+    if (last == k) epi_stage(accB, last, last % NB, st);
+    else epi_stage(accA, last, last % NB, st);
   }
   if constexpr (MODE == XS_RELU2) {
     wait_vm_lgkm0<0>();
@@ -540,6 +674,18 @@ int xs_v_launch(const LowrankGemmArgs& g, hipStream_t stream) {
   if (!xs_v_supported(g) || !g.u || !g.ra[2] || g.pair_shift < 0 || g.pair_shift > 1) return NOISE_EINVAL;
   if (((uintptr_t)g.ra[2] | (uintptr_t)g.u) & 15) return NOISE_EINVAL;
   return xs_launch<XS_V>(g, stream);
+}
+
+bool xs_ve_supported(const LowrankGemmArgs& g) {
+  return xs_shape_ok(g) && !g.out_tiled && g.N == 512 && g.u_ld == 4 && g.ra_ld % 4 == 0 && g.gate && g.ve_w &&
+         g.ve_a && g.ve_b && g.idx && g.ve_v > 0 && g.tok_mstride >= 0 && g.tok_mstride % 2 == 0 &&
+         !(((uintptr_t)g.gate | (uintptr_t)g.ve_w | (uintptr_t)g.ve_b | (uintptr_t)g.idx) & 15);
+}
+
+int xs_ve_launch(const LowrankGemmArgs& g, hipStream_t stream) {
+  if (!xs_ve_supported(g) || !g.u || !g.ra[2] || g.pair_shift < 0 || g.pair_shift > 1) return NOISE_EINVAL;
+  if (((uintptr_t)g.ra[2] | (uintptr_t)g.u) & 15) return NOISE_EINVAL;
+  return xs_launch<XS_VE>(g, stream);
 }
 
 int xs_qk_launch(const LowrankGemmArgs& g, hipStream_t stream) {

@@ -173,6 +173,59 @@ def test_block_entry_and_qkv_match_oracle():
     assert (v2 - vref).abs().max() <= 2 ** -7 * vref.abs().max() + 1e-3
 
 
+@pytest.mark.parametrize('m,T', [(64, 512), (36, 256)])
+def test_value_embedding_v_many_blocks_per_workgroup(m, T):
+    """v with the gated value embedding (train/val/eggroll.py:84-89) at sizes where every workgroup of the
+    weight-resident kernel walks several 32-row blocks (its ring of x blocks, gathered embedding rows and
+    next-block token ids in steady state, odd and even block counts), one token sequence per member (four
+    distinct sequences) and antithetic pairs sharing a direction: v = bf16(h W_v^T) + s bf16(u_v) a_v +
+    gate (W[idx] + s a[idx] b), within fp16 rounding and one bf16 step of the dense product."""
+    g = torch.Generator().manual_seed(31)
+    V, M, dirs = 4096, m * T, m // 2
+    sign = antithetic_signs(m, 0.05)
+    h = torch.randn(M, 512, generator=g).bfloat16()
+    wqkv = torch.randn(1536, 512, generator=g) / 22
+    a = [torch.randn(dirs, 512, generator=g) for _ in range(3)]
+    u = torch.randn(M, 4, generator=g)
+    u[:, 3] = sign.repeat_interleave(T)
+    gate = 2 * torch.sigmoid(torch.randn(M, 8, generator=g))
+    vw = torch.randn(V, 512, generator=g) * 0.1
+    va, vb = torch.randn(dirs, V, generator=g), torch.randn(dirs, 512, generator=g)
+    seqs = torch.stack([zipf_tokens(T, seed=40 + j)[0] for j in range(4)])
+    idx = seqs[torch.arange(m) % 4]                         # [m, T]: member p reads sequence p % 4
+    cos, sin = om.rotary_tables()
+    d = {k: t.to(DEV).contiguous() for k, t in dict(h=h, u=u, gate=gate, vw=vw, va=va, vb=vb, idx=idx, sign=sign,
+                                                    aq=a[0], ak=a[1], av=a[2], cos=cos, sin=sin).items()}
+    w16 = wqkv.bfloat16().to(DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for ve in (True, False):
+        log_case(f'qkv value embedding={ve} m={m} T={T} (per-member tokens, pair_shift 1)')
+        qkv = torch.empty(M, 1536, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_qkv', d['h'].data_ptr(), w16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(),
+                  d['av'].data_ptr(), d['u'].data_ptr(), d['sign'].data_ptr(), m, T, 1, d['cos'].data_ptr(),
+                  d['sin'].data_ptr(), d['gate'].data_ptr() if ve else None, d['vw'].data_ptr() if ve else None, V,
+                  d['va'].data_ptr() if ve else None, d['vb'].data_ptr() if ve else None,
+                  d['idx'].data_ptr() if ve else None, T, qkv.data_ptr(), s)
+        torch.cuda.synchronize()
+        out[ve] = qkv.cpu()
+    # q | k do not depend on the value embedding
+    assert torch.equal(out[True][:, :1024], out[False][:, :1024])
+    member = torch.arange(M) // T
+    dirn, srow = member // 2, sign[member][:, None]
+    tok = idx.reshape(-1)
+    dense = om.bf(h.float() @ om.bf(wqkv[1024:]).t())
+    v0 = dense + (srow * om.bf(u[:, 2:3])) * a[2][dirn]
+    ve_rows = vw[tok] + (srow * va[dirn, tok][:, None]) * vb[dirn]
+    v1 = v0 + gate.repeat_interleave(64, 1) * ve_rows
+    for ve, ref in ((False, v0), (True, v1)):
+        got = out[ve][:, 1024:].view(torch.float16).float()
+        assert rel_err(got, ref) < 2e-3, ve
+        assert (got - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, ve
+        # v leaves as fp16 of the fp32 value: closer to ref than the bf16 rounding of ref
+        assert rel_err(got, ref.half().float()) < rel_err(om.bf(ref), ref), ve
+
+
 
 def test_deferred_residuals_match_eager_lowrank():
     """Two c_proj outputs deferred into the block entry and one into the MLP entry equal the eager
