@@ -115,7 +115,8 @@ int noise_embed_norm(const float* w, long vocab, const float* a, const float* b,
  * lambda_r / lambda_0 point at this block's entries of resid_lambdas / x0_lambdas (device memory);
  * u_qkv[row, 0..2] = bf16(h . bf16(b_{q,k,v}[dir])), u_qkv[row, 3] = sign[member] (row stride 4: the row
  * noise_qkv reads); when gate_w is not null the value
- * gate gate[row, 0..7] = 2 sigmoid(lowrank(h[:32], gate_w, gate_a, gate_b)).
+ * gate gate[row, 0..7] = 2 sigmoid(lowrank(h[:32], gate_w, gate_a, gate_b)) (gate_w [8, 32] and gate_b
+ * [dirs, 32] 16-byte aligned).
  * Replaces train/val/eggroll.py:76-84, :88. eps_r / eps_0 point at this block's column of the
  * [dirs, n_layer] lambda noise (row stride eps_ld). x_out may alias x_in. The npend (<= 2) deferred
  * residuals in pend (the previous block's attention and MLP c_proj outputs) are added to x_in, in order,

@@ -47,7 +47,7 @@ constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i inside each 16
 // Sum over aligned groups of WIDTH lanes, every lane of a group receiving it. Inside a row of 16 lanes the
 // partial sums combine through DPP operands of the adds (after the two quad steps all lanes of a quad hold
 // its sum, so the mirrors pair whole quads, then whole halves); the four row sums of a 64-lane group meet
-// through v_readlane. No LDS permute: ds_bpermute costs an LDS round trip per step.
+// through gfx950's lane swaps. No LDS permute: ds_bpermute costs an LDS round trip per step.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 || WIDTH == 64, "group width");
@@ -56,9 +56,12 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (WIDTH >= 8) v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
   if constexpr (WIDTH >= 16) v += dpp_f32<DPP_ROW_MIRROR>(v);
   if constexpr (WIDTH == 64) {
-    const int b = __float_as_int(v);
-    v = (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
-        (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+    // the four row sums r0..r3 meet as (r0 + r1) + (r2 + r3) through two VALU lane swaps (v_permlane16_swap,
+    // v_permlane32_swap: no SGPR round trip and none of the wait states a v_readlane result needs)
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float pr = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(pr), __float_as_uint(pr), false, false);
+    v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
   }
   return v;
 }

@@ -177,36 +177,28 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
     ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = s;  // the member's sign rides with the dots
   }
   if (g.gate_w) {
-    // lanes 0..3 hold h[:32]; every lane computes one (gate head, partial) product set
-    float hv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) hv[e] = bf16r(x.v[e]);
-    float ub = 0.f;
-    if (lane < 4) {
-      const float* br = g.gate_b + (long)dir * 32 + lane * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ub += hv[e] * bf16r(br[e]);
-    }
-    ub = group_sum<4>(ub);  // lanes 0..3 now all hold sum over the 32 gate channels
-    const float ubr = bf16r(ub);
-    float z[8];
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      float d = 0.f;
-      if (lane < 4) {
-        const float* wr = g.gate_w + hh * 32 + lane * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d += hv[e] * bf16r(wr[e]);
-      }
-      z[hh] = group_sum<4>(d);
-    }
-    if (lane == 0) {
-      const float* ar = g.gate_a + (long)dir * 8;
-#pragma unroll
-      for (int hh = 0; hh < 8; ++hh) {
-        const float gl = bf16r(z[hh]) + s * ubr * ar[hh];
-        g.gate[row * 8 + hh] = 2.f / (1.f + __expf(-gl));
-      }
+    // gate = 2 sigmoid(lowrank(h[:32], ve_gate)) (train/val/eggroll.py:87) under autocast: bf16 h[:32] against
+    // bf16 rows of W_g and bf16 b_g, exact products, fp32 sums, each rounded to bf16. Every lane takes part:
+    // lane l forms head l / 8's products over channels 4 c .. 4 c + 3 (c = l % 8) and the dot with b over the
+    // same channels; each group of 8 lanes then sums. h[4 c .. 4 c + 3] (two bf16 pairs) comes from lane c / 2,
+    // which holds channels 8 (c / 2) .. + 7.
+    const int hh = lane >> 3, c = lane & 7, src = (c >> 1) << 2;
+    const unsigned w0 = __builtin_amdgcn_ds_bpermute(src, hb.p[0]), w1 = __builtin_amdgcn_ds_bpermute(src, hb.p[1]);
+    const unsigned w2 = __builtin_amdgcn_ds_bpermute(src, hb.p[2]), w3 = __builtin_amdgcn_ds_bpermute(src, hb.p[3]);
+    const unsigned h01 = (c & 1) ? w2 : w0, h23 = (c & 1) ? w3 : w1;
+    const float4 wg = *reinterpret_cast<const float4*>(g.gate_w + hh * 32 + 4 * c);
+    const float4 bg = *reinterpret_cast<const float4*>(g.gate_b + (long)dir * 32 + 4 * c);
+    auto dot4 = [&](const float4& v) {
+      const float d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, h01),
+                                                      __builtin_bit_cast(bf16x2, pack_bf16x2(v.x, v.y)), 0.f, false);
+      return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, h23),
+                                             __builtin_bit_cast(bf16x2, pack_bf16x2(v.z, v.w)), d, false);
+    };
+    const float z = group_sum<8>(dot4(wg));   // head hh's dense logit in lanes 8 hh .. 8 hh + 7
+    const float ub = group_sum<8>(dot4(bg));  // h[:32] . b in every lane
+    if (c == 0) {
+      const float gl = bf16r(z) + s * bf16r(ub) * g.gate_a[(long)dir * 8 + hh];
+      g.gate[row * 8 + hh] = 2.f / (1.f + __expf(-gl));
     }
   }
 }
@@ -430,7 +422,8 @@ int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.T <= 0 || !g.x_out || !g.h || !g.u_qkv || !g.sign || !g.eps_r || !g.eps_0 ||
       !g.lambda_r || !g.lambda_0 || !g.b_qkv[0] || !g.b_qkv[1] || !g.b_qkv[2])
     return NOISE_EINVAL;
-  if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate)) return NOISE_EINVAL;
+  if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate || (((uintptr_t)g.gate_w | (uintptr_t)g.gate_b) & 15)))
+    return NOISE_EINVAL;
   if (bad_pending(g.pend, g.npend)) return NOISE_EINVAL;
   hipLaunchKernelGGL(block_entry_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
