@@ -80,7 +80,9 @@ struct VeVec {
   int64_t tok[R];     // token ids of the NEXT block's rows (they address that block's embedding gather)
 };
 struct VeRows {
-  float w[R][32];     // ve_w[tok] over the wave's 32 columns, one row per block row
+  float w[R][32];     // ve_w[tok] over the wave's 32 columns, one row per block row; the 16-byte chunk c of row r
+                      // sits at chunk c ^ ((r / 2) % 8), so the 16 rows one read instruction touches fall in
+                      // distinct banks
   float b[32];        // ve_b[dir] over the wave's 32 columns
   float a[R];         // ve_a[dir, tok] per block row
 };
@@ -270,14 +272,16 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   float ve_x[2][8], ve_g[2];
 
   // The gather of block k's embedding rows into this wave's VeRows (VE_DMA loads): tk[q] is the token of block
-  // row 8 q + lane / 8 (lane % 8 loads columns 4 (lane % 8) .. + 3 of the wave's 32), tka the token of row
-  // lane % 32 (lanes 0-31 load a[dir, tok]).
+  // row r = 8 q + lane / 8, whose physical chunk lane % 8 receives logical chunk (lane % 8) ^ ((r / 2) % 8)
+  // (columns 4 c .. 4 c + 3 of the wave's 32); tka the token of row lane % 32 (lanes 0-31 load a[dir, tok]).
   auto ve_issue = [&](int k, const int64_t(&tk)[4], int64_t tka) {
     const int p = blk_of(k) * R / g.T, dir = p >> g.pair_shift;
     VeRows& vr = ver[wave];
-    const int c4 = fw + 4 * (lane & 7);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma_x4(g.ve_w + tk[q] * 512 + c4, &vr.w[8 * q][0]);
+    for (int q = 0; q < 4; ++q) {
+      const int r = 8 * q + (lane >> 3);
+      dma_x4(g.ve_w + tk[q] * 512 + fw + 4 * ((lane & 7) ^ ((r >> 1) & 7)), &vr.w[8 * q][0]);
+    }
     if (lane < 8) dma_x4_s(g.ve_b + (long)dir * 512 + fw, lane16, &vr.b[0]);
     if (lane < R) dma_x1(g.ve_a + (long)dir * g.ve_v + tka, &vr.a[0]);
   };
@@ -302,8 +306,9 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       const int row = 16 * i + r;
       const float sa = q.uq[row][3] * vr.a[row];
       ve_g[i] = q.gate[row][head];
-      const float4 w0 = *reinterpret_cast<const float4*>(&vr.w[row][8 * grp]);
-      const float4 w1 = *reinterpret_cast<const float4*>(&vr.w[row][8 * grp + 4]);
+      const int sw = (row >> 1) & 7;
+      const float4 w0 = *reinterpret_cast<const float4*>(&vr.w[row][4 * ((2 * grp) ^ sw)]);
+      const float4 w1 = *reinterpret_cast<const float4*>(&vr.w[row][4 * ((2 * grp + 1) ^ sw)]);
       const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
       for (int c = 0; c < 8; ++c) ve_x[i][c] = ww[c] + sa * bb[c];
