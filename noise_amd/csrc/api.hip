@@ -395,7 +395,7 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
   if (members <= 0 || T <= 0 || !bytes || !lowrank_gemm_parts(vocab)) return NOISE_EINVAL;
   const size_t M = (size_t)members * T;
   Carve c(nullptr);
-  c.take<bf16>(M * (fp32_head ? 3 : 1) * DM);      // head operand
+  c.take<bf16>(M * (fp32_head ? 2 : 1) * DM);      // head operand ([hi | lo] rows for the fp32 head)
   c.take<float>(M);                                // h . b
   c.take<float>(M * lowrank_gemm_parts(vocab));    // partial sums of exp(z')
   c.take<float>(M);                                // z' at the target
@@ -417,9 +417,9 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t M = (size_t)members * T;
-  const int K = (fp32_head ? 3 : 1) * DM, parts = lowrank_gemm_parts(vocab);
+  const int K = (fp32_head ? 3 : 1) * DM, lda = (fp32_head ? 2 : 1) * DM, parts = lowrank_gemm_parts(vocab);
   Carve c(workspace);
-  bf16* hop = c.take<bf16>(M * K);
+  bf16* hop = c.take<bf16>(M * lda);
   float* u = c.take<float>(M);
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
@@ -427,7 +427,8 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   if (int rc = copy_pending(pend, npend, hn.pend)) return rc;
   hn.npend = npend;
   if (int rc = head_norm_launch(hn, s)) return rc;
-  LowrankGemmArgs g = base_args(hop, K, (long)T * K, w_head, K, vocab, a, sign, members, T, pair_shift);
+  LowrankGemmArgs g = base_args(hop, lda, (long)T * lda, w_head, K, vocab, a, sign, members, T, pair_shift);
+  g.a_fold = fp32_head ? DM : 0;
   g.u = u;
   g.u_parts = 1;
   g.u_ld = 1;

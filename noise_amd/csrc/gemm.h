@@ -31,10 +31,13 @@ struct LowrankGemmArgs {
   // A operand: row r (member p = r / T, token t = r % T) starts at A + p * a_mstride + t * lda.
   // a_mstride = T * lda for per-member activations, 0 for one activation broadcast to all members.
   // a_tiled: A is TILE16 with leading dimension lda over all M rows (requires a_mstride = T * lda).
+  // a_fold > 0: the contraction index k >= a_fold reads A column k - a_fold (the fp32 head's [hi | lo] rows
+  // serve the K = 1536 product [hi | hi | lo] . [W_hi | W_lo | W_hi] without a stored second copy of hi).
   const __bf16* A;
   long lda;
   long a_mstride;
   int a_tiled;
+  int a_fold;
   const __bf16* W;  // [N, K], K contiguous (nn.Linear orientation)
   long ldw;
   int M, N, K;

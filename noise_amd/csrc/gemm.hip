@@ -167,7 +167,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto issue = [&](int kt, int buf) {
     bf16* sx = smem + buf * C::STAGE;
     bf16* sw = sx + BM * BK;
-    const int k0 = kt * BK, ka = g.a_tiled ? kt * 512 : k0;
+    const int k0 = kt * BK, ka = g.a_tiled ? kt * 512 : (g.a_fold && k0 >= g.a_fold ? k0 - g.a_fold : k0);
 #pragma unroll
     for (int d = 0; d < C::LA; ++d)
       __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
@@ -546,8 +546,10 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     if (xs_dense_supported(g)) return xs_dense_launch(g, stream);
     return launch_epi<EPI_DENSE>(g, stream);
   }
+  if (g.a_fold && (epi != EPI_CE || g.a_tiled || g.a_fold < 0 || g.a_fold % 64 || g.a_fold >= g.K))
+    return NOISE_EINVAL;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
-      g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K ||
+      g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K - g.a_fold || g.ldw < g.K ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
       g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.seg0 < 0 || g.seg0 + g.N / g.seg_n > 3 || g.u_qstride < 1)
     return NOISE_EINVAL;

@@ -78,7 +78,7 @@ struct HeadNormArgs {
   const void* x;         // [M, 512] fp32, or bf16 when x_bf16
   int x_bf16;
   const float* gain;     // [512] or null
-  __bf16* h;             // fp32 head: [M, 1536] = [hi | hi | lo]; bf16 head: [M, 512]
+  __bf16* h;             // fp32 head: [M, 1024] = [hi | lo]; bf16 head: [M, 512]
   const float* b;        // [dirs, 512]
   float* u;              // [M]
   const float* sign;

@@ -222,10 +222,10 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
   if (lane == 0) g.u[row] = u;
 }
 
-// Final norm feeding the head (train/val/eggroll.py:94-99). fp32 head: the operand is the bf16
-// split [hi | hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)) against [W_hi | W_lo | W_hi], so one
-// bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16 relative; the dot h.b is fp32. bf16 head: the
-// operand is bf16(h) and the dot follows autocast.
+// Final norm feeding the head (train/val/eggroll.py:94-99). fp32 head: the operand rows are the bf16
+// split [hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)); the head GEMM reads them as [hi | hi | lo] (its
+// a_fold) against [W_hi | W_lo | W_hi], so one bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16
+// relative; the dot h.b is fp32. bf16 head: the operand is bf16(h) and the dot follows autocast.
 __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -252,10 +252,9 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     Row8 lo;
 #pragma unroll
     for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
-    bf16* o = g.h + row * (3 * D) + lane * 8;
+    bf16* o = g.h + row * (2 * D) + lane * 8;
     store8_bf16(o, x);
-    store8_bf16(o + D, x);
-    store8_bf16(o + 2 * D, lo);
+    store8_bf16(o + D, lo);
     const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
     float acc = 0.f;
 #pragma unroll
