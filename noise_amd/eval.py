@@ -11,10 +11,13 @@ fp32-accurate head), accumulates in fp64 and returns the mean over all predictio
 Rounding differs from utils/eval.py. The reference runs GPT.forward under CUDA autocast with bf16 embeddings, so
 its whole residual stream is bf16: x0, every residual add and mix, the norms' outputs, rotary's products, the value
 gate and the attention probabilities round to bf16 (rms_norm and the 0-dim lambda products keep their input's
-bf16 dtype). The kernels keep the population path's rounding points instead: an fp32 residual stream and fp32
-norms, bf16 GEMM operands and outputs, fp16 attention operands. On a trained-scale synthetic model the two streams'
-mean losses differ by about 2e-3 (a CPU estimate on 2 x 256 tokens), so a score from `evaluate` is not
-interchangeable with the reference's at that level.
+bf16 dtype, and F.rms_norm's default eps follows the input dtype: 2^-7 for bf16). The kernels keep the population
+path's rounding points instead: an fp32 residual stream and fp32 norms, bf16 GEMM operands and outputs, fp16
+attention operands. On a trained-scale synthetic model (4 x 256 tokens, CPU) the two mean losses differ by 1.8e-3.
+That is the size of the shift any single one of those rounding points produces on its own there (0.4e-3 to
+2.0e-3 each: the bf16 stream, its eps, the bf16 tables, rotary's per-product rounding, bf16 q / k / P, the bf16
+head), and of the shift the GEMMs' fp32 accumulation order alone produces at that scale (~1.5e-3), so a score from
+`evaluate` agrees with the reference's to about 2e-3, not better.
 """
 from pathlib import Path
 
