@@ -404,8 +404,8 @@ def run_library(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=3)
-    ap.add_argument('--warmup', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=10)
+    ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy', 'stream', 'library'),
                     default='step')
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
