@@ -392,7 +392,8 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
 }
 
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes) {
-  if (members <= 0 || T <= 0 || !bytes || !lowrank_gemm_parts(vocab)) return NOISE_EINVAL;
+  // the CE finalisation reads each row's partials four at a time: vocab / 64 partials, a multiple of 4
+  if (members <= 0 || T <= 0 || !bytes || vocab <= 0 || vocab % 256 || !lowrank_gemm_parts(vocab)) return NOISE_EINVAL;
   const size_t M = (size_t)members * T;
   Carve c(nullptr);
   c.take<bf16>(M * (fp32_head ? 2 : 1) * DM);      // head operand ([hi | lo] rows for the fp32 head)

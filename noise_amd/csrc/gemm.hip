@@ -551,7 +551,7 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K - g.a_fold || g.ldw < g.K ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
-      g.seg_n <= 0 || g.seg_n % 256 || g.N % g.seg_n || g.seg0 < 0 || g.seg0 + g.N / g.seg_n > 3 || g.u_qstride < 1)
+      g.seg_n <= 0 || g.seg_n % 128 || g.N % g.seg_n || g.seg0 < 0 || g.seg0 + g.N / g.seg_n > 3 || g.u_qstride < 1)
     return NOISE_EINVAL;
   const int nseg = g.N / g.seg_n;
   if (g.u_qstride == 1 && g.u_ld < (g.seg0 + nseg) * g.u_parts) return NOISE_EINVAL;

@@ -86,6 +86,10 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert head(None, 0, 0, 1, None) == EINVAL       # a loss needs targets
     assert head(None, 0, 0, None, None) == EINVAL    # nothing to produce
     assert head(None, 256, 0, None, 1) == ENOSPC     # logits only
+    # the CE partials are read four at a time: vocab / 64 must be a multiple of 4
+    assert lib.noise_head_ce_workspace_size(2, 256, 640, 1, ctypes.byref(ctypes.c_size_t(0))) == EINVAL
+    assert lib.noise_head_ce(1, 0, None, 1, 640, 1, 1, 1, 1, 1, 0, 1, 256, 0, 0, 1, None, 1, 1 << 40, None, 0,
+                             None) == EINVAL
     assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
     assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
     ptr, count, _keep = _lib.gather_params([(1, 1, None, 8, 4)])   # b null with in > 0

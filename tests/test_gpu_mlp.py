@@ -99,6 +99,24 @@ def test_lowrank_linear_ragged_rows(T):
     assert rel_err(y.cpu(), ref) < 1e-3
 
 
+@pytest.mark.parametrize('dout', [384, 640])
+def test_lowrank_linear_narrow_tiles(dout):
+    """Output widths that are a multiple of 128 but not of 256 run the tile GEMM's 256 x 128 configuration."""
+    from noise_amd import ops
+    g = torch.Generator().manual_seed(6)
+    P, T, din = 4, 128, 512
+    log_case(f'lowrank_linear narrow tiles P={P} T={T} {din}->{dout}')
+    x = torch.randn(P, T, din, generator=g).bfloat16()
+    w = (torch.randn(dout, din, generator=g) / 20).bfloat16()
+    a, b = torch.randn(P, dout, generator=g), torch.randn(P, din, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 3e-2, -3e-2])
+    y = ops.lowrank_linear(x.to(DEV), w.to(DEV), a.to(DEV), b.to(DEV), sign.to(DEV))
+    torch.cuda.synchronize()
+    ref = om.lowrank(x.float(), w.float(), a, b, sign, 'bf16')
+    assert rel_err(y.cpu(), ref) < 1e-3
+    assert (y.cpu() - ref).abs().max() < 2e-2
+
+
 def test_mlp_config1_full_size_sampled_members():
     """Config 1 at its real shape (P = 256, T = 2048, shared x); three members checked in full."""
     from noise_amd import ops

@@ -173,6 +173,53 @@ def test_block_entry_and_qkv_match_oracle():
     assert (v2 - vref).abs().max() <= 2 ** -7 * vref.abs().max() + 1e-3
 
 
+def test_qkv_tile_gemm_path_for_token_counts_not_a_multiple_of_32():
+    """noise_qkv at T = 48 (not a multiple of the weight-resident kernel's 32-row blocks) runs q | k | v, with the
+    gated value embedding, on the tile GEMM's QKV epilogue: the same formats (fp16, q times log2(e) / 8) and the
+    same arithmetic, checked against the oracle ops from the GPU's own h, u and gate."""
+    g = torch.Generator().manual_seed(33)
+    m, T, V = 4, 48, 4096
+    M = m * T
+    sign = antithetic_signs(m, 0.05)
+    h = torch.randn(M, 512, generator=g).bfloat16()
+    wq, wk, wv = (torch.randn(512, 512, generator=g) / 22 for _ in range(3))
+    aq, ak, av = (torch.randn(m // 2, 512, generator=g) for _ in range(3))
+    u = torch.randn(M, 4, generator=g)
+    u[:, 3] = sign.repeat_interleave(T)
+    gate = 2 * torch.sigmoid(torch.randn(M, 8, generator=g))
+    vw = torch.randn(V, 512, generator=g) * 0.1
+    va, vb = torch.randn(m // 2, V, generator=g), torch.randn(m // 2, 512, generator=g)
+    idx, _ = zipf_tokens(T, seed=34)
+    cos, sin = om.rotary_tables()
+    d = {k: t.to(DEV).contiguous() for k, t in dict(h=h, u=u, gate=gate, vw=vw, va=va, vb=vb, idx=idx, sign=sign,
+                                                    aq=aq, ak=ak, av=av, cos=cos, sin=sin).items()}
+    w16 = torch.cat([wq, wk, wv]).bfloat16().to(DEV)
+    qkv = torch.empty(M, 1536, device=DEV, dtype=torch.bfloat16)
+    log_case(f'qkv tile-GEMM path m={m} T={T}')
+    _lib.call('noise_qkv', d['h'].data_ptr(), w16.data_ptr(), d['aq'].data_ptr(), d['ak'].data_ptr(),
+              d['av'].data_ptr(), d['u'].data_ptr(), d['sign'].data_ptr(), m, T, 1, d['cos'].data_ptr(),
+              d['sin'].data_ptr(), d['gate'].data_ptr(), d['vw'].data_ptr(), V, d['va'].data_ptr(), d['vb'].data_ptr(),
+              d['idx'].data_ptr(), 0, qkv.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    member = torch.arange(M) // T
+    dirn, srow = member // 2, sign[member][:, None]
+    hf = h.float()
+
+    def lin(w, a, col):
+        return om.bf(hf @ om.bf(w).t()) + (srow * om.bf(u[:, col:col + 1])) * a[dirn]
+    q, k, v = lin(wq, aq, 0), lin(wk, ak, 1), lin(wv, av, 2)
+    tok = idx.repeat(m)
+    v = v + gate.repeat_interleave(64, 1) * (vw[tok] + (srow * va[dirn, tok][:, None]) * vb[dirn])
+    c, sn = cos[:T], sin[:T]
+    qr = om.norm(om.apply_rotary(q.view(m, T, 8, 64), c, sn)).reshape(M, 512)
+    kr = om.norm(om.apply_rotary(k.view(m, T, 8, 64), c, sn)).reshape(M, 512)
+    got = qkv.cpu().view(torch.float16).float()
+    got[:, :512] /= math.log2(math.e) / 8
+    for sl, ref in ((slice(0, 512), qr), (slice(512, 1024), kr), (slice(1024, 1536), v)):
+        assert rel_err(got[:, sl], ref) < 2e-3, sl
+        assert (got[:, sl] - ref).abs().max() <= 2 ** -7 * ref.abs().max() + 1e-3, sl
+
+
 @pytest.mark.parametrize('m,T', [(64, 512), (36, 256)])
 def test_value_embedding_v_many_blocks_per_workgroup(m, T):
     """v with the gated value embedding (train/val/eggroll.py:84-89) at sizes where every workgroup of the
@@ -407,6 +454,37 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
         else:
             ref = om.head_loss(h, W, a, b, sign, targets, 'bf16', 'bf16')
             assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
+
+
+@pytest.mark.parametrize('fp32', [1, 0])
+def test_head_ce_other_vocab_and_partial_row_tile(fp32):
+    """A 768-entry vocabulary (3 column tiles, 12 CE partials per row) and a token count (96) that leaves the
+    last 256-row tile partial."""
+    g = torch.Generator().manual_seed(14)
+    m, T, V = 4, 96, 768
+    x = torch.randn(m * T, 512, generator=g) * 3
+    W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
+    targets = torch.randint(0, V, (T,), generator=g)
+    s = torch.cuda.current_stream().cuda_stream
+    h = om.norm(x.view(m, T, 512))
+    xd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (x, W, a, b, sign, targets))
+    log_case(f'head_ce m={m} T={T} V={V} fp32_head={fp32}')
+    wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+    loss = torch.empty(m, device=DEV)
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV, dtype=torch.uint8)
+    _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
+              sd.data_ptr(), td.data_ptr(), 0, m, T, 0, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None, ws.data_ptr(),
+              ws.numel(), None, 0, s)
+    torch.cuda.synchronize()
+    if fp32:
+        ref = om.head_loss(h, W, a, b, sign, targets, 'fp32', 'fp32')
+        assert (loss.cpu() - ref).abs().max() < 1e-4, (loss.cpu(), ref)
+    else:
+        ref = om.head_loss(h, W, a, b, sign, targets, 'bf16', 'bf16')
+        assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
 
 
 def test_head_ce_config3_bf16_input_with_gain():
