@@ -47,6 +47,12 @@ typedef void* noise_stream_t; /* hipStream_t */
                                * (r, c) at (r/16)*16*cols + (c/32)*512 + 8*p + c%8 with
                                * p = 4*(r%16) + (((c%32)/8) ^ (((r%16)/2) % 4)). Same footprint as ROWS; a
                                * producer writes and the GEMM loads it as whole 128-byte lines. */
+#define NOISE_LAYOUT_WTILE 2  /* a bf16 weight W [rows = out, cols = in] (rows % 64 == 0, cols % 32 == 0) in the
+                               * order of the tile GEMM's 32-deep stages: the 1 KiB block (g, s) at element
+                               * (g*cols/32 + s)*512 holds cols 32s .. 32s+31 of the 16 rows with tiled index
+                               * i = 16g + r (r < 16), row r being weight row
+                               * (i - i%64) + (r/4)*16 + ((i%64)/16)*4 + r%4, its 16-byte chunk c at
+                               * c ^ ((r/2) % 4). Same footprint as ROWS; written by noise_weight_tiles. */
 
 /* A c_proj output not yet added to the residual stream (a deferred residual): row r of member p receives
  *   y[r, c] + sign[p] * bf16(sum_{q < u_parts} u[r * u_row_stride + q * u_part_stride]) * a[dir * 512 + c]
@@ -90,7 +96,8 @@ int noise_lowrank_linear(const void* x, long x_ld, long x_mstride, const void* w
  *   w_fc    bf16 [f, d];  a_fc [dirs, f], b_fc [dirs, d]
  *   w_proj  bf16 [d, f];  a_proj [dirs, d], b_proj [dirs, f]
  *   y_f32 / y_bf16 / accumulate as in noise_lowrank_linear; d == 512, f % 256 == 0, T % 32 == 0.
- * Workspace: noise_lowrank_mlp_workspace_size(). */
+ * Workspace: noise_lowrank_mlp_workspace_size() (the hidden, its dot partials and a WTILE copy of w_proj, made
+ * on every call). */
 int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* bytes);
 int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc, const void* w_proj, int d, int f,
                       const float* a_fc, const float* b_fc, const float* a_proj, const float* b_proj,
@@ -198,12 +205,18 @@ int noise_lowrank_resid(const void* x, const void* w, int in, int out, const flo
                         long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
                         float* resid, noise_stream_t stream);
 
+/* The NOISE_LAYOUT_WTILE copy of a row-major bf16 weight w [rows, cols] into out (rows * cols bf16): the
+ * per-step layout change of a GEMM weight, like the bf16 cast of train/val/eggroll.py:144's autocast done
+ * once per step. rows % 64 == 0, cols % 32 == 0, 16-byte aligned pointers. */
+int noise_weight_tiles(const void* w, int rows, int cols, void* out, noise_stream_t stream);
+
 /* y = bf16(x W^T) [members*T, out] for x bf16 [members*T, in] (x_layout NOISE_LAYOUT_ROWS or
- * NOISE_LAYOUT_TILE16), w bf16 [out, in]: the dense product of a c_proj `lowrank` whose rank-1 term and
- * residual add are deferred to the row kernel that next reads the stream (noise_pending_t). in % 64 == 0,
+ * NOISE_LAYOUT_TILE16), w bf16 [out, in] (w_layout NOISE_LAYOUT_ROWS or NOISE_LAYOUT_WTILE, the layout the
+ * K > 512 tile GEMM loads fastest): the dense product of a c_proj `lowrank` whose rank-1 term and residual
+ * add are deferred to the row kernel that next reads the stream (noise_pending_t). in % 64 == 0,
  * out % 128 == 0; TILE16 also T % 16 == 0. */
-int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int members, int T, void* y,
-                     noise_stream_t stream);
+int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int w_layout, int members, int T,
+                     void* y, noise_stream_t stream);
 
 /* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). The npend (<= 2)
  * deferred residuals in pend are added to x, in order, before the norm; x itself is not written. */

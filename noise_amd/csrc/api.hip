@@ -142,6 +142,7 @@ int noise_lowrank_mlp_workspace_size(int members, int T, int d, int f, size_t* b
   c.take<float>(M);                            // u_fc
   c.take<float>(M * xs_relu2_parts(f));        // partial dots h.b_proj, part-major
   c.take<bf16>(M * f);                         // hidden h
+  c.take<bf16>((size_t)d * f);                 // w_proj in the tile GEMM's WTILE layout
   *bytes = c.used;
   return NOISE_OK;
 }
@@ -162,6 +163,7 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   const int parts = xs_relu2_parts(f);
   float* upart = c.take<float>(M * parts);
   bf16* hid = c.take<bf16>(M * f);
+  bf16* wpt = c.take<bf16>((size_t)d * f);
   if (int rc = rowdot_launch(static_cast<const bf16*>(x), x_ld, x_mstride, (int)M, d, T, pair_shift, b_fc, d, u_fc, s))
     return rc;
   LowrankGemmArgs g1 = base_args(x, x_ld, x_mstride, w_fc, d, f, a_fc, sign, members, T, pair_shift);
@@ -176,8 +178,11 @@ int noise_lowrank_mlp(const void* x, long x_ld, long x_mstride, const void* w_fc
   g1.upart_out = upart;
   g1.upart_ld = parts;
   if (int rc = lowrank_gemm_launch(EPI_RELU2, g1, s)) return rc;
-  LowrankGemmArgs g2 = base_args(hid, f, (long)T * f, w_proj, f, d, a_proj, sign, members, T, pair_shift);
+  // c_proj loads both operands as whole 128-byte lines: the hidden in TILE16, w_proj copied into WTILE
+  if (int rc = weight_tiles_launch(static_cast<const bf16*>(w_proj), f, d, f, wpt, s)) return rc;
+  LowrankGemmArgs g2 = base_args(hid, f, (long)T * f, wpt, f, d, a_proj, sign, members, T, pair_shift);
   g2.a_tiled = 1;
+  g2.w_tiled = 1;
   g2.u = upart;
   g2.u_parts = parts;
   g2.u_ld = 1;
@@ -359,12 +364,19 @@ int noise_norm_dot(const float* x, void* h, const float* b, float* u, const floa
   return norm_dot_launch(g, static_cast<hipStream_t>(stream));
 }
 
-int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int members, int T, void* y,
-                     noise_stream_t stream) {
+int noise_weight_tiles(const void* w, int rows, int cols, void* out, noise_stream_t stream) {
+  return weight_tiles_launch(static_cast<const bf16*>(w), cols, rows, cols, static_cast<bf16*>(out),
+                             static_cast<hipStream_t>(stream));
+}
+
+int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int w_layout, int members, int T,
+                     void* y, noise_stream_t stream) {
   if (members <= 0 || T <= 0 || (long)members * T > 0x7fffffffL || in <= 0 || out <= 0) return NOISE_EINVAL;
   if (x_layout != NOISE_LAYOUT_ROWS && x_layout != NOISE_LAYOUT_TILE16) return NOISE_EINVAL;
+  if (w_layout != NOISE_LAYOUT_ROWS && w_layout != NOISE_LAYOUT_WTILE) return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, nullptr, nullptr, members, T, 0);
   g.a_tiled = x_layout == NOISE_LAYOUT_TILE16;
+  g.w_tiled = w_layout == NOISE_LAYOUT_WTILE;
   g.out_bf16 = static_cast<bf16*>(y);
   g.ldo = out;
   return lowrank_gemm_launch(EPI_DENSE, g, static_cast<hipStream_t>(stream));
@@ -424,6 +436,8 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   float* u = c.take<float>(M);
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
+  // Both operands stay row-major: WTILE / TILE16 copies of them (whole-line loads) measured 1-2% slower on this
+  // GEMM, whose column tiles of one XCD read the same weight blocks at the same time.
   HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
   if (int rc = copy_pending(pend, npend, hn.pend)) return rc;
   hn.npend = npend;

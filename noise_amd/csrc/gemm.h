@@ -27,6 +27,20 @@ __host__ __device__ inline long tile16_offset(long r, long c, long ld) {
   return (r >> 4) * 16 * ld + (c >> 5) * 512 + 8 * p + (c & 7);
 }
 
+// WTILE layout of a bf16 weight W [N, K] (N % 64 == 0, K % 32 == 0), the order in which the tile GEMM's
+// 32-deep LDS stages hold it: the 1 KiB block (g, s) at element (g * K / 32 + s) * 512 holds columns
+// 32 s .. 32 s + 31 of the 16 rows with tiled index i = 16 g + r (r < 16), row r of the block being weight row
+// (i & ~63) + (r >> 2) * 16 + ((i & 63) >> 4) * 4 + (r & 3), its 16-byte chunk c at chunk c ^ ((r >> 1) & 3).
+// Within each 64-row band, MFMA block j of a wave's 64 output columns then reads 16 consecutive LDS rows and
+// a lane's 16 output columns are contiguous (the tile GEMM's transposed product). One wave-wide LDS-DMA
+// instruction moves one block as eight whole 128-byte lines (row-major rows give 64-byte half lines, which
+// the L2 -> LDS path serves at about half the rate).
+__host__ __device__ inline long wtile_offset(long n, long k, long K) {
+  const long loc = n & 63;
+  const long i = (n & ~63L) + ((loc >> 2) & 3) * 16 + ((loc >> 4) << 2) + (loc & 3), r = i & 15;
+  return ((i >> 4) * (K >> 5) + (k >> 5)) * 512 + 32 * r + 8 * (((k & 31) >> 3) ^ ((r >> 1) & 3)) + (k & 7);
+}
+
 struct LowrankGemmArgs {
   // A operand: row r (member p = r / T, token t = r % T) starts at A + p * a_mstride + t * lda.
   // a_mstride = T * lda for per-member activations, 0 for one activation broadcast to all members.
@@ -38,8 +52,9 @@ struct LowrankGemmArgs {
   long a_mstride;
   int a_tiled;
   int a_fold;
-  const __bf16* W;  // [N, K], K contiguous (nn.Linear orientation)
-  long ldw;
+  const __bf16* W;  // [N, K], K contiguous (nn.Linear orientation), or WTILE when w_tiled
+  long ldw;         // row stride of a row-major W (ignored when w_tiled)
+  int w_tiled;
   int M, N, K;
   int T;              // rows per member
   int pair_shift;     // perturbation row of member p is p >> pair_shift (1: antithetic pairs share a, b)
@@ -87,6 +102,9 @@ struct LowrankGemmArgs {
   long tok_mstride;      // 0: one sequence shared by every member; T: one sequence per member
   float* logits;
 };
+
+// WTILE copy (out, N * K bf16) of a row-major bf16 weight in [N, K] with row stride ld.
+int weight_tiles_launch(const __bf16* in, long ld, int N, int K, __bf16* out, hipStream_t stream);
 
 // Number of per-row partials EPI_CE writes for an N-column output (0: N unsupported).
 int lowrank_gemm_parts(int N);

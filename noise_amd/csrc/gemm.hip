@@ -157,6 +157,11 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     }
 #pragma unroll
     for (int d = 0; d < C::LB; ++d) {
+      if (g.w_tiled) {
+        // WTILE: these 16 LDS rows are one 1 KiB block per 32-deep stage, already in LDS order
+        b_src[d] = g.W + (long)((n0 >> 4) + wave * C::LB + d) * KT * 512 + 8 * lane;
+        continue;
+      }
       const int R = (wave * C::LB + d) * C::ROWS_PER_DMA + lrow;
       const int c = (lane % C::CPR) ^ ((R / C::RPL) % C::CPR);
       const int loc = R % WN, r = loc & 15;
@@ -167,14 +172,17 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto issue = [&](int kt, int buf) {
     bf16* sx = smem + buf * C::STAGE;
     bf16* sw = sx + BM * BK;
-    const int k0 = kt * BK, ka = g.a_tiled ? kt * 512 : (g.a_fold && k0 >= g.a_fold ? k0 - g.a_fold : k0);
+    // A column of this stage (a_fold: the contraction index k >= a_fold reads column k - a_fold); a TILE16 A
+    // and a WTILE W hold one 512-element block per 32 columns
+    const int k0 = kt * BK, kc = g.a_fold && k0 >= g.a_fold ? k0 - g.a_fold : k0;
+    const long ka = g.a_tiled ? (long)kc * 16 : kc, kw = g.w_tiled ? (long)kt * 512 : k0;
 #pragma unroll
     for (int d = 0; d < C::LA; ++d)
       __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
                                        (lds_void_t*)(sx + (wave * C::LA + d) * 512), 16, 0, 0);
 #pragma unroll
     for (int d = 0; d < C::LB; ++d)
-      __builtin_amdgcn_global_load_lds((const void*)(b_src[d] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[d] + kw),
                                        (lds_void_t*)(sw + (wave * C::LB + d) * 512), 16, 0, 0);
   };
 
@@ -504,9 +512,12 @@ int num_cus() {
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int OCC, int EPI>
 int launch_cfg(const LowrankGemmArgs& g, hipStream_t stream) {
+  using C = Cfg<BM, BN, BK, STAGES, WGM, WGN>;
   if (g.N % BN || g.K % 64) return NOISE_ENOTSUP;
-  // a TILE16 A operand is one tile per 16-row DMA instruction and 32-deep stage
-  if (g.a_tiled && (BK != 32 || Cfg<BM, BN, BK, STAGES, WGM, WGN>::ROWS_PER_DMA != 16)) return NOISE_ENOTSUP;
+  // a TILE16 A operand is one tile per 16-row DMA instruction and 32-deep stage; a WTILE W one block, whose row
+  // order is the one of 64-column wave tiles with 16 contiguous columns per lane
+  if (g.a_tiled && (BK != 32 || C::ROWS_PER_DMA != 16)) return NOISE_ENOTSUP;
+  if (g.w_tiled && (BK != 32 || C::ROWS_PER_DMA != 16 || C::WN != 64 || C::CW != 16)) return NOISE_ENOTSUP;
   const long tiles = (long)((g.M + BM - 1) / BM) * (g.N / BN);
   if (tiles > 0x7fffffffL) return NOISE_ENOTSUP;
   // OCC persistent workgroups per CU, a multiple of 8 for the XCD split
@@ -528,6 +539,32 @@ int launch_epi(const LowrankGemmArgs& g, hipStream_t stream) {
 
 }  // namespace
 
+namespace {
+// WTILE copy of a row-major bf16 weight: thread q writes the 16-byte output chunk q (block q / 64, row r and
+// physical chunk p of the block), read from the weight row and logical chunk the layout assigns to it.
+__global__ void __launch_bounds__(256) weight_tiles_kernel(const bf16* __restrict__ in, long ld, int K, long chunks,
+                                                           bf16* __restrict__ out) {
+  const long q = (long)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const long blk = q >> 6, kt = K >> 5, g = blk / kt, st = blk - g * kt;
+  const int u = (int)(q & 63), r = u >> 2, c = (u & 3) ^ ((r >> 1) & 3);
+  const long i = 16 * g + r;
+  const long n = (i & ~63L) + (r >> 2) * 16 + ((i & 63) >> 4) * 4 + (r & 3);
+  *reinterpret_cast<uint4*>(out + 8 * q) = *reinterpret_cast<const uint4*>(in + n * ld + 32 * st + 8 * c);
+}
+}  // namespace
+
+int weight_tiles_launch(const bf16* in, long ld, int N, int K, bf16* out, hipStream_t stream) {
+  if (!in || !out || N <= 0 || K <= 0 || N % 64 || K % 32 || ld < K || ld % 8 ||
+      (((uintptr_t)in | (uintptr_t)out) & 15))
+    return NOISE_EINVAL;
+  const long chunks = (long)N * K / 8;
+  hipLaunchKernelGGL(weight_tiles_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, in, ld, K,
+                     chunks, out);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
 int lowrank_gemm_parts(int N) {
   if (N <= 0 || N % 128) return 0;
   return use_big(N) ? N / cfg_wave_n<CFG_BIG>() : N / cfg_wave_n<CFG_SMALL>();
@@ -538,8 +575,9 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     return NOISE_EINVAL;
   if (g.out_tiled && (epi != EPI_RELU2 || g.M % 16 || g.ldo % 32)) return NOISE_EINVAL;
   if (epi == EPI_DENSE) {
-    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.out_bf16 || g.lda % 8 || g.ldw % 8 ||
-        g.a_mstride % 8 || g.lda < g.K || g.ldw < g.K || g.ldo % 8 || g.ldo < g.N || g.N % 128 || g.K % 64 ||
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.out_bf16 || g.lda % 8 ||
+        (!g.w_tiled && (g.ldw % 8 || g.ldw < g.K)) || g.a_mstride % 8 || g.lda < g.K || g.ldo % 8 || g.ldo < g.N ||
+        g.N % 128 || g.K % 64 ||
         (((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15))
       return NOISE_EINVAL;
     // K = 512 (the attention c_proj): the weight-resident kernel streams x once per 256 output columns
@@ -549,7 +587,8 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
   if (g.a_fold && (epi != EPI_CE || g.a_tiled || g.a_fold < 0 || g.a_fold % 64 || g.a_fold >= g.K))
     return NOISE_EINVAL;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
-      g.u_ld < 1 || g.lda % 8 || g.ldw % 8 || g.a_mstride % 8 || g.lda < g.K - g.a_fold || g.ldw < g.K ||
+      g.u_ld < 1 || g.lda % 8 || (!g.w_tiled && (g.ldw % 8 || g.ldw < g.K)) || g.a_mstride % 8 ||
+      g.lda < g.K - g.a_fold ||
       g.pair_shift < 0 || g.pair_shift > 1 || g.ra_ld % 4 || g.ldo % 8 || g.N % 128 || g.K % 64 ||
       g.seg_n <= 0 || g.seg_n % 128 || g.N % g.seg_n || g.seg0 < 0 || g.seg0 + g.N / g.seg_n > 3 || g.u_qstride < 1)
     return NOISE_EINVAL;

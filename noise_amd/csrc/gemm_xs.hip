@@ -163,9 +163,12 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int lcol = 8 * (r >> 2) + 4 * j + (r & 3);
-      const bf16* wp = g.W + (long)(QK ? qk_col(nslice, wave, lcol) : fw + lcol) * g.ldw + 128 * grp;
+      const long n = QK ? qk_col(nslice, wave, lcol) : fw + lcol;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) wr[j][s] = *reinterpret_cast<const bf16x8*>(wp + 8 * s);
+      for (int s = 0; s < KS; ++s) {
+        const long k = 128 * grp + 8 * s;  // 8 columns of one 16-byte chunk, in either layout
+        wr[j][s] = *reinterpret_cast<const bf16x8*>(g.W + (g.w_tiled ? wtile_offset(n, k, KD) : n * g.ldw + k));
+      }
     }
   }
   // the resident fragments have landed before any LDS-bound load is issued, so no wait below covers them
@@ -630,7 +633,8 @@ int xs_relu2_parts(int N) { return (N > 0 && N % BN == 0) ? N / BN : 0; }
 namespace {
 bool xs_shape_ok(const LowrankGemmArgs& g) {
   return g.K == KD && g.N % BN == 0 && g.N > 0 && g.M % R == 0 && g.T % R == 0 && !g.a_tiled && g.lda % 8 == 0 &&
-         g.ldw % 8 == 0 && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.lda >= g.K && g.ldw >= g.K && g.ldo >= g.N &&
+         (g.w_tiled || (g.ldw % 8 == 0 && g.ldw >= g.K)) && g.a_mstride % 8 == 0 && g.ldo % 8 == 0 && g.lda >= g.K &&
+         g.ldo >= g.N &&
          g.A && g.W && g.out_bf16 && !(((uintptr_t)g.A | (uintptr_t)g.W | (uintptr_t)g.out_bf16) & 15);
 }
 template <int MODE>

@@ -34,8 +34,9 @@ def _need_cuda(t, dtype, name):
 
 class Weights:
     """Per-step device copies of the shared weights in the kernels' formats: bf16 GEMM operands (the
-    autocast cast the reference performs inside every matmul, done once per step) and the fp32-head
-    split operand. Built from `p` = name -> fp32 parameter (train/val/eggroll.py:113)."""
+    autocast cast the reference performs inside every matmul, done once per step; the MLP c_proj weight in
+    the tile GEMM's WTILE layout) and the fp32-head split operand. Built from `p` = name -> fp32 parameter
+    (train/val/eggroll.py:113)."""
 
     def __init__(self, p, config=None, head='fp32'):
         if head not in HEAD_MODES:
@@ -50,13 +51,16 @@ class Weights:
         self.proj = torch.empty(L, D, D, device=dev, dtype=torch.bfloat16)
         self.fc = torch.empty(L, F, D, device=dev, dtype=torch.bfloat16)
         self.mproj = torch.empty(L, D, F, device=dev, dtype=torch.bfloat16)
+        # the MLP c_proj weight (K = 2048, the tile GEMM's operand) is kept in the library's WTILE layout
+        rows = torch.empty(D, F, device=dev, dtype=torch.bfloat16)
         for i in range(L):
             pre = f'transformer.h.{i}.'
             for k, name in enumerate(('attn.c_q.weight', 'attn.c_k.weight', 'attn.c_v.weight')):
                 self._cast(p[pre + name], self.qkv[i, k * D:(k + 1) * D], s)
             self._cast(p[pre + 'attn.c_proj.weight'], self.proj[i], s)
             self._cast(p[pre + 'mlp.c_fc.weight'], self.fc[i], s)
-            self._cast(p[pre + 'mlp.c_proj.weight'], self.mproj[i], s)
+            self._cast(p[pre + 'mlp.c_proj.weight'], rows, s)
+            _lib.call('noise_weight_tiles', rows.data_ptr(), D, F, self.mproj[i].data_ptr(), s)
         w_head = p['lm_head.weight']
         V = w_head.shape[0]
         if head == 'fp32':
@@ -225,7 +229,8 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
                   _p(buf.y), _p(buf.u_attn), 0, 0, 0, s)
         tm.close(t0)
         t0 = tm.mark('attn_proj')
-        _lib.call('noise_dense_bf16', _p(buf.y), _lib.LAYOUT_ROWS, D, D, _p(W.proj[i]), m, T, _p(buf.y_ap), s)
+        _lib.call('noise_dense_bf16', _p(buf.y), _lib.LAYOUT_ROWS, D, D, _p(W.proj[i]), _lib.LAYOUT_ROWS, m, T,
+                  _p(buf.y_ap), s)
         tm.close(t0)
         attn_out = (_p(buf.y_ap), _p(buf.u_attn), H, H, 1, _p(ap))
         af, bf_ = noise[pre + 'mlp.c_fc.weight']
@@ -238,7 +243,8 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
         # the hidden stays in the library's TILE16 layout between the two MLP GEMMs
         _lib.call('noise_mlp_fc', _p(buf.h), _p(W.fc[i]), D, F, _p(af), _p(buf.u_fc), _p(bm), _p(sign), m, T, ps,
                   _p(buf.hidden), _lib.LAYOUT_TILE16, _p(buf.u_mlp), s)
-        _lib.call('noise_dense_bf16', _p(buf.hidden), _lib.LAYOUT_TILE16, F, D, _p(W.mproj[i]), m, T, _p(buf.y_mp), s)
+        _lib.call('noise_dense_bf16', _p(buf.hidden), _lib.LAYOUT_TILE16, F, D, _p(W.mproj[i]), _lib.LAYOUT_WTILE, m,
+                  T, _p(buf.y_mp), s)
         tm.close(t0)
         # the fc partials are part-major with stride m * T (this chunk's rows)
         mlp_out = (_p(buf.y_mp), _p(buf.u_mlp), buf.parts, 1, m * T, _p(am))

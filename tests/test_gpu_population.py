@@ -19,7 +19,7 @@ from noise_amd.model import make_model
 from noise_amd.synthetic import antithetic_signs, population_noise, trained_like, zipf_tokens
 from oracle import eggroll as oe
 from oracle import model as om
-from tests._util import log_case, rel_err, tile16_index
+from tests._util import log_case, rel_err, tile16_index, wtile_index
 
 pytestmark = pytest.mark.gpu
 DEV = 'cuda'
@@ -337,7 +337,8 @@ def test_deferred_residuals_match_eager_lowrank():
 
 def test_mlp_hidden_tile16_matches_rows():
     """noise_mlp_fc writes the same hidden (bit for bit, up to the layout) and the same partials in TILE16 as in
-    ROWS, and noise_dense_bf16 on the TILE16 hidden returns exactly its result on the row-major one."""
+    ROWS, and noise_dense_bf16 on the TILE16 hidden returns exactly its result on the row-major one, with the
+    weight row-major or in the WTILE copy noise_weight_tiles makes (itself checked element by element)."""
     g = torch.Generator().manual_seed(13)
     m, T, D, F = 4, 64, 512, 2048
     M = m * T
@@ -351,31 +352,46 @@ def test_mlp_hidden_tile16_matches_rows():
     log_case(f'mlp hidden TILE16 vs ROWS m={m} T={T}')
     s = torch.cuda.current_stream().cuda_stream
     parts = _lib.value('noise_mlp_fc_parts', F)
+    wt = torch.empty_like(d['wpj'])
+    _lib.call('noise_weight_tiles', d['wpj'].data_ptr(), D, F, wt.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert torch.equal(wt.cpu().flatten()[wtile_index(D, F)], wpj)
     out = {}
     for layout in (_lib.LAYOUT_ROWS, _lib.LAYOUT_TILE16):
         hid = torch.empty(M, F, device=DEV, dtype=torch.bfloat16)
         up = torch.empty(parts, M, device=DEV)
         _lib.call('noise_mlp_fc', d['h'].data_ptr(), d['wfc'].data_ptr(), D, F, d['afc'].data_ptr(), d['u'].data_ptr(),
                   d['bpj'].data_ptr(), d['sign'].data_ptr(), m, T, 1, hid.data_ptr(), layout, up.data_ptr(), s)
-        y = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
-        _lib.call('noise_dense_bf16', hid.data_ptr(), layout, F, D, d['wpj'].data_ptr(), m, T, y.data_ptr(), s)
+        ys = []
+        for wl, w in ((_lib.LAYOUT_ROWS, d['wpj']), (_lib.LAYOUT_WTILE, wt)):
+            y = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+            _lib.call('noise_dense_bf16', hid.data_ptr(), layout, F, D, w.data_ptr(), wl, m, T, y.data_ptr(), s)
+            ys.append(y)
         torch.cuda.synchronize()
-        out[layout] = (hid.cpu(), up.cpu(), y.cpu())
-    rows_h, rows_u, rows_y = out[_lib.LAYOUT_ROWS]
-    tile_h, tile_u, tile_y = out[_lib.LAYOUT_TILE16]
+        out[layout] = (hid.cpu(), up.cpu(), ys[0].cpu(), ys[1].cpu())
+    rows_h, rows_u, rows_y, rows_yw = out[_lib.LAYOUT_ROWS]
+    tile_h, tile_u, tile_y, tile_yw = out[_lib.LAYOUT_TILE16]
     assert torch.equal(tile_h.flatten()[tile16_index(M, F)], rows_h)
     assert torch.equal(tile_u, rows_u)
     assert torch.equal(tile_y, rows_y)
+    assert torch.equal(rows_yw, rows_y)
+    assert torch.equal(tile_yw, rows_y)
     # and the dense product itself: bf16(hidden W^T) with fp32 accumulation
     ref = (rows_h.float() @ wpj.float().t()).bfloat16().float()
     assert rel_err(rows_y.float(), ref) < 5e-3
     # K = 512 (the attention c_proj shape: the weight-resident kernel) against the same reference
     log_case(f'dense K=512 m={m} T={T}')
     wap = (torch.randn(D, D, generator=g) * D ** -0.5).bfloat16()
-    ya = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_dense_bf16', d['h'].data_ptr(), _lib.LAYOUT_ROWS, D, D, wap.to(DEV).data_ptr(), m, T,
+    wapd = wap.to(DEV)
+    wapt = torch.empty_like(wapd)
+    _lib.call('noise_weight_tiles', wapd.data_ptr(), D, D, wapt.data_ptr(), s)
+    ya, yat = (torch.empty(M, D, device=DEV, dtype=torch.bfloat16) for _ in range(2))
+    _lib.call('noise_dense_bf16', d['h'].data_ptr(), _lib.LAYOUT_ROWS, D, D, wapd.data_ptr(), _lib.LAYOUT_ROWS, m, T,
               ya.data_ptr(), s)
+    _lib.call('noise_dense_bf16', d['h'].data_ptr(), _lib.LAYOUT_ROWS, D, D, wapt.data_ptr(), _lib.LAYOUT_WTILE, m, T,
+              yat.data_ptr(), s)
     torch.cuda.synchronize()
+    assert torch.equal(yat.cpu(), ya.cpu())
     refa = (h.float() @ wap.float().t()).bfloat16().float()
     assert rel_err(ya.cpu().float(), refa) < 5e-3
     # one bf16 ulp at most: only the fp32 summation order differs
@@ -456,12 +472,12 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
             assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
 
 
-@pytest.mark.parametrize('fp32', [1, 0])
-def test_head_ce_other_vocab_and_partial_row_tile(fp32):
-    """A 768-entry vocabulary (3 column tiles, 12 CE partials per row) and a token count (96) that leaves the
-    last 256-row tile partial."""
+@pytest.mark.parametrize('fp32,T', [(1, 96), (0, 96), (1, 90), (0, 90)])
+def test_head_ce_other_vocab_and_partial_row_tile(fp32, T):
+    """A 768-entry vocabulary (3 column tiles, 12 CE partials per row) and token counts that leave the last
+    256-row tile partial: 96 (the normalised operand in TILE16) and 90 (not a multiple of 16: row-major)."""
     g = torch.Generator().manual_seed(14)
-    m, T, V = 4, 96, 768
+    m, V = 4, 768
     x = torch.randn(m * T, 512, generator=g) * 3
     W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2
     a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
