@@ -90,6 +90,14 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_head_ce_workspace_size(2, 256, 640, 1, ctypes.byref(ctypes.c_size_t(0))) == EINVAL
     assert lib.noise_head_ce(1, 0, None, 1, 640, 1, 1, 1, 1, 1, 0, 1, 256, 0, 0, 1, None, 1, 1 << 40, None, 0,
                              None) == EINVAL
+    # WTILE copies need rows % 64 == 0, cols % 32 == 0 and 16-byte aligned pointers; the dense product knows the
+    # ROWS and WTILE weight layouts only
+    assert lib.noise_weight_tiles(16, 96, 512, 16, None) == EINVAL
+    assert lib.noise_weight_tiles(16, 128, 48, 16, None) == EINVAL
+    assert lib.noise_weight_tiles(8, 128, 512, 16, None) == EINVAL
+    assert lib.noise_weight_tiles(None, 128, 512, 16, None) == EINVAL
+    assert lib.noise_dense_bf16(16, 0, 2048, 512, 16, 3, 1, 256, 16, None) == EINVAL
+    assert lib.noise_dense_bf16(16, 2, 2048, 512, 16, 0, 1, 256, 16, None) == EINVAL  # WTILE is not an x layout
     assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
     assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
     ptr, count, _keep = _lib.gather_params([(1, 1, None, 8, 4)])   # b null with in > 0
