@@ -344,7 +344,9 @@ int noise_attention_noalloc(const void* qkv, int members, int T, int window, int
 int noise_lowrank_resid(const void* x, const void* w, int in, int out, const float* a, const float* u, int u_parts,
                         long u_row_stride, long u_part_stride, const float* sign, int members, int T, int pair_shift,
                         float* resid, noise_stream_t stream) {
-  if (bad_members(members, T, pair_shift) || u_parts <= 0 || u_row_stride < 1 || u_part_stride < 1) return NOISE_EINVAL;
+  if (bad_members(members, T, pair_shift) || u_parts <= 0 || u_row_stride < 1 || u_row_stride > 0x7fffffffL ||
+      u_part_stride < 1)
+    return NOISE_EINVAL;
   LowrankGemmArgs g = base_args(x, in, (long)T * in, w, in, out, a, sign, members, T, pair_shift);
   g.u = u;
   g.u_parts = u_parts;

@@ -98,6 +98,8 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_weight_tiles(None, 128, 512, 16, None) == EINVAL
     assert lib.noise_dense_bf16(16, 0, 2048, 512, 16, 3, 1, 256, 16, None) == EINVAL
     assert lib.noise_dense_bf16(16, 2, 2048, 512, 16, 0, 1, 256, 16, None) == EINVAL  # WTILE is not an x layout
+    # a partial-sum row stride beyond the kernels' 32-bit field
+    assert lib.noise_lowrank_resid(16, 16, 512, 512, 16, 16, 1, 1 << 33, 1, 16, 2, 256, 1, 16, None) == EINVAL
     assert lib.noise_embed_norm(None, 4096, None, None, None, None, 1, 16, 0, None, None) == EINVAL
     assert lib.noise_outer_update(None, 8, 1, 8, 1, 4, 2, 8, 1.0, 1, None) == EINVAL  # a null needs out == 1
     ptr, count, _keep = _lib.gather_params([(1, 1, None, 8, 4)])   # b null with in > 0
