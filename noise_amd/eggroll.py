@@ -25,6 +25,17 @@ NOISE = 2 ** 28
 FITNESS = {'zscore': _lib.FITNESS_ZSCORE, 'rank': _lib.FITNESS_RANK}
 
 
+def gather_losses(losses, world):
+    """Every member's loss in member order, from each rank's contiguous share (rank r evaluates members
+    r * per_rank .. (r + 1) * per_rank - 1): the `all_gather` of train/val/eggroll.py:147-150. One rank: the
+    losses themselves."""
+    if world == 1:
+        return losses
+    gathered = [torch.empty_like(losses) for _ in range(world)]
+    torch.distributed.all_gather(gathered, losses)
+    return torch.cat(gathered)
+
+
 def member_sequences(lo, hi, per_seq, chunk_pairs=CHUNK, device=None):
     """Sequence index of members lo .. hi - 1. The reference walks a rank's members in chunks of 2 * CHUNK and
     evaluates each whole chunk on sequence start // per_seq (train/val/eggroll.py:139-145): when per_seq is not a
@@ -122,10 +133,7 @@ class Eggroll:
             losses[c0 - lo:c1 - lo] = self.pop.loss(self.params, noise, sign[:c1 - c0], seq_x, seq_y, pair_shift=1,
                                                     weights=weights)
             del noise
-        if self.world > 1:
-            gathered = [torch.empty_like(losses) for _ in range(self.world)]
-            torch.distributed.all_gather(gathered, losses)
-            losses = torch.cat(gathered)
+        losses = gather_losses(losses, self.world)
         self.last_losses = losses
         nfit = len(losses) // 2
         fit = torch.empty(nfit, device=self.device)

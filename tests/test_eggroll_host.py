@@ -1,8 +1,11 @@
 """Host-side bookkeeping of noise_amd.eggroll against the oracle's restatement of the reference's loop (CPU)."""
+import socket
+
 import pytest
 import torch
+import torch.multiprocessing as mp
 
-from noise_amd.eggroll import member_sequences
+from noise_amd.eggroll import gather_losses, member_sequences
 from oracle import eggroll as oe
 
 
@@ -19,3 +22,35 @@ def test_member_sequences_follow_the_reference_chunks(pairs, batch, chunk, world
         # any split of the rank's members into kernel passes sees the same mapping
         for c0 in range(lo, hi, 6):
             assert torch.equal(member_sequences(c0, min(hi, c0 + 6), per_seq, chunk), want[c0:min(hi, c0 + 6)])
+
+
+def _gather_rank(rank, world, port, per_rank, out):
+    torch.distributed.init_process_group('gloo', init_method=f'tcp://127.0.0.1:{port}', rank=rank,
+                                         world_size=world)
+    try:
+        # rank r's share: the losses of members r * per_rank .. (r + 1) * per_rank - 1 (CPU tensors on gloo)
+        share = torch.arange(rank * per_rank, (rank + 1) * per_rank, dtype=torch.float32) * 0.5 + 3.0
+        got = gather_losses(share, world)
+        out[rank] = got.tolist()
+    finally:
+        torch.distributed.destroy_process_group()
+
+
+@pytest.mark.parametrize('world', [2, 3])
+def test_gather_losses_puts_every_rank_share_in_member_order(world):
+    """The multi-rank loss gather (train/val/eggroll.py:147-150) on gloo with CPU tensors, one process per rank:
+    every rank ends with the whole population in member order, so the fitness and update it rebuilds are the same
+    on every rank and equal to the one-rank run."""
+    with socket.socket() as s:
+        s.bind(('127.0.0.1', 0))
+        port = s.getsockname()[1]
+    per_rank = 6
+    out = mp.Manager().dict()
+    mp.spawn(_gather_rank, args=(world, port, per_rank, out), nprocs=world, join=True)
+    want = (torch.arange(world * per_rank, dtype=torch.float32) * 0.5 + 3.0).tolist()
+    for rank in range(world):
+        assert out[rank] == want, rank
+    # one rank: the losses themselves
+    one = torch.arange(4.0)
+    assert gather_losses(one, 1) is one
+
