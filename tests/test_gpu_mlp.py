@@ -117,6 +117,33 @@ def test_lowrank_linear_narrow_tiles(dout):
     assert (y.cpu() - ref).abs().max() < 2e-2
 
 
+@pytest.mark.parametrize('dout,din', [(384, 2048), (640, 1024)])
+def test_dense_wtile_weight_on_narrow_tiles(dout, din):
+    """The dense c_proj product with a WTILE weight on the 256 x 128 tile configuration (output widths a multiple of
+    128, not of 256) returns exactly the row-major weight's result, and bf16(x W^T) within one bf16 step."""
+    from noise_amd import _lib
+    g = torch.Generator().manual_seed(8)
+    P, T = 2, 128
+    M = P * T
+    log_case(f'dense WTILE narrow tiles M={M} {din}->{dout}')
+    x = torch.randn(M, din, generator=g).bfloat16()
+    w = (torch.randn(dout, din, generator=g) * din ** -0.5).bfloat16()
+    xd, wd = x.to(DEV), w.to(DEV)
+    wt = torch.empty_like(wd)
+    s = torch.cuda.current_stream().cuda_stream
+    _lib.call('noise_weight_tiles', wd.data_ptr(), dout, din, wt.data_ptr(), s)
+    ys = []
+    for layout, ww in ((_lib.LAYOUT_ROWS, wd), (_lib.LAYOUT_WTILE, wt)):
+        y = torch.empty(M, dout, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_dense_bf16', xd.data_ptr(), _lib.LAYOUT_ROWS, din, dout, ww.data_ptr(), layout, P, T,
+                  y.data_ptr(), s)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[1].cpu(), ys[0].cpu())
+    ref = (x.float() @ w.float().t()).bfloat16().float()
+    assert ((ys[0].cpu().float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6).all()
+
+
 def test_mlp_config1_full_size_sampled_members():
     """Config 1 at its real shape (P = 256, T = 2048, shared x); three members checked in full."""
     from noise_amd import ops
