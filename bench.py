@@ -119,7 +119,7 @@ def run_step(args):
     pairs = args.pairs
     P = 2 * pairs
     model = make_model(dev, 0)
-    es = Eggroll(model, pairs, chunk=args.chunk, head='fp32', fitness=args.fitness, sigma=SIGMA)
+    es = Eggroll(model, pairs, chunk=args.chunk, head=args.head, fitness=args.fitness, sigma=SIGMA)
     opt = Adam(model.parameters(), lr=LR, betas=BETAS, eps=1e-8)
     idx, tgt = zipf_tokens(T, seed=1)
     x, y = idx[None].to(dev), tgt[None].to(dev)
@@ -158,7 +158,8 @@ def run_step(args):
         'dtype': 'bf16',
         'data': 'synthetic (Zipf(1.1) tokens, seed-0 reference init, N(0,1) noise buffer)',
         'config': {'workload': 'config4_population_step', 'members': P, 'pairs': pairs, 'tokens': T,
-                   'model': '37.7M GPT (8 x 512, vocab 4096)', 'head': 'fp32 (bf16 hi/lo split on MFMA)',
+                   'model': '37.7M GPT (8 x 512, vocab 4096)',
+                   'head': 'fp32 (bf16 hi/lo split on MFMA)' if args.head == 'fp32' else 'bf16 (autocast rounding)',
                    'sigma': SIGMA, 'fitness': args.fitness, 'optimizer': 'Adam (HIP)', 'chunk_members': args.chunk,
                    'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
@@ -416,6 +417,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--fitness', choices=('rank', 'zscore'), default='rank',
                     help="config 4 names rank-normalised fitness; 'zscore' is the reference's (train/val/eggroll.py:151-152)")
+    ap.add_argument('--head', choices=('fp32', 'bf16'), default='fp32',
+                    help="config 4 names an fp32 head; 'bf16' is the reference's autocast head (train/val/eggroll.py:99 "
+                         "under :144), for comparison")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: every box in this build has a single MI355X; --gpus {args.gpus} '
