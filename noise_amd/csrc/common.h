@@ -26,6 +26,24 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950), the same rounding torch uses.
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 __device__ __forceinline__ float bf16r(float x) { return (float)(bf16)x; }
+// bf16r of two values with one v_cvt_pk_bf16_f32 for the pair, widened back by a shift and a mask. The
+// conversion is issued from inline assembly: from C++ the compiler splits the pair back into one conversion and
+// one shift per value.
+__device__ __forceinline__ void bf16r2(float a, float b, float& ra, float& rb) {
+  unsigned u;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
+  ra = __uint_as_float(u << 16);
+  rb = __uint_as_float(u & 0xffff0000u);
+}
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+// The bf16 pair {bf16(relu(a)^2), bf16(relu(b)^2)} (low half a): a |a| and b |b| rounded as a pair, whose halves
+// with the sign bit set (a < 0, or -0) become +0 by one packed 16-bit integer max with 0. For a > 0, a |a| is the
+// same fp32 product as relu(a)^2; a NaN keeps its sign, so a positive NaN stays NaN (relu propagates NaN).
+__device__ __forceinline__ unsigned relu2_bf16x2(float a, float b) {
+  const bf16x2 p = {to_bf16(a * fabsf(a)), to_bf16(b * fabsf(b))};
+  const s16x2 m = __builtin_elementwise_max(__builtin_bit_cast(s16x2, p), s16x2{0, 0});
+  return __builtin_bit_cast(unsigned, m);
+}
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -371,8 +371,10 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       const int i = st < 6 ? 0 : 1, sub = st - (i ? 6 : 1);
       if (sub < 4) {
         const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
-        float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
-        float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+        float v0, v1;
+        bf16r2(acc[i][j][e0], acc[i][j][e0 + 1], v0, v1);
+        v0 += ev_u[i] * ev_a[c];
+        v1 += ev_u[i] * ev_a[c + 1];
         if constexpr (VE) {
           // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
           v0 += ve_g[i] * ve_x[i][c];
@@ -426,8 +428,9 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       const int i = st < 8 ? 0 : 1, sub = st - (i ? 8 : 3);
       if (sub < 4) {
         const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
-        ev_v[i][c] = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
-        ev_v[i][c + 1] = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
+        bf16r2(acc[i][j][e0], acc[i][j][e0 + 1], ev_v[i][c], ev_v[i][c + 1]);
+        ev_v[i][c] += ev_u[i] * ev_a[c];
+        ev_v[i][c + 1] += ev_u[i] * ev_a[c + 1];
       } else {
         // pair (d, d + 32) = (x1, x2) of elements e, e + 4: [x1 cos + x2 sin, -x1 sin + x2 cos]
         float ss = 0.f;
@@ -480,10 +483,11 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       // columns c, c + 1 of the lane's 8: dense part rounded to bf16 (autocast GEMM output), fp32
       // rank-1 correction, relu^2, bf16
       const int j = sub >> 1, e0 = (sub & 1) * 2, c = 4 * j + e0;
-      const float v0 = bf16r(acc[i][j][e0]) + ev_u[i] * ev_a[c];
-      const float v1 = bf16r(acc[i][j][e0 + 1]) + ev_u[i] * ev_a[c + 1];
-      const float r0 = fmaxf(v0, 0.f), r1 = fmaxf(v1, 0.f);
-      const unsigned h2 = pack_bf16(r0 * r0, r1 * r1);
+      float v0, v1;
+      bf16r2(acc[i][j][e0], acc[i][j][e0 + 1], v0, v1);
+      v0 += ev_u[i] * ev_a[c];
+      v1 += ev_u[i] * ev_a[c + 1];
+      const unsigned h2 = relu2_bf16x2(v0, v1);
       ev_h[i][sub] = h2;
       ev_dot[i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(h2), as_bf16x2(ev_bp[sub]), sub == 0 ? 0.f : ev_dot[i], false);
     } else if (sub == 4) {
