@@ -141,9 +141,12 @@ __device__ __forceinline__ void store_stream_x4(void* p, u32x4 v) {
 // read wait for every outstanding LDS-bound load). The kernels wait for them themselves: vector memory
 // operations complete in issue order.
 typedef __attribute__((address_space(3))) void lds_void_t;
+// The LDS byte offset of a generic pointer into __shared__ memory: the low 32 bits of its flat address (the shared
+// aperture's base is 4 GiB aligned). A cast to the LDS address space would add a null-pointer check on every use.
+__device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned)(uintptr_t)p; }
 // global_load_lds_dword{x4}: each active lane's bytes land at lds + size * lane. M0 is saved and restored.
 __device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   unsigned saved;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                : "=&s"(saved)
@@ -153,7 +156,7 @@ __device__ __forceinline__ void dma_x4(const void* src, const void* lds) {
 // The same load from a wave-uniform base (SGPR pair) plus a per-lane 32-bit byte offset: the address arithmetic
 // stays on the scalar unit and the offset VGPR is computed once.
 __device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   unsigned saved;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
                : "=&s"(saved)
@@ -161,7 +164,7 @@ __device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const 
                : "memory");
 }
 __device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
-  const unsigned off = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void_t*)lds);
+  const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   unsigned saved;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
                : "=&s"(saved)

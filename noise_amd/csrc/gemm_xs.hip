@@ -38,6 +38,7 @@
 // row are summed in LDS (fixed order) by wave 0, which stores one partial per (slice, row): upart_out is
 // part-major [N / 256][M], 128 contiguous bytes per block.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "gemm.h"
@@ -518,8 +519,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 
   // One iteration: wait for block k, MFMAs of block k into acc, interleaved step by step with the epilogue
   // of block k - 1 (epi) and the partial sums of block k - 2 (sum); then the loads of block k + NB - 1
-  // into the slot block k - 1 used.
-  auto iter = [&](f32x4 (&acc)[2][2], const f32x4 (&prev)[2][2], int k, bool epi, bool sum) {
+  // into the slot block k - 1 used. A steady iteration (`steady`) is one with FIRST_STORE + 2 <= k <= nb - NB:
+  // the previous iterations' stores and the later blocks' loads are all outstanding, so its waits, the sums and
+  // the refill need no run-time case analysis (a cascade of scalar compares and branches otherwise). The q|k
+  // and value-embedding modes keep the general form only: with a second copy of the loop hipcc spills their
+  // registers to scratch.
+  auto iter = [&](f32x4 (&acc)[2][2], const f32x4 (&prev)[2][2], int k, bool epi, bool sum, auto steady) {
+    constexpr bool ST = decltype(steady)::value;
     // stores are issued in iterations j >= FIRST_STORE (q|k stores block j - 2's rows, the others block j - 1's)
     if constexpr (VE) {
       // Block k has landed once the operations issued after its loads are the only ones outstanding: in
@@ -534,6 +540,8 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       } else {
         if (xn) wait_vm_lgkm0<2 + E + D>(); else wait_vm_lgkm0<2 + E>();
       }
+    } else if constexpr (ST) {
+      wait_vm_lgkm0<(NB - 2) * DMA_PER_BLOCK<MODE> + 2 * STORES_PER_EPI>();
     } else {
       wait_block(min(NB - 2, nb - 1 - k), min(2, max(0, k - FIRST_STORE)));
     }
@@ -576,12 +584,15 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         }
       }
       if constexpr (MODE == XS_RELU2) {
-        if (s == 13 && sum) sum_partials(k - 2);
+        if (s == 13 && (ST || sum)) sum_partials(k - 2);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (k + NB - 1 < nb) issue(k + NB - 1);
+    if (ST || k + NB - 1 < nb) issue(k + NB - 1);
   };
+  constexpr std::true_type steady{};
+  constexpr std::false_type general{};
+  constexpr bool STEADY_LOOP = !QK && !VE;
 
   if constexpr (VE) {
     // block 0's embedding gather goes out before the ring's loads, from token ids read straight from memory
@@ -595,16 +606,23 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   for (int k = 0; k < NB - 1; ++k)
     if (k < nb) issue(k);
 
-  iter(accA, accB, 0, false, false);
+  iter(accA, accB, 0, false, false, general);
   int k = 1;
   for (; k + 1 < nb; k += 2) {
-    iter(accB, accA, k, true, k >= 2);
-    iter(accA, accB, k + 1, true, true);
+    if (STEADY_LOOP && k >= FIRST_STORE + 2 && k + 1 <= nb - NB) {
+      if constexpr (STEADY_LOOP) {
+        iter(accB, accA, k, true, true, steady);
+        iter(accA, accB, k + 1, true, true, steady);
+      }
+    } else {
+      iter(accB, accA, k, true, k >= 2, general);
+      iter(accA, accB, k + 1, true, true, general);
+    }
   }
   // tail: the last block's epilogue; partial sums of the last two blocks, each after a barrier
   int last = k - 1;
   if (k < nb) {
-    iter(accB, accA, k, true, k >= 2);
+    iter(accB, accA, k, true, k >= 2, general);
     last = k;
   }
   wait_vm_lgkm0<0>();
