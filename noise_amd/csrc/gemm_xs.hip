@@ -180,21 +180,42 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // ---- loads of block k into ring slot k % NB. Wave w fills x rows 4 w + q: lane L loads k 8 L .. 8 L + 7.
   // Lanes 0-7 load a_p, 8-15 b_next over the wave's 32 columns, 16-23 the block's 32 input-side dots; lane 0
   // the member's sign.
-  // Blocks are issued in order k = 0, 1, 2, ...: the next one's first row, member and token advance by
-  // streams * R rows per call (no integer division per block).
+  // Blocks are issued in order k = 0, 1, 2, ...: the next one's first row, member and token, its x rows and
+  // (relu^2) the lane's vector source advance by streams * R rows per call, with no integer division or 64-bit
+  // multiply per block; the vector source is recomputed only when the block starts a new member.
   int nx_row = blk_of(0) * R;
   int nx_p = nx_row / g.T, nx_t0 = nx_row - nx_p * g.T;
   const int step_rows = streams * R;
   const unsigned lane16 = 16u * lane;  // the lane's byte offset in a 1 KiB row load
+  const bf16* nx_x = g.A + (long)nx_p * g.a_mstride + (long)(nx_t0 + 4 * wave) * g.lda;
+  const long x_step = (long)step_rows * g.lda, x_wrap = g.a_mstride - (long)g.T * g.lda;
+  // relu^2: lanes 0-7 load a_p, 8-15 b_next (the wave's 32 columns of direction p >> pair_shift), 16-23 the
+  // block's 32 input-side dots (rows row0 ..)
+  auto vsrc_at = [&](int p, int row0) -> const float* {
+    const int dir = p >> g.pair_shift;
+    return lane < 8    ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
+           : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
+                       : g.u + row0 + 4 * (lane - 16);
+  };
+  const float* nx_v = MODE == XS_RELU2 ? vsrc_at(nx_p, nx_row) : nullptr;
+  const int v_step = lane >= 16 ? step_rows : 0;
   auto issue = [&](int k) {
     const int buf = k % NB, row0 = nx_row, p = nx_p, t0 = nx_t0, dir = p >> g.pair_shift;
+    const char* xb = reinterpret_cast<const char*>(nx_x);
+    const float* vsrc = nx_v;
     nx_row += step_rows;
     nx_t0 += step_rows;
-    while (nx_t0 >= g.T) {
-      nx_t0 -= g.T;
-      ++nx_p;
+    nx_x += x_step;
+    if (nx_t0 >= g.T) {
+      do {
+        nx_t0 -= g.T;
+        ++nx_p;
+        nx_x += x_wrap;
+      } while (nx_t0 >= g.T);
+      if constexpr (MODE == XS_RELU2) nx_v = vsrc_at(nx_p, nx_row);
+    } else if constexpr (MODE == XS_RELU2) {
+      nx_v += v_step;
     }
-    const char* xb = reinterpret_cast<const char*>(g.A + (long)p * g.a_mstride + (long)(t0 + 4 * wave) * g.lda);
     char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_x4_s(xb + (long)q * g.lda * 2, lane16, xsl + q * XROW);
@@ -240,9 +261,6 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       }
       return;
     }
-    const float* vsrc = lane < 8 ? g.ra[0] + (long)dir * g.ra_ld + fw + 4 * lane
-                        : lane < 16 ? g.rb_next + (long)dir * g.rb_next_ld + fw + 4 * (lane - 8)
-                                    : g.u + row0 + 4 * (lane - 16);
     if constexpr (MODE == XS_RELU2) {
       if (lane < 24) dma_x4(vsrc, &svec[buf][wave][0]);
       if (lane == 0) dma_x1(g.sign + p, &svec[buf][wave][SIGN_OFF]);
@@ -327,7 +345,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
 
   // TILE16 (c_fc h): the half's 1 KiB tile of the wave's 32 columns, 16-byte unit 4 r + (grp ^ ((r / 2) % 4))
   const unsigned tile_off = 16u * (unsigned)(4 * (lane & 15) + (grp ^ (((lane & 15) >> 1) & 3)));
-  auto half_base = [&](int blk, int i) { return g.out_bf16 + ((long)blk * R + 16 * i) * g.ldo + col0; };
+  // the block's first output row at the wave's first column; row half i adds 16 i rows (one base per block for
+  // both halves' stores)
+  auto blk_base = [&](int blk) { return g.out_bf16 + (long)blk * (R * g.ldo) + col0; };
+  auto half_base = [&](int blk, int i) { return blk_base(blk) + 16 * i * g.ldo; };
+  // relu^2 h, the lane's byte offset from half_base: row-major (st_off) or TILE16 (tile_off into the wave's 1 KiB
+  // tile of each 16-row half, which starts (fw / 32) * 512 elements into the half's first row)
+  const unsigned h_lane = g.out_tiled ? tile_off + 2u * (unsigned)((fw >> 5) * 512 - col0) : st_off;
   auto store_half = [&](int blk, int i, u32x4 v) {
     *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(half_base(blk, i)) + st_off) = v;
   };
@@ -495,10 +519,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       // row-major: 16 rows x 64 bytes per instruction; TILE16: one contiguous 1 KiB tile (16 rows, the
       // wave's 32 columns), eight whole 128-byte lines
       const u32x4 hv = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
-      if (g.out_tiled)
-        store_stream_x4_s(g.out_bf16 + ((long)blk_of(pk) * R + 16 * i) * g.ldo + (fw >> 5) * 512, tile_off, hv);
-      else
-        store_stream_x4_s(half_base(blk_of(pk), i), st_off, hv);
+      store_stream_x4_s(half_base(blk_of(pk), i), h_lane, hv);
       const f32pair a = rowpair16(ev_dot[i]);  // rows 0 + 1 and 2 + 3 of the 16-lane rows
       ev_dot[i] = a.lo + a.hi;
     } else {
@@ -508,12 +529,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
     }
   };
   // wave 0: the 8 wave partials of block pk's rows (written before the last barrier) -> one partial per row
+  float* const up_lane = g.upart_out + (long)nslice * g.M + (long)blk_of(0) * R + lane;
   auto sum_partials = [&](int pk) {
     if (wave == 0 && lane < R) {
       const float4 p0 = *reinterpret_cast<const float4*>(&red[pk & 1][lane][0]);
       const float4 p1 = *reinterpret_cast<const float4*>(&red[pk & 1][lane][4]);
       const float s = ((((((p0.x + p0.y) + p0.z) + p0.w) + p1.x) + p1.y) + p1.z) + p1.w;
-      g.upart_out[(long)nslice * g.M + (long)blk_of(pk) * R + lane] = s;
+      up_lane[pk * step_rows] = s;
     }
   };
 
