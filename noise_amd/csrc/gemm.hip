@@ -36,6 +36,8 @@
 // while the next tile's operands land.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "common.h"
 #include "gemm.h"
 
@@ -128,6 +130,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   __shared__ float ep_u[C::UGROUPS][BM];                               // partial sums of x.b per row
   __shared__ float ep_sign;
 
+  // (a wave index made uniform with readfirstlane measured slower here: config 1 2.20 -> 2.50 ms, head +6%)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = g.N / BN, ntiles = tiles_m * tiles_n;
@@ -169,13 +172,18 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       b_src[d] = g.W + (long)n * g.ldw + c * 8;
     }
   };
+  // elements one stage advances the A and W sources by: BK columns, or one 512-element block per 32 columns for
+  // a TILE16 A and a WTILE W (both require BK = 32)
+  const int a_step = g.a_tiled ? 16 * BK : BK, w_step = g.w_tiled ? 512 : BK;
   auto issue = [&](int kt, int buf) {
     bf16* sx = smem + buf * C::STAGE;
     bf16* sw = sx + BM * BK;
-    // A column of this stage (a_fold: the contraction index k >= a_fold reads column k - a_fold); a TILE16 A
-    // and a WTILE W hold one 512-element block per 32 columns
-    const int k0 = kt * BK, kc = g.a_fold && k0 >= g.a_fold ? k0 - g.a_fold : k0;
-    const long ka = g.a_tiled ? (long)kc * 16 : kc, kw = g.w_tiled ? (long)kt * 512 : k0;
+    // A stage of this k stage (a_fold, the head only: the contraction index k >= a_fold reads column k - a_fold)
+    int ks = kt;
+    if constexpr (EPI == EPI_CE) {
+      if (g.a_fold && kt * BK >= g.a_fold) ks -= g.a_fold / BK;
+    }
+    const long ka = ks * a_step, kw = kt * w_step;
 #pragma unroll
     for (int d = 0; d < C::LA; ++d)
       __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
@@ -230,18 +238,29 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // Make step t's stage readable: when t opens a new stage, wait for its DMA, barrier, and refill the
   // stage retired by the previous step. Before the wait for stage kt, the stages issued are
   // 0 .. STAGES-1 (prologue) and kt-2+STAGES at most (refills of the earlier opens), so
-  // min(KT-1, max(STAGES-1, kt-2+STAGES)) - kt later stages may stay in flight.
-  auto open = [&](int t) {
+  // min(KT-1, max(STAGES-1, kt-2+STAGES)) - kt later stages may stay in flight. A steady open (`steady`,
+  // 1 <= kt <= KT - STAGES) has STAGES - 2 later stages in flight and refills, both known at compile time (the
+  // general form selects its s_waitcnt through scalar compares and branches).
+  auto open = [&](int t, auto steady) {
+    constexpr bool ST = decltype(steady)::value;
     if (t % SUB == 0) {
       const int kt = t / SUB;
-      wait_stage<C::L, STAGES - 1>(min(KT - 1, max(STAGES - 1, kt - 2 + STAGES)) - kt);
+      if constexpr (ST)
+        wait_vm_lgkm0<(STAGES - 2) * C::L>();
+      else
+        wait_stage<C::L, STAGES - 1>(min(KT - 1, max(STAGES - 1, kt - 2 + STAGES)) - kt);
       __builtin_amdgcn_s_barrier();
-      if (kt >= 1 && kt - 1 + STAGES < KT) issue(kt - 1 + STAGES, (kt - 1) % STAGES);
+      if (ST || (kt >= 1 && kt - 1 + STAGES < KT)) issue(kt - 1 + STAGES, (kt - 1) % STAGES);
     }
   };
+  constexpr std::true_type steady{};
+  constexpr std::false_type general{};
+  // the dense product and the head run their steady steps from a loop of their own; the other epilogues keep
+  // one loop (with a second one, config 1's EPI_STORE product measured 4% slower)
+  constexpr bool STEADY_LOOP = SUB == 1 && (EPI == EPI_DENSE || EPI == EPI_CE);
   // Step t's MFMAs with (wc, xf) while step t + 1's operands are read into (wn_, xf).
-  auto step_read = [&](int t, const bf16x8 (&wc)[FN], bf16x8 (&wn_)[FN]) {
-    open(t + 1);
+  auto step_read = [&](int t, const bf16x8 (&wc)[FN], bf16x8 (&wn_)[FN], auto st) {
+    open(t + 1, st);
     const int buf = ((t + 1) / SUB) % STAGES, kk = (t + 1) % SUB;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -292,17 +311,25 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    open(0);
+    open(0, general);
     read_w(wa, 0, 0);
 #pragma unroll
     for (int i = 0; i < FM; ++i) read_x(xf[i], 0, 0, i);
     // KS is even (K % 64 == 0): pairs of steps alternate the W register sets; the last step reads
     // nothing.
-    for (int t = 0; t < KS - 2; t += 2) {
-      step_read(t, wa, wb);
-      step_read(t + 1, wb, wa);
+    int t = 0;
+    if constexpr (STEADY_LOOP) {
+      // pairs whose two opens (k stages t + 1, t + 2; one step per stage) are both steady
+      for (; t + 2 <= KT - STAGES && t < KS - 2; t += 2) {
+        step_read(t, wa, wb, steady);
+        step_read(t + 1, wb, wa, steady);
+      }
     }
-    step_read(KS - 2, wa, wb);
+    for (; t < KS - 2; t += 2) {
+      step_read(t, wa, wb, general);
+      step_read(t + 1, wb, wa, general);
+    }
+    step_read(KS - 2, wa, wb, general);
     step_last(wb);
 
     // every wave has read the ring for the last time: prefetch the next tile
