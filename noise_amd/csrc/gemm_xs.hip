@@ -352,8 +352,13 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   // relu^2 h, the lane's byte offset from half_base: row-major (st_off) or TILE16 (tile_off into the wave's 1 KiB
   // tile of each 16-row half, which starts (fw / 32) * 512 elements into the half's first row)
   const unsigned h_lane = g.out_tiled ? tile_off + 2u * (unsigned)((fw >> 5) * 512 - col0) : st_off;
-  auto store_half = [&](int blk, int i, u32x4 v) {
-    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(half_base(blk, i)) + st_off) = v;
+  // The epilogues of blocks 0, 1, 2, ... run in order, one per iteration k >= 1 and the last after the loop:
+  // ep_base is the base of the next one (every mode but q|k, which stores a block one iteration later), advanced
+  // by one block of rows after each, with no 64-bit multiply per block.
+  bf16* ep_base = blk_base(blk_of(0));
+  const long ep_step = (long)streams * R * g.ldo;
+  auto store_half = [&](int i, u32x4 v) {
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(ep_base + 16 * i * g.ldo) + st_off) = v;
   };
   // q|k: the lane's dims d0 .. d0 + 3 at st_off, their partners d0 + 32 .. at st_off + 64 bytes
   auto store_half_qk = [&](int blk, int i, u32x4 v) {
@@ -407,7 +412,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         }
         ev_h[i][sub] = pack_f16(v0, v1);
       } else {
-        store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+        store_half(i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       }
       return;
     }
@@ -482,7 +487,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
         const int j = sub >> 1, e0 = (sub & 1) * 2;
         ev_h[i][sub] = pack_bf16(acc[i][j][e0], acc[i][j][e0 + 1]);
       } else {
-        store_half(blk_of(pk), i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
+        store_half(i, u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]});
       }
       return;
     }
@@ -519,7 +524,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       // row-major: 16 rows x 64 bytes per instruction; TILE16: one contiguous 1 KiB tile (16 rows, the
       // wave's 32 columns), eight whole 128-byte lines
       const u32x4 hv = u32x4{ev_h[i][0], ev_h[i][1], ev_h[i][2], ev_h[i][3]};
-      store_stream_x4_s(half_base(blk_of(pk), i), h_lane, hv);
+      store_stream_x4_s(ep_base + 16 * i * g.ldo, h_lane, hv);
       const f32pair a = rowpair16(ev_dot[i]);  // rows 0 + 1 and 2 + 3 of the 16-lane rows
       ev_dot[i] = a.lo + a.hi;
     } else {
@@ -610,6 +615,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (epi) ep_base += ep_step;
     if (ST || k + NB - 1 < nb) issue(k + NB - 1);
   };
   constexpr std::true_type steady{};
