@@ -163,6 +163,22 @@ __device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const 
                : "v"(voff), "s"(base), "s"(off)
                : "memory");
 }
+// Four such loads from the bases b[0..3] (same lane offset) into LDS lds, lds + STEP, lds + 2 STEP, lds + 3 STEP
+// bytes, with one save and restore of M0 for the four.
+template <unsigned STEP>
+__device__ __forceinline__ void dma_x4_s4(const void* b0, const void* b1, const void* b2, const void* b3, unsigned voff,
+                                          const void* lds) {
+  const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %4\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %5\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %6\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(off), "s"(b0), "s"(b1), "s"(b2), "s"(b3), "i"(STEP)
+      : "memory");
+}
 __device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
   const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   unsigned saved;

@@ -189,6 +189,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   const unsigned lane16 = 16u * lane;  // the lane's byte offset in a 1 KiB row load
   const bf16* nx_x = g.A + (long)nx_p * g.a_mstride + (long)(nx_t0 + 4 * wave) * g.lda;
   const long x_step = (long)step_rows * g.lda, x_wrap = g.a_mstride - (long)g.T * g.lda;
+  const long x_row = 2 * g.lda;  // bytes between the x rows one wave loads
   // relu^2: lanes 0-7 load a_p, 8-15 b_next (the wave's 32 columns of direction p >> pair_shift), 16-23 the
   // block's 32 input-side dots (rows row0 ..)
   auto vsrc_at = [&](int p, int row0) -> const float* {
@@ -217,8 +218,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       nx_v += v_step;
     }
     char* xsl = smem + buf * XBYTES + 4 * wave * XROW;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dma_x4_s(xb + (long)q * g.lda * 2, lane16, xsl + q * XROW);
+    dma_x4_s4<XROW>(xb, xb + x_row, xb + 2 * x_row, xb + 3 * x_row, lane16, xsl);
     // u_qkv rows of the block: 16 bytes per row (lanes 0-31)
     const float* urows = g.u + (long)row0 * 4;
     if constexpr (VV) {
