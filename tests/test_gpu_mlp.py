@@ -144,6 +144,25 @@ def test_dense_wtile_weight_on_narrow_tiles(dout, din):
     assert ((ys[0].cpu().float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6).all()
 
 
+@pytest.mark.parametrize('P', [28, 36, 44])
+def test_mlp_block_counts_around_the_steady_loop(P):
+    """The c_fc kernel runs an iteration from its steady loop when all earlier stores and later loads are outstanding
+    (blocks 3 .. nb - 4 of a workgroup's nb). At T = 256 on a 256-CU part each workgroup gets P / 4 blocks: 7, 9 and
+    11 put the first and last steady pairs at different block indices. Sampled members match the oracle at the
+    small-case bound."""
+    from noise_amd import ops
+    T = 256
+    log_case(f'mlp steady-loop block counts P={P} T={T}')
+    args = _mlp_inputs(P, T, False, 1e-2, seed=9)
+    dev = [t.to(DEV) for t in args]
+    y = ops.lowrank_mlp(*dev, T=T, pair_shift=1)
+    torch.cuda.synchronize()
+    members = [0, 1, P // 2, P - 1]
+    ref = _oracle_members(*args, members)
+    got = y[members].cpu()
+    assert rel_err(got, ref) < 4e-3, rel_err(got, ref)
+
+
 def test_mlp_config1_full_size_sampled_members():
     """Config 1 at its real shape (P = 256, T = 2048, shared x); three members checked in full."""
     from noise_amd import ops
