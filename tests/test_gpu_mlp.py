@@ -163,6 +163,26 @@ def test_mlp_block_counts_around_the_steady_loop(P):
     assert rel_err(got, ref) < 4e-3, rel_err(got, ref)
 
 
+@pytest.mark.parametrize('P', [112, 144, 176])
+def test_dense_block_counts_around_the_steady_loop(P):
+    """The attention c_proj product (K = N = 512, the weight-resident kernel's dense mode) at 7, 9 and 11 blocks per
+    workgroup on a 256-CU part (two 256-column slices, 16 row streams per XCD, T = 256): bf16(x W^T) within one
+    bf16 step everywhere."""
+    from noise_amd import _lib
+    T, D = 256, 512
+    M = P * T
+    log_case(f'dense steady-loop block counts P={P} T={T}')
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(M, D, generator=g).bfloat16()
+    w = (torch.randn(D, D, generator=g) * D ** -0.5).bfloat16()
+    y = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_dense_bf16', x.to(DEV).data_ptr(), _lib.LAYOUT_ROWS, D, D, w.to(DEV).data_ptr(), _lib.LAYOUT_ROWS,
+              P, T, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = (x.float() @ w.float().t()).bfloat16().float()
+    assert ((y.cpu().float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6).all()
+
+
 def test_mlp_config1_full_size_sampled_members():
     """Config 1 at its real shape (P = 256, T = 2048, shared x); three members checked in full."""
     from noise_amd import ops
