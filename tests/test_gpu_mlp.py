@@ -175,9 +175,31 @@ def test_dense_block_counts_around_the_steady_loop(P):
     g = torch.Generator().manual_seed(10)
     x = torch.randn(M, D, generator=g).bfloat16()
     w = (torch.randn(D, D, generator=g) * D ** -0.5).bfloat16()
+    xd, wd = x.to(DEV), w.to(DEV)  # held: a temporary's memory could be reused before the kernel reads it
     y = torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_dense_bf16', x.to(DEV).data_ptr(), _lib.LAYOUT_ROWS, D, D, w.to(DEV).data_ptr(), _lib.LAYOUT_ROWS,
-              P, T, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    _lib.call('noise_dense_bf16', xd.data_ptr(), _lib.LAYOUT_ROWS, D, D, wd.data_ptr(), _lib.LAYOUT_ROWS, P, T,
+              y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = (x.float() @ w.float().t()).bfloat16().float()
+    assert ((y.cpu().float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6).all()
+
+
+@pytest.mark.parametrize('din', [128, 192, 256, 320, 1536])
+def test_dense_tile_gemm_depths_around_the_steady_loop(din):
+    """The tile GEMM's dense product runs k stages 1 .. KT - 4 (KT = din / 32) from its steady loop in pairs: none at
+    KT = 4 or 6, one pair at 8, one at 10 (an odd count left for the general loop), 22 at 48. bf16(x W^T) within one
+    bf16 step everywhere."""
+    from noise_amd import _lib
+    P, T, dout = 4, 256, 512
+    M = P * T
+    log_case(f'dense tile GEMM depth M={M} {din}->{dout}')
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(M, din, generator=g).bfloat16()
+    w = (torch.randn(dout, din, generator=g) * din ** -0.5).bfloat16()
+    xd, wd = x.to(DEV), w.to(DEV)  # held: a temporary's memory could be reused before the kernel reads it
+    y = torch.empty(M, dout, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_dense_bf16', xd.data_ptr(), _lib.LAYOUT_ROWS, din, dout, wd.data_ptr(), _lib.LAYOUT_ROWS, P, T,
+              y.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     ref = (x.float() @ w.float().t()).bfloat16().float()
     assert ((y.cpu().float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6).all()
