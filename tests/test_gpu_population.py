@@ -544,14 +544,14 @@ def _population_case(model, params, P, T, sigma, seed, head='fp32'):
     return got, noise, sign, idx, tgt
 
 
-def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False):
+def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False, head='fp32'):
     """bf16-mode oracle losses, and how far they move under three equally valid changes of rounding: every
     GEMM accumulating in fp64 instead of fp32, attention computed in fp64, and attention at TF32-class
     precision (q, k, v and the probabilities rounded to fp16, the reference's TF32 flex attention's
     significand). The largest move (per loss and per antithetic difference) is the floor: at trained-scale
     weights the bf16 path is chaotic, and one alternative alone under-samples how far valid roundings diverge
     (the CPU oracle's own results also shift with the host's summation order)."""
-    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head=head)
     orig_attn = om.attention
 
     def attention_p16(q, k, v, window, dtype=torch.float32):
@@ -571,7 +571,7 @@ def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False):
                     attention_p16):
         om.attention = variant
         try:
-            alts.append(om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32'))
+            alts.append(om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head=head))
         finally:
             om.attention = orig_attn
     orig = om.lowrank
@@ -585,7 +585,7 @@ def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False):
 
     om.lowrank = lowrank64
     try:
-        alt = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+        alt = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head=head)
     finally:
         om.lowrank = orig
     floor = max(float((a - ref).abs().max()) for a in (alt, *alts))
@@ -595,15 +595,17 @@ def _oracle_with_floor(params, noise, sign, idx, tgt, return_alts=False):
     return ref, floor, pair_floor
 
 
-def test_population_loss_config0_at_reference_init():
+@pytest.mark.parametrize('head', ['fp32', 'bf16'])
+def test_population_loss_config0_at_reference_init(head):
     """Config 0 (P = 8, T = 256, sigma = 1e-3) on the reference's seed-0 weights: losses and the
-    antithetic differences within 1e-4 of the bf16-mode oracle."""
+    antithetic differences within 1e-4 of the bf16-mode oracle, with the fp32 head and with the reference's
+    autocast (bf16) head that `bench.py --head bf16` times."""
     model = make_model('cpu', 0)
     params = {n: p.detach().clone() for n, p in model.named_parameters()}
     P, T = 8, 256
-    log_case(f'population_loss P={P} T={T} reference init')
-    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11)
-    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head='fp32')
+    log_case(f'population_loss P={P} T={T} reference init head={head}')
+    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11, head=head)
+    ref = om.population_loss(params, noise, sign, idx, tgt, mode='bf16', head=head)
     assert torch.isfinite(got).all()
     assert (got - ref).abs().max() < 1e-4, (got, ref)
     dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
@@ -639,12 +641,15 @@ def test_population_loss_config4_full_size_sampled_members():
     assert (dg - dr).abs().max() < 1e-4, (dg, dr)
 
 
-def test_population_loss_trained_weights_within_rounding_floor(trained):
+@pytest.mark.parametrize('head', ['fp32', 'bf16'])
+def test_population_loss_trained_weights_within_rounding_floor(trained, head):
+    """Trained-scale weights, with the fp32 head and with the autocast (bf16) head: within twice the oracle's
+    rounding floor (measured in the test) plus 1e-4."""
     model, params = trained
     P, T = 8, 256
-    log_case(f'population_loss P={P} T={T} trained-scale weights')
-    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11)
-    ref, floor, pair_floor = _oracle_with_floor(params, noise, sign, idx, tgt)
+    log_case(f'population_loss P={P} T={T} trained-scale weights head={head}')
+    got, noise, sign, idx, tgt = _population_case(model, params, P, T, 1e-3, seed=11, head=head)
+    ref, floor, pair_floor = _oracle_with_floor(params, noise, sign, idx, tgt, head=head)
     assert torch.isfinite(got).all()
     assert (got - ref).abs().max() <= 2 * floor + 1e-4, (got, ref, floor)
     dg, dr = got[1::2] - got[0::2], ref[1::2] - ref[0::2]
