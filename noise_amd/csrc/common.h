@@ -164,7 +164,8 @@ __device__ __forceinline__ void dma_x4_s(const void* base, unsigned voff, const 
                : "memory");
 }
 // Four such loads from the bases b[0..3] (same lane offset) into LDS lds, lds + STEP, lds + 2 STEP, lds + 3 STEP
-// bytes, with one save and restore of M0 for the four.
+// bytes, with one save and restore of M0 for the four. The s_add_u32 that advances M0 writes SCC, which the
+// clobber list declares, so the compiler keeps no scalar condition live across the block.
 template <unsigned STEP>
 __device__ __forceinline__ void dma_x4_s4(const void* b0, const void* b1, const void* b2, const void* b3, unsigned voff,
                                           const void* lds) {
@@ -177,7 +178,7 @@ __device__ __forceinline__ void dma_x4_s4(const void* b0, const void* b1, const 
       "s_add_u32 m0, m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %6\n\ts_mov_b32 m0, %0"
       : "=&s"(saved)
       : "v"(voff), "s"(off), "s"(b0), "s"(b1), "s"(b2), "s"(b3), "i"(STEP)
-      : "memory");
+      : "memory", "scc");
 }
 __device__ __forceinline__ void dma_x1(const void* src, const void* lds) {
   const unsigned off = __builtin_amdgcn_readfirstlane(lds_offset(lds));

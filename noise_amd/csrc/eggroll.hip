@@ -298,19 +298,26 @@ int outer_update_launch(const OuterUpdateArgs* mats, int n, const float* w, int 
 
 int adam_batch_launch(const AdamTensor* tensors, int n, float beta1, float beta2, float eps, hipStream_t s) {
   if (n <= 0 || !tensors) return NOISE_EINVAL;
+  // every tensor and every chunk's block count is checked before the first launch: a rejected call updates nothing
+  for (int base = 0; base < n; base += ADAM_MAX) {
+    long blocks = 0;
+    for (int k = base; k < std::min(n, base + ADAM_MAX); ++k) {
+      const AdamTensor& t = tensors[k];
+      if (!t.param || !t.grad || !t.m || !t.v || t.n <= 0 || !(t.bc2_sqrt > 0.f)) return NOISE_EINVAL;
+      blocks += (t.n + 255) / 256;
+    }
+    if (blocks > 0x7fffffffL) return NOISE_ENOTSUP;
+  }
   for (int base = 0; base < n; base += ADAM_MAX) {
     AdamBatchArgs g{};
     g.n = std::min(ADAM_MAX, n - base);
     g.beta1 = beta1, g.beta2 = beta2, g.eps = eps;
     long blocks = 0;
     for (int k = 0; k < g.n; ++k) {
-      const AdamTensor& t = tensors[base + k];
-      if (!t.param || !t.grad || !t.m || !t.v || t.n <= 0 || !(t.bc2_sqrt > 0.f)) return NOISE_EINVAL;
-      g.t[k] = t;
-      blocks += (t.n + 255) / 256;
+      g.t[k] = tensors[base + k];
+      blocks += (g.t[k].n + 255) / 256;
       g.t[k].block_end = blocks;
     }
-    if (blocks > 0x7fffffffL) return NOISE_ENOTSUP;
     hipLaunchKernelGGL(adam_batch_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g);
     NOISE_CHECK_LAUNCH();
   }

@@ -373,28 +373,16 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   auto epi_stage = [&](const f32x4 (&acc)[2][2], int pk, int pbuf, int st) {
     const char* vw = &svec[pbuf][wave][0];
     if constexpr (VV || VE) {
-      // stages 0: vectors; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 (fp32, as the
+      // stages 0: the wave's a; 1-4 / 6-9: v = bf16(dense) + s bf16(u_v) a of row half 0 / 1 (fp32, as the
       // reference's lowrank output), plus the gated embedding term in VE mode, as fp16 pairs; 5 / 10: the row
       // half's store
-      const float* avw;
-      const float(*uqr)[4];
-      if constexpr (VE) {
-        avw = &vv[pbuf].av[wave][0];
-        uqr = vv[pbuf].uq;
-      } else {
-        avw = &qv[pbuf].av[wave][0];
-        uqr = qv[pbuf].uq;
-      }
-      const int r = lane & 15;
+      const float* avw = VE ? &vv[pbuf].av[wave][0] : &qv[pbuf].av[wave][0];
       if (st == 0) {
+        // a over the wave's own columns (this wave's own load); ev_u was read in the block's own iteration
         const float4 a0 = *reinterpret_cast<const float4*>(avw + 8 * grp);
         const float4 a1 = *reinterpret_cast<const float4*>(avw + 8 * grp + 4);
         ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
         ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
-        const float4 u0 = *reinterpret_cast<const float4*>(&uqr[r][0]);
-        const float4 u1 = *reinterpret_cast<const float4*>(&uqr[16 + r][0]);
-        ev_u[0] = u0.w * bf16r(u0.z);
-        ev_u[1] = u1.w * bf16r(u1.z);
         return;
       }
       if (st > 10) return;
@@ -420,7 +408,7 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       // Iteration k runs, for block pk - 1 (held from iteration k - 1): stages 0 / 1, the head's RMSNorm
       // (utils/model.py:46-47, eps = 2^-23) of row half 0 / 1 from both waves' sums of squares, written
       // to LDS last iteration and visible since this iteration's barrier, and the fp16 store; for block pk:
-      // stage 2 the vectors, 3-6 / 8-11 v = bf16(dense) + s bf16(u) a of row half 0 / 1, 7 / 12 rotary
+      // stage 2 the wave's a, 3-6 / 8-11 v = bf16(dense) + s bf16(u) a of row half 0 / 1, 7 / 12 rotary
       // (utils/model.py:55-58) and the wave's sum of squares into LDS.
       const QkVec& q = qv[pbuf];
       const int r = lane & 15, seg = nslice >> 1;
@@ -438,21 +426,12 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       }
       if (pk < 0 || st > 12) return;
       if (st == 2) {
+        // a over the wave's own columns (this wave's own load); ev_u and ev_cs were read in the block's own
+        // iteration
         const float4 a0 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp]);
         const float4 a1 = *reinterpret_cast<const float4*>(&q.av[wave][8 * grp + 4]);
         ev_a[0] = a0.x, ev_a[1] = a0.y, ev_a[2] = a0.z, ev_a[3] = a0.w;
         ev_a[4] = a1.x, ev_a[5] = a1.y, ev_a[6] = a1.z, ev_a[7] = a1.w;
-        const float4 u0 = *reinterpret_cast<const float4*>(&q.uq[r][0]);
-        const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
-        ev_u[0] = u0.w * bf16r(seg ? u0.y : u0.x);
-        ev_u[1] = u1.w * bf16r(seg ? u1.y : u1.x);
-        const int dd = (qk_ocol & 63) & 31;  // the lane's first dim d0 (< 32): 4 dims, half of a 16-byte chunk
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int c = 0; c < 2; ++c)
-            ev_cs[i][c] = *reinterpret_cast<const bf16x4*>(
-                &q.cs[c][16 * i + r][8 * ((dd >> 3) ^ ((r >> 2) & 3)) + (dd & 7)]);
         return;
       }
       const int i = st < 8 ? 0 : 1, sub = st - (i ? 8 : 3);
@@ -531,6 +510,34 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       const f32pair b = halves32(ev_dot[i]);
       ev_dot[i] = b.lo + b.hi;
       red[pk & 1][lr][wave] = ev_dot[i];  // the row's four lanes write the same value
+    }
+  };
+  // The per-block vectors one wave loads for all eight (the u_qkv rows, whose u and sign give ev_u; q|k: also the
+  // rotary rows, loaded by waves 0-3) are read into registers in the iteration of their own block k, after the
+  // epilogue of block k - 1 has used the previous ones (MFMA step 13). Block k's ring slot is refilled at the end
+  // of iteration k + 1, after that iteration's barrier, which every wave passes only once its reads of iteration
+  // k are complete; an epilogue read of iteration k + 1 would race with a faster wave's refill.
+  auto read_shared = [&](int k) {
+    const int buf = k % NB, r = lane & 15;
+    if constexpr (VV || VE) {
+      const float(*uqr)[4] = VE ? vv[buf].uq : qv[buf].uq;
+      const float4 u0 = *reinterpret_cast<const float4*>(&uqr[r][0]);
+      const float4 u1 = *reinterpret_cast<const float4*>(&uqr[16 + r][0]);
+      ev_u[0] = u0.w * bf16r(u0.z);
+      ev_u[1] = u1.w * bf16r(u1.z);
+    } else if constexpr (QK) {
+      const QkVec& q = qv[buf];
+      const int seg = nslice >> 1;
+      const float4 u0 = *reinterpret_cast<const float4*>(&q.uq[r][0]);
+      const float4 u1 = *reinterpret_cast<const float4*>(&q.uq[16 + r][0]);
+      ev_u[0] = u0.w * bf16r(seg ? u0.y : u0.x);
+      ev_u[1] = u1.w * bf16r(seg ? u1.y : u1.x);
+      const int dd = (qk_ocol & 63) & 31;  // the lane's first dim d0 (< 32): 4 dims, half of a 16-byte chunk
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          ev_cs[i][c] = *reinterpret_cast<const bf16x4*>(&q.cs[c][16 * i + r][8 * ((dd >> 3) ^ ((r >> 2) & 3)) + (dd & 7)]);
     }
   };
   // wave 0: the 8 wave partials of block pk's rows (written before the last barrier) -> one partial per row
@@ -612,6 +619,9 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
       }
       if constexpr (MODE == XS_RELU2) {
         if (s == 13 && (ST || sum)) sum_partials(k - 2);
+      }
+      if constexpr (VV || VE || QK) {
+        if (s == 13) read_shared(k);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

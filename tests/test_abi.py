@@ -74,6 +74,13 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_fitness(1, 7, 4, 0, 1, 1, None) == EINVAL        # odd number of losses
     assert lib.noise_fitness(1, 8, 4, 5, 1, 1, None) == EINVAL        # unknown mode
     assert lib.noise_adam(None, None, None, None, 10, 1e-3, .5, .95, 1e-8, 1.0, None) == EINVAL
+    # a bad tensor in the second 64-tensor chunk refuses the whole batch before the first chunk's launch (the
+    # earlier tensors' addresses are never dereferenced: nothing is launched)
+    good = (16, 16, 16, 16, 256, 1e-3, 1.0)
+    ptr, count, _keep = _lib.adam_tensors([good] * 64 + [(None, 16, 16, 16, 256, 1e-3, 1.0)])
+    assert lib.noise_adam_batch(ptr, count, .5, .95, 1e-8, None) == EINVAL
+    ptr, count, _keep = _lib.adam_tensors([good] * 70 + [(16, 16, 16, 16, 256, 1e-3, 0.0)])  # bc2_sqrt must be > 0
+    assert lib.noise_adam_batch(ptr, count, .5, .95, 1e-8, None) == EINVAL
     assert lib.noise_attention(1, 1, 100, 50, 0, 1, None, 0, 1, None, None, None, 0, None) == EINVAL  # T % 128
     # the allocation-free attention refuses moments beyond its fixed array (1024 x 2048 needs 16 Mi partials)
     assert lib.noise_attention_noalloc(1, 1024, 2048, 2048, 1, 1, None, 0, 1, None, 1, None) == ENOSPC

@@ -50,8 +50,14 @@ def test_attention_noalloc_equals_workspace_entry_on_two_calls():
 
 
 def test_attention_noalloc_refuses_sizes_beyond_its_array():
+    """257 members at 2048 tokens need more moment partials than the array holds. Every buffer is a real device
+    allocation of the full requested size, so even a regressed size guard would only launch in-bounds work."""
     log_case('attention_noalloc size limit')
-    qkv, bp = _inputs(2, 128, 3)
-    rc = _lib.load().noise_attention_noalloc(qkv.data_ptr(), 257, 2048, 2048, 1, 1, None, 0, 1, None, 1,
-                                             torch.cuda.current_stream().cuda_stream)
+    P, T = 257, 2048
+    qkv = torch.zeros(P * T, 1536, device=DEV, dtype=torch.bfloat16)
+    y = torch.empty(P * T, 512, device=DEV, dtype=torch.bfloat16)
+    mom = torch.empty(P, 8, 2, 64, device=DEV)
+    rc = _lib.load().noise_attention_noalloc(qkv.data_ptr(), P, T, 2048, 1, 1, None, 0, y.data_ptr(), None,
+                                             mom.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     assert rc == -2  # NOISE_ENOSPC
