@@ -168,9 +168,12 @@ int noise_qkv(const void* h, const void* w_qkv, const float* a_q, const float* a
 #define NOISE_QK_BF16 0       /* q, k bf16 (the credit reruns' moved heads, train/val/run.py:186-189) */
 #define NOISE_QK_F16 1        /* q, k fp16 */
 #define NOISE_QK_F16_Q_LOG2 2 /* q, k fp16 with q pre-multiplied by log2(e) / 8, as noise_qkv writes them (qk_norm != 0) */
+#define NOISE_QK_BF16_V_BF16 3 /* q, k and v bf16, probabilities rounded to bf16 for P V (qk_norm != 0): torch's
+                                 * attention on bf16 operands, as GPT.forward runs it under autocast in
+                                 * utils/eval.py:44-45 (flex on bf16 q, k, v, utils/model.py:31) */
 
 /* Windowed causal attention on q | k | v rows of [members*T, 1536] 16-bit values (8 heads x 64): q and k in
- * qk_format (NOISE_QK_*); v fp16.
+ * qk_format (NOISE_QK_*); v fp16 (bf16 for NOISE_QK_BF16_V_BF16).
  * y bf16 [members*T, 512]; a query at s
  * sees keys s - window .. s (utils/model.py:14-31). When b_proj is not null, writes the c_proj
  * input-side dot partials upart [members*T, 8]. When mom is not null, writes per-(member, head)
@@ -217,6 +220,30 @@ int noise_weight_tiles(const void* w, int rows, int cols, void* out, noise_strea
  * out % 128 == 0; TILE16 also T % 16 == 0. */
 int noise_dense_bf16(const void* x, int x_layout, int in, int out, const void* w, int w_layout, int members, int T,
                      void* y, noise_stream_t stream);
+
+/* The clean forward's residual stream at the rounding points GPT.forward has under torch's bf16 autocast with bf16
+ * embedding tables, as the speedrun's scorer runs it (utils/eval.py:44-45 on utils/model.py:193-210, tables bf16
+ * per :171-175). Rows r = b * T + t of batch row b: every tensor is bf16 and every op rounds to bf16.
+ *   x = x_in, or x0 = bf16(norm(wte[idx])) when x_in is null (:196-197; rms_norm of a bf16 input computes in
+ *       fp32 with eps 2^-23 and casts back)
+ *   x = bf16(x + y1), then bf16(x + y2) for the non-null block outputs y1, y2 (the residual adds of :118-119)
+ *   x = bf16(bf16(bf16(l_r) x) + bf16(bf16(l_0) x0)) when lambda_r is not null (:199; the 0-d fp32 lambdas
+ *       are cast to bf16 by type promotion against the bf16 stream)
+ *   x_out = x (nullable); h = bf16(norm(x)) (nullable)
+ *   gate = 2 bf16(sigmoid(bf16(h[:32] . bf16(gate_w)^T))) [rows, 8] when gate_w [8, 32] is not null (:89)
+ * wte [vocab, 512] fp32 holding bf16 values; idx: row (b, t) reads idx[b * idx_mstride + t]. x_in, y1, y2,
+ * x_out, h bf16 [rows, 512], 16-byte aligned. */
+int noise_ac_stream(const void* x_in, const float* wte, long vocab, const int64_t* idx, long idx_mstride,
+                    const void* y1, const void* y2, const float* lambda_r, const float* lambda_0, void* x_out, void* h,
+                    const float* gate_w, float* gate, int rows, int T, noise_stream_t stream);
+
+/* q | k | v [rows, 1536] bf16 (the bf16 outputs of c_q, c_k, c_v under autocast) updated in place as
+ * utils/model.py:83-94 treats them under torch's bf16 autocast: q and k rotated with bf16 tables, every product
+ * and sum rounded to bf16 (:55-58, :93), then norm per 64-dim head, bf16 out (:94); when gate is not null,
+ * v = bf16(v + bf16(gate[row, head] ve_w[tok])) (:88-90, :200) with ve_w [vocab, 512] fp32 holding bf16 values.
+ * The output is noise_attention's NOISE_QK_BF16_V_BF16 operand. */
+int noise_ac_qkv(void* qkv, const void* rot_cos, const void* rot_sin, const float* gate, const float* ve_w,
+                 long vocab, const int64_t* idx, long idx_mstride, int rows, int T, noise_stream_t stream);
 
 /* h = bf16(norm(x)); u[row] = bf16(h . bf16(b[dir])) (MLP entry, train/val/eggroll.py:93). The npend (<= 2)
  * deferred residuals in pend are added to x, in order, before the norm; x itself is not written. */

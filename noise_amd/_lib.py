@@ -17,7 +17,7 @@ ERRORS = {-1: 'NOISE_EINVAL (rejected argument)', -2: 'NOISE_ENOSPC (workspace t
           -3: 'NOISE_ENOTSUP (shape outside the kernel tiling)'}
 
 FITNESS_ZSCORE, FITNESS_RANK = 0, 1
-QK_BF16, QK_F16, QK_F16_Q_LOG2 = 0, 1, 2
+QK_BF16, QK_F16, QK_F16_Q_LOG2, QK_BF16_V_BF16 = 0, 1, 2, 3
 LAYOUT_ROWS, LAYOUT_TILE16, LAYOUT_WTILE = 0, 1, 2
 CE_MEMBER_MEAN, CE_NONE, CE_SUM, CE_MEAN = 0, 1, 2, 3
 
@@ -38,6 +38,8 @@ SIGNATURES = {
     'noise_attention_noalloc': [P, I, I, I, I, I, P, I, P, P, P, P],
     'noise_lowrank_resid': [P, P, I, I, P, P, I, L, L, P, I, I, I, P, P],
     'noise_norm_dot': [P, P, P, P, P, I, I, I, P, I, P],
+    'noise_ac_stream': [P, P, L, P, L, P, P, P, P, P, P, P, P, I, I, P],
+    'noise_ac_qkv': [P, P, P, P, P, L, P, L, I, I, P],
     'noise_weight_tiles': [P, I, I, P, P],
     'noise_dense_bf16': [P, I, I, I, P, I, I, I, P, P],
     'noise_mlp_fc_parts': [I],

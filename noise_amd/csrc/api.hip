@@ -4,6 +4,7 @@
 
 #include "../../include/noise_hip.h"
 #include "attention.h"
+#include "autocast.h"
 #include "common.h"
 #include "credit.h"
 #include "eggroll.h"
@@ -11,7 +12,8 @@
 #include "probes.h"
 #include "rowops.h"
 
-static_assert(NOISE_QK_BF16 == QK_BF16 && NOISE_QK_F16 == QK_F16 && NOISE_QK_F16_Q_LOG2 == QK_F16_Q_LOG2,
+static_assert(NOISE_QK_BF16 == QK_BF16 && NOISE_QK_F16 == QK_F16 && NOISE_QK_F16_Q_LOG2 == QK_F16_Q_LOG2 &&
+                  NOISE_QK_BF16_V_BF16 == QK_BF16_V_BF16,
               "q/k format codes");
 static_assert(NOISE_CE_MEMBER_MEAN == CE_MEMBER_MEAN && NOISE_CE_NONE == CE_NONE && NOISE_CE_SUM == CE_SUM &&
                   NOISE_CE_MEAN == CE_MEAN,
@@ -355,6 +357,46 @@ int noise_lowrank_resid(const void* x, const void* w, int in, int out, const flo
   g.out_f32 = resid;
   g.ldo = out;
   return lowrank_gemm_launch(EPI_RESID, g, static_cast<hipStream_t>(stream));
+}
+
+int noise_ac_stream(const void* x_in, const float* wte, long vocab, const int64_t* idx, long idx_mstride,
+                    const void* y1, const void* y2, const float* lambda_r, const float* lambda_0, void* x_out, void* h,
+                    const float* gate_w, float* gate, int rows, int T, noise_stream_t stream) {
+  if (rows <= 0 || T <= 0 || rows % T) return NOISE_EINVAL;
+  AcStreamArgs g{};
+  g.x_in = static_cast<const bf16*>(x_in);
+  g.emb_w = wte;
+  g.V = vocab;
+  g.idx = idx;
+  g.idx_mstride = idx_mstride;
+  g.add[0] = static_cast<const bf16*>(y1);
+  g.add[1] = static_cast<const bf16*>(y2);
+  g.lambda_r = lambda_r;
+  g.lambda_0 = lambda_0;
+  g.x_out = static_cast<bf16*>(x_out);
+  g.h = static_cast<bf16*>(h);
+  g.gate_w = gate_w;
+  g.gate = gate;
+  g.M = rows;
+  g.T = T;
+  return ac_stream_launch(g, static_cast<hipStream_t>(stream));
+}
+
+int noise_ac_qkv(void* qkv, const void* rot_cos, const void* rot_sin, const float* gate, const float* ve_w,
+                 long vocab, const int64_t* idx, long idx_mstride, int rows, int T, noise_stream_t stream) {
+  if (rows <= 0 || T <= 0 || rows % T) return NOISE_EINVAL;
+  AcQkvArgs g{};
+  g.qkv = static_cast<bf16*>(qkv);
+  g.rot_cos = static_cast<const bf16*>(rot_cos);
+  g.rot_sin = static_cast<const bf16*>(rot_sin);
+  g.gate = gate;
+  g.ve_w = ve_w;
+  g.V = vocab;
+  g.idx = idx;
+  g.idx_mstride = idx_mstride;
+  g.M = rows;
+  g.T = T;
+  return ac_qkv_launch(g, static_cast<hipStream_t>(stream));
 }
 
 int noise_norm_dot(const float* x, void* h, const float* b, float* u, const float* sign, int members, int T,

@@ -7,7 +7,9 @@
 // reference feeds flex (rotary and QK-norm already applied by the QKV kernels): an 11-bit significand, the
 // precision class of the TF32 attention the reference runs under set_float32_matmul_precision('high')
 // (train/val/eggroll.py:184). The credit reruns (train/val/run.py:594-634) run attention on bf16 q and k, as
-// the reference does there; the q/k element type is a template parameter, v is fp16 in both.
+// the reference does there; the q/k element type is a template parameter, v is fp16 in both. The clean forward at
+// torch's bf16 autocast rounding (the speedrun's scorer, utils/eval.py:44-45) runs it on bf16 q, k and v with the
+// probabilities rounded to bf16 for P V, as torch's attention on bf16 operands does.
 //
 // One workgroup = one (member, head, 128-query block); 4 waves of 32 queries; four workgroups per CU (122
 // VGPRs, 34 KiB of LDS each: 4 waves per SIMD hide the LDS and transcendental latencies).
@@ -32,6 +34,8 @@
 //   banks, nor for 32 lanes on 64 banks). Each lane ends with dims 16 db + 4 (lane / 16) .. + 3 of one
 //   query for db = 0..3: 8-byte stores, and the c_proj dot y . b_proj over the head's 64 dims is a 4-lane
 //   reduction.
+#include <type_traits>
+
 #include "attention.h"
 #include "common.h"
 
@@ -88,11 +92,24 @@ __device__ __forceinline__ unsigned pack2(float a, float b) {
 // F16: q and k are fp16 (bf16 otherwise); they travel as raw 16-bit lanes and only the score MFMA reads their type.
 // QL2: q arrives pre-multiplied by log2(e) / 8 (noise_qkv writes it so), so the MFMA returns scores in base-2 units
 // and the softmax takes exp2 of them directly: one VALU multiply per score less (with QKN no max is subtracted).
-template <bool QKN, bool F16, bool QL2>
+// VB: v is bf16 and the probabilities are rounded to bf16 for P V (the operands of torch's attention on bf16 q, k, v:
+// the autocast clean forward); fp16 otherwise.
+template <bool QKN, bool F16, bool QL2, bool VB>
 __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   static_assert(!QL2 || QKN, "pre-scaled q is the population forward's QK-normalised format");
+  static_assert(!VB || !F16, "bf16 v comes with bf16 q and k");
+  // element type of v and of the probabilities
+  using PT = typename std::conditional<VB, bf16, f16>::type;
+  typedef PT pt8 __attribute__((ext_vector_type(8)));
+  typedef PT pt4 __attribute__((ext_vector_type(4)));
+  auto mfma_pv = [](const pt8& a, const pt8& b, const f32x4& c) {
+    if constexpr (VB)
+      return mfma16x16x32(a, b, c);
+    else
+      return mfma16x16x32_f16(a, b, c);
+  };
   __shared__ __attribute__((aligned(1024))) bf16 sk[2][BKV * HD];
-  __shared__ __attribute__((aligned(1024))) f16 sv[2][BKV * HD];
+  __shared__ __attribute__((aligned(1024))) PT sv[2][BKV * HD];
   __shared__ float smom[NWAVE][2][HD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), grp = lane >> 4;
@@ -168,7 +185,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
         vofs[hh][db] = R * 128 + 16 * ((2 * db + (a >> 1)) ^ vsw(R)) + 8 * (a & 1);
       }
   }
-  const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+  const pt8 ones = {(PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f};
 
   // Scores of keys a query may not see become -inf (branch-free): keys after it when the block touches the
   // causal edge, keys more than `window` before it when the block touches the window edge. Key
@@ -195,7 +212,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     }
   };
   // Online softmax of one key block for query block qb of this wave.
-  auto softmax = [&](f32x4 (&s)[2][KB], f16x8 (&pf)[2][KC], int qb) {
+  auto softmax = [&](f32x4 (&s)[2][KB], pt8 (&pf)[2][KC], int qb) {
     float mc = 0.f;
     if constexpr (!QKN) {
       float m0 = -INFINITY, m1 = -INFINITY;
@@ -224,7 +241,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           pf[qb][c][4 * hlf + e] =
-              (f16)__builtin_amdgcn_exp2f(QL2 ? s[qb][2 * c + hlf][e] : fmaf(s[qb][2 * c + hlf][e], c2, -mc));
+              (PT)__builtin_amdgcn_exp2f(QL2 ? s[qb][2 * c + hlf][e] : fmaf(s[qb][2 * c + hlf][e], c2, -mc));
   };
 
   issue(j0, 0);
@@ -253,7 +270,7 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
     // blocks away from the causal edge and the window edge need no mask
     const bool causal_edge = kstart + BKV - 1 > q0, window_edge = q0 + BQ - 1 - kstart > g.window;
     if (causal_edge || window_edge) apply_mask(s, kstart, causal_edge, window_edge);
-    f16x8 pf[2][KC];
+    pt8 pf[2][KC];
     softmax(s, pf, 0);
     softmax(s, pf, 1);
     // O^T += V^T P^T
@@ -263,15 +280,15 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
       for (int db = 0; db < 4; ++db) {
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + 4096 * c + vofs[0][db]));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(vt + 4096 * c + vofs[1][db]));
-        const f16x4 lo16 = __builtin_bit_cast(f16x4, lo), hi16 = __builtin_bit_cast(f16x4, hi);
-        const f16x8 vf = {lo16[0], lo16[1], lo16[2], lo16[3], hi16[0], hi16[1], hi16[2], hi16[3]};
+        const pt4 lo16 = __builtin_bit_cast(pt4, lo), hi16 = __builtin_bit_cast(pt4, hi);
+        const pt8 vf = {lo16[0], lo16[1], lo16[2], lo16[3], hi16[0], hi16[1], hi16[2], hi16[3]};
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma16x16x32_f16(vf, pf[qb][c], o[qb][db]);
+        for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma_pv(vf, pf[qb][c], o[qb][db]);
       }
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) osum[qb] = mfma16x16x32_f16(ones, pf[qb][c], osum[qb]);
+      for (int qb = 0; qb < 2; ++qb) osum[qb] = mfma_pv(ones, pf[qb][c], osum[qb]);
     // block j + 1 has landed for this wave (the only vector memory operations in flight are its loads);
     // the barrier makes every wave's part visible and retires slot buf
     __builtin_amdgcn_s_waitcnt(0);
@@ -358,20 +375,23 @@ int attention_launch(const AttnArgs& g, hipStream_t s) {
     return NOISE_EINVAL;
   if (g.upart && (!g.b_proj || g.upart_ld < g.H || g.b_ld < g.H * HD)) return NOISE_EINVAL;
   if (g.mom && !g.mom_out) return NOISE_EINVAL;
-  if (g.qk_format < QK_BF16 || g.qk_format > QK_F16_Q_LOG2 || (g.qk_format == QK_F16_Q_LOG2 && !g.qk_norm))
+  if (g.qk_format < QK_BF16 || g.qk_format > QK_BF16_V_BF16 ||
+      ((g.qk_format == QK_F16_Q_LOG2 || g.qk_format == QK_BF16_V_BF16) && !g.qk_norm))
     return NOISE_EINVAL;
   const long grid = (long)(g.T / BQ) * g.H * g.members;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   if (g.qk_format == QK_F16_Q_LOG2)
-    hipLaunchKernelGGL((attention_kernel<true, true, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<true, true, true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+  else if (g.qk_format == QK_BF16_V_BF16)
+    hipLaunchKernelGGL((attention_kernel<true, false, false, true>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else if (g.qk_norm && g.qk_format == QK_F16)
-    hipLaunchKernelGGL((attention_kernel<true, true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<true, true, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else if (g.qk_norm)
-    hipLaunchKernelGGL((attention_kernel<true, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<true, false, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else if (g.qk_format == QK_F16)
-    hipLaunchKernelGGL((attention_kernel<false, true, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<false, true, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   else
-    hipLaunchKernelGGL((attention_kernel<false, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
+    hipLaunchKernelGGL((attention_kernel<false, false, false, false>), dim3((unsigned)grid), dim3(NTH), 0, s, g);
   NOISE_CHECK_LAUNCH();
   if (g.mom) {
     const long n = (long)g.members * g.H * 2 * HD;

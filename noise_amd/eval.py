@@ -5,19 +5,15 @@ split (utils/eval.py:24-53).
 `init_weights` stores the token and value embeddings in bfloat16 before the state dict is copied in
 (utils/model.py:171-175, utils/eval.py:24-31): the tables here keep fp32 storage holding the
 bf16-rounded values, which is what the kernels read. `evaluate` runs `GPT.forward(..., 'sum')` over
-batches of rows on the population kernels at sigma = 0 (head='bf16' by default; 'fp32' for the
-fp32-accurate head), accumulates in fp64 and returns the mean over all predictions.
+batches of rows, accumulates in fp64 and returns the mean over all predictions.
 
-Rounding differs from utils/eval.py. The reference runs GPT.forward under CUDA autocast with bf16 embeddings, so
-its whole residual stream is bf16: x0, every residual add and mix, the norms' outputs, rotary's products, the value
-gate and the attention probabilities round to bf16 (rms_norm and the 0-dim lambda products keep their input's
-bf16 dtype, and F.rms_norm's default eps follows the input dtype: 2^-7 for bf16). The kernels keep the population
-path's rounding points instead: an fp32 residual stream and fp32 norms, bf16 GEMM operands and outputs, fp16
-attention operands. On a trained-scale synthetic model (4 x 256 tokens, CPU) the two mean losses differ by 1.8e-3.
-That is the size of the shift any single one of those rounding points produces on its own there (0.4e-3 to
-2.0e-3 each: the bf16 stream, its eps, the bf16 tables, rotary's per-product rounding, bf16 q / k / P, the bf16
-head), and of the shift the GEMMs' fp32 accumulation order alone produces at that scale (~1.5e-3), so a score from
-`evaluate` agrees with the reference's to about 2e-3, not better.
+Rounding. By default (`rounding='autocast'`) the forward keeps the rounding points utils/eval.py:44-45 gives it:
+torch's bf16 autocast, under which the whole residual stream is bf16 and every op rounds to bf16 (x0, the lambda
+mix with bf16-cast lambdas, the residual adds, the norms' outputs, rotary's products and sums, the value gate, bf16
+q / k / v and probabilities in attention, the bf16 head); `noise_amd.population.autocast_forward` runs it and
+`oracle.model.autocast_forward` restates it. `rounding='population'` runs the population path's rounding instead
+(fp32 residual stream and norms, fp16 attention operands; head='bf16' or 'fp32'), which moves the score of a
+trained-scale model by about 2e-3.
 """
 from pathlib import Path
 
@@ -25,7 +21,7 @@ import torch
 from torch import distributed as dist
 
 from .model import GPT, GPTConfig
-from .population import Weights, clean_forward
+from .population import ROUNDINGS, Weights, autocast_forward, clean_forward
 
 SEQ = 2049       # tokens per row: 2048 inputs + the shifted targets (utils/prepare_data.py:19)
 VAL_ROWS = 544   # rows of the validation split, 1,114,112 predictions (utils/prepare_data.py:21)
@@ -56,21 +52,27 @@ def load_rows(path, rows=VAL_ROWS):
 
 
 @torch.no_grad()
-def evaluate(state_dict, data_dir='data', batch_size=16, rows=None, head='bf16'):
+def evaluate(state_dict, data_dir='data', batch_size=16, rows=None, head='bf16', rounding='autocast'):
     """Mean loss over every prediction of `rows` ([n, T + 1] token ids; by default the validation split
-    under data_dir). Under torch.distributed the rows are split across ranks and the sums all-reduced."""
+    under data_dir). Under torch.distributed the rows are split across ranks and the sums all-reduced.
+    rounding: 'autocast' (utils/eval.py's, the default) or 'population' (with `head`)."""
+    if rounding not in ROUNDINGS:
+        raise ValueError(f'rounding must be one of {ROUNDINGS}')
     rank, world = (dist.get_rank(), dist.get_world_size()) if dist.is_initialized() else (0, 1)
     device = torch.device('cuda', torch.cuda.current_device())
     model = load_model(state_dict, device)
     if rows is None:
         rows = load_rows(Path(data_dir) / 'val.pt')
     rows = rows[rank::world]
-    weights = Weights(dict(model.named_parameters()), model.config, head)
+    weights = Weights(dict(model.named_parameters()), model.config, 'bf16' if rounding == 'autocast' else head)
     total = torch.zeros(2, dtype=torch.float64, device=device)  # summed loss, predictions
     for batch in rows.split(batch_size):
         batch = batch.to(device)
-        loss = clean_forward(model, batch[:, :-1].contiguous(), batch[:, 1:].contiguous(), 'sum', head=head,
-                             weights=weights)
+        x, y = batch[:, :-1].contiguous(), batch[:, 1:].contiguous()
+        if rounding == 'autocast':
+            loss = autocast_forward(model, x, y, 'sum', weights=weights)
+        else:
+            loss = clean_forward(model, x, y, 'sum', head=head, weights=weights)
         total[0] += loss.double()
         total[1] += batch[:, 1:].numel()
     if world > 1:

@@ -3,7 +3,7 @@
 The module tree (names, shapes, parameter order) is the contract `utils/eval.py:24-31` loads with
 `strict=True`, so it is kept identical to `utils/model.py:61-147`. Compute never runs through these
 nn.Modules: `GPT.forward` dispatches to the population kernels with one member per batch row and
-sigma = 0 (`noise_amd.population.clean_forward`).
+sigma = 0 (`noise_amd.population.clean_forward`, or `autocast_forward` under torch's bf16 autocast).
 """
 from dataclasses import dataclass
 
@@ -129,8 +129,12 @@ class GPT(nn.Module):
         self.cos, self.sin = cos[None, :, None, :], sin[None, :, None, :]
 
     def forward(self, idx, targets=None, loss_reduction='mean'):
-        """Clean forward (utils/model.py:193-210) on the HIP kernels: one member per batch row, sigma = 0."""
-        from .population import clean_forward
+        """Clean forward (utils/model.py:193-210) on the HIP kernels: one member per batch row, sigma = 0. Called
+        under torch.autocast('cuda', dtype=torch.bfloat16), as utils/eval.py:44-45 calls it, it keeps that autocast's
+        rounding points (noise_amd.population.autocast_forward); otherwise the population path's."""
+        from .population import autocast_forward, clean_forward
+        if torch.is_autocast_enabled('cuda') and torch.get_autocast_dtype('cuda') == torch.bfloat16:
+            return autocast_forward(self, idx, targets, loss_reduction)
         return clean_forward(self, idx, targets, loss_reduction)
 
 

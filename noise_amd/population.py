@@ -348,6 +348,100 @@ def population_loss(model, p, noise, sign, idx, targets, head='fp32', chunk=256)
 
 
 REDUCTIONS = {'mean': _lib.CE_MEAN, 'sum': _lib.CE_SUM, 'none': _lib.CE_NONE}
+ROUNDINGS = ('population', 'autocast')
+
+
+def _check_clean_inputs(model, idx, targets, loss_reduction):
+    if loss_reduction not in REDUCTIONS:
+        raise ValueError(f"loss_reduction must be one of {tuple(REDUCTIONS)}, got {loss_reduction!r}")
+    _need_cuda(idx, torch.int64, 'idx')
+    if idx.dim() != 2:
+        raise ValueError(f'idx must be [B, T], got {tuple(idx.shape)}')
+    B, T = idx.shape
+    if T % 128:
+        raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')
+    V = model.transformer.wte.weight.shape[0]
+    if idx.min().item() < 0 or idx.max().item() >= V:
+        raise IndexError(f'token ids must lie in [0, {V})')
+    if targets is not None:
+        _need_cuda(targets, torch.int64, 'targets')
+        if targets.shape != idx.shape:
+            raise ValueError(f'targets must be {tuple(idx.shape)}, got {tuple(targets.shape)}')
+        valid = targets != -1
+        if ((targets < 0) & valid).any().item() or (targets >= V).any().item():
+            raise IndexError(f'targets must lie in [0, {V}) or be -1 (ignored)')
+    return B, T, V
+
+
+def autocast_forward(model, idx, targets=None, loss_reduction='mean', weights=None):
+    """GPT.forward (utils/model.py:193-210) on the HIP kernels at the rounding points the speedrun's scorer gives it:
+    torch's bf16 autocast with the token and value embeddings stored in bf16 (utils/eval.py:44-45,
+    utils/model.py:171-175). The residual stream is bf16 and every op rounds to bf16: noise_ac_stream (embedding
+    norm, residual adds, lambda mix, norms, value gate), noise_dense_bf16 (every nn.Linear: bf16 operands, fp32
+    accumulation, bf16 output), noise_ac_qkv (rotary and QK norm in bf16, value embedding), noise_attention on bf16
+    q, k, v with bf16 probabilities, noise_mlp_fc at sigma = 0 (relu(bf16)^2 rounded to bf16 where c_proj casts it)
+    and the bf16 head with the fp32 cap and cross-entropy (noise_head_ce). Same returns as clean_forward. The
+    embedding tables are read as bf16 (fp32 tensors holding bf16 values, as noise_amd.eval.load_model keeps them)."""
+    B, T, V = _check_clean_inputs(model, idx, targets, loss_reduction)
+    cfg = model.config
+    p = dict(model.named_parameters())
+    dev = idx.device
+    W = weights or Weights(p, cfg, 'bf16')
+    if W.head != 'bf16':
+        raise ValueError("the autocast forward needs bf16 head weights (Weights(p, config, 'bf16'))")
+    s = _stream()
+    M = B * T
+    b16 = torch.bfloat16
+    x, h, xf = (torch.empty(M, D, device=dev, dtype=b16) for _ in range(3))
+    y, y_ap, y_mp = (torch.empty(M, D, device=dev, dtype=b16) for _ in range(3))
+    qkv = torch.empty(M, 3 * D, device=dev, dtype=b16)
+    hidden = torch.empty(M, F, device=dev, dtype=b16)
+    gate = torch.empty(M, H, device=dev)
+    parts = _lib.value('noise_mlp_fc_parts', F)
+    upart = torch.empty(parts, M, device=dev)
+    # sigma = 0: zero rank-1 vectors and signs, so noise_mlp_fc and the head add exactly nothing
+    zf, zb, zu, zsign = (torch.zeros(B, F, device=dev), torch.zeros(B, F, device=dev), torch.zeros(M, device=dev),
+                         torch.zeros(B, device=dev))
+    za, zbh = torch.zeros(B, W.head_w.shape[0], device=dev), torch.zeros(B, D, device=dev)
+    pop = Population(model, chunk=B, head='bf16')
+    cos, sin = pop.tables(T)
+    idx = idx.contiguous()
+    wte = p['transformer.wte.weight']
+    lam_r, lam_0 = p['resid_lambdas'], p['x0_lambdas']
+    for i in range(cfg.n_layer):
+        pre = f'transformer.h.{i}.'
+        ve = has_ve(i, cfg.n_layer)
+        first = i == 0
+        _lib.call('noise_ac_stream', None if first else _p(x), _p(wte), V, _p(idx), T, None if first else _p(y_ap),
+                  None if first else _p(y_mp), lam_r.data_ptr() + 4 * i, lam_0.data_ptr() + 4 * i, _p(x), _p(h),
+                  _p(p[pre + 'attn.ve_gate.weight']) if ve else None, _p(gate) if ve else None, M, T, s)
+        _lib.call('noise_dense_bf16', _p(h), _lib.LAYOUT_ROWS, D, 3 * D, _p(W.qkv[i]), _lib.LAYOUT_ROWS, B, T, _p(qkv), s)
+        vw = p[f'value_embeds.{i}.weight'] if ve else None
+        _lib.call('noise_ac_qkv', _p(qkv), _p(cos), _p(sin), _p(gate) if ve else None, _p(vw), V if ve else 0,
+                  _p(idx), T, M, T, s)
+        _lib.call('noise_attention', _p(qkv), B, T, pop.windows[i], 1, _lib.QK_BF16_V_BF16, None, 0, _p(y), None, None,
+                  None, 0, s)
+        _lib.call('noise_dense_bf16', _p(y), _lib.LAYOUT_ROWS, D, D, _p(W.proj[i]), _lib.LAYOUT_ROWS, B, T, _p(y_ap), s)
+        _lib.call('noise_ac_stream', _p(x), None, 0, None, 0, _p(y_ap), None, None, None, None, _p(h), None, None, M, T,
+                  s)
+        _lib.call('noise_mlp_fc', _p(h), _p(W.fc[i]), D, F, _p(zf), _p(zu), _p(zb), _p(zsign), B, T, 0, _p(hidden),
+                  _lib.LAYOUT_TILE16, _p(upart), s)
+        _lib.call('noise_dense_bf16', _p(hidden), _lib.LAYOUT_TILE16, F, D, _p(W.mproj[i]), _lib.LAYOUT_WTILE, B, T,
+                  _p(y_mp), s)
+    _lib.call('noise_ac_stream', _p(x), None, 0, None, 0, _p(y_ap), _p(y_mp), None, None, _p(xf), None, None, None, M, T,
+              s)
+    Vh = W.head_w.shape[0]
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', B, T, Vh, 0), device=dev, dtype=torch.uint8)
+    if targets is None:
+        logits = torch.empty(B, T, Vh, device=dev)
+        _lib.call('noise_head_ce', _p(xf), 1, None, _p(W.head_w), Vh, 0, _p(za), _p(zbh), _p(zsign), None, T, B, T, 0,
+                  _lib.CE_MEMBER_MEAN, None, _p(logits), _p(ws), ws.numel(), None, 0, s)
+        return logits
+    red = REDUCTIONS[loss_reduction]
+    out = torch.empty(M if red == _lib.CE_NONE else 1, device=dev)
+    _lib.call('noise_head_ce', _p(xf), 1, None, _p(W.head_w), Vh, 0, _p(za), _p(zbh), _p(zsign),
+              _p(targets.contiguous()), T, B, T, 0, red, _p(out), None, _p(ws), ws.numel(), None, 0, s)
+    return out if red == _lib.CE_NONE else out[0]
 
 
 def clean_forward(model, idx, targets=None, loss_reduction='mean', head='fp32', weights=None):
@@ -360,25 +454,8 @@ def clean_forward(model, idx, targets=None, loss_reduction='mean', head='fp32', 
     fp32 logits [B, T, vocab] are returned. The kernels keep the rounding points of the population path (fp32
     residual stream and norms, bf16 GEMMs, fp16 attention operands), not the all-bf16 stream GPT.forward has under
     autocast with bf16 embeddings; head='fp32' keeps the head fp32-accurate, 'bf16' rounds it as autocast does."""
-    if loss_reduction not in REDUCTIONS:
-        raise ValueError(f"loss_reduction must be one of {tuple(REDUCTIONS)}, got {loss_reduction!r}")
-    _need_cuda(idx, torch.int64, 'idx')
-    if idx.dim() != 2:
-        raise ValueError(f'idx must be [B, T], got {tuple(idx.shape)}')
-    B, T = idx.shape
-    if T % 128:
-        raise ValueError(f'T = {T} must be a multiple of 128 (attention query blocks)')
+    B, T, V = _check_clean_inputs(model, idx, targets, loss_reduction)
     p = dict(model.named_parameters())
-    V = p['transformer.wte.weight'].shape[0]
-    if idx.min().item() < 0 or idx.max().item() >= V:
-        raise IndexError(f'token ids must lie in [0, {V})')
-    if targets is not None:
-        _need_cuda(targets, torch.int64, 'targets')
-        if targets.shape != idx.shape:
-            raise ValueError(f'targets must be {tuple(idx.shape)}, got {tuple(targets.shape)}')
-        valid = targets != -1
-        if ((targets < 0) & valid).any().item() or (targets >= V).any().item():
-            raise IndexError(f'targets must lie in [0, {V}) or be -1 (ignored)')
     dev = idx.device
     # sigma = 0: zero signs and zero noise rows (finite, so s * (x . b) * a is exactly zero)
     noise = {n: (torch.zeros(B, t.shape[0], device=dev), torch.zeros(B, t.shape[1], device=dev)) if t.dim() == 2

@@ -17,6 +17,9 @@ Two rounding modes:
 ``head='fp32'`` evaluates the lm_head GEMM in float32 (the north star's fp32 head); ``head='bf16'`` is
 the reference's autocast head.
 
+``autocast_forward`` restates the clean GPT.forward at the rounding points of the speedrun's scorer
+(utils/eval.py:44-45: bf16 autocast with bf16 embedding tables), where the whole residual stream is bf16.
+
 Parity pins (tests/test_oracle.py): norm against F.rms_norm; rotary against the complex-rotation
 closed form; attention against an fp64 loop over (query, key) on tiny T; lowrank / lowrank_embed
 against the materialised perturbed weight W + s a b^T; population_loss against (i) the golden
@@ -206,6 +209,103 @@ def gpt_forward(p, idx, targets=None, loss_reduction='mean', cos=None, sin=None,
     if targets is None:
         return logits
     return F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1,
+                           reduction=loss_reduction)
+
+
+def attention_bf16(q, k, v, window):
+    """torch's attention on bf16 q, k, v [B, T, H, D] (flex, utils/model.py:31, as GPT.forward runs it under autocast):
+    fp32 scores of the bf16 operands scaled by 1/sqrt(D), softmax probabilities exp(s - rowmax) rounded to bf16 for
+    P V with fp32 accumulation, the normaliser summed from the unrounded probabilities, bf16 output. (The flex
+    kernel's running maximum and block order are not restated: parity unpinned below that rounding class.)"""
+    B, T, H, D = q.shape
+    qh, kh, vh = (t.transpose(1, 2).double() for t in (q, k, v))
+    scores = (qh @ kh.transpose(-1, -2) / math.sqrt(D)).float()
+    pos = torch.arange(T)
+    mask = (pos[:, None] >= pos[None, :]) & (pos[:, None] - pos[None, :] <= window)
+    scores = scores.masked_fill(~mask, float('-inf'))
+    pr = torch.exp(scores - scores.amax(-1, keepdim=True))
+    y = (bf(pr).double() @ vh) / pr.double().sum(-1, keepdim=True)
+    return bf(y.float()).transpose(1, 2)
+
+
+def ac_norm(x):
+    """norm of a bf16 tensor under autocast: fp32 mean of squares, eps 2^-23, bf16 result (utils/model.py:46-47;
+    torch 2.10's rms_norm computes a bf16 input in fp32 with the fp32 epsilon)."""
+    return bf(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + EPS))
+
+
+def ac_mix(lam_r, lam_0, x, x0):
+    """lambda_r * x + lambda_0 * x0 with 0-d fp32 lambdas on the bf16 stream (utils/model.py:199): type promotion
+    casts the lambdas to bf16; the products and the sum round to bf16."""
+    return bf(bf(bf(lam_r) * x) + bf(bf(lam_0) * x0))
+
+
+def ac_rotary(x, cos, sin):
+    """apply_rotary_emb (utils/model.py:55-58) on bf16 x [B, T, H, D] and bf16 tables [T, D/2]: every product and
+    every sum rounds to bf16."""
+    d = x.shape[3] // 2
+    c, s = cos.float()[None, :, None, :], sin.float()[None, :, None, :]
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([bf(bf(x1 * c) + bf(x2 * s)), bf(bf(x1 * -s) + bf(x2 * c))], 3)
+
+
+def ac_value_gate(v, gate_logit, ve):
+    """v + 2 sigmoid(gate_logit) * ve (utils/model.py:89-90) on bf16 v [B, T, H, D], the bf16 gate logits [B, T, H]
+    and the bf16 value embedding: sigmoid rounds to bf16, the doubling is exact, the product and the sum round."""
+    gate = 2 * bf(torch.sigmoid(gate_logit))
+    return bf(v + bf(gate.unsqueeze(-1) * ve))
+
+
+def autocast_forward(p, idx, targets=None, loss_reduction='mean', cos=None, sin=None, windows=None,
+                     accumulate=torch.float32):
+    """GPT.forward (utils/model.py:193-210) as the speedrun's scorer runs it: under CUDA bf16 autocast
+    (utils/eval.py:44-45) with the token and value embeddings stored in bf16 (utils/model.py:171-175). Every tensor
+    of the stream is bf16 and every op rounds its result to bf16 (torch computes elementwise ops in fp32):
+
+    * norm of a bf16 input (ac_norm; :196, :94, :118-119, :202);
+    * the lambda mix (ac_mix, :199);
+    * every nn.Linear: bf16 operands, accumulation in `accumulate` (fp32, as the GPU's GEMMs; fp64 gives an equally
+      valid rounding for measuring this mode's floor), bf16 output (autocast);
+    * the value gate (ac_value_gate, :89-90) and rotary (ac_rotary, :93);
+    * attention on bf16 q, k, v (attention_bf16, :95);
+    * residual adds rounded; relu(bf16).square() is an exact fp32 square (pow autocasts to fp32), rounded by the
+      c_proj's input cast (:107, :118-119);
+    * the head's bf16 logits are widened to fp32 before the cap and the cross-entropy (:203-209).
+
+    The dtype rules were checked on the MI355X box against torch 2.10's CUDA autocast: bf16 results for the mix,
+    norm, linear and sigmoid; fp32 for relu.square; the mix equals ac_mix; the mix, rotary and value-gate results
+    equal torch's CPU bf16 arithmetic bit for bit (which tests/test_oracle.py compares these helpers with)."""
+    if cos is None:
+        cos, sin = rotary_tables()
+    if windows is None:
+        windows = window_sizes()
+    B, T = idx.shape
+    cos, sin = cos[:T], sin[:T]
+
+    def lin(name, x):
+        return bf((bf(x).to(accumulate) @ bf(p[name]).to(accumulate).t()).float())
+
+    x = x0 = ac_norm(bf(p['transformer.wte.weight'])[idx])
+    for i in range(N_LAYER):
+        pre = f'transformer.h.{i}.'
+        x = ac_mix(p['resid_lambdas'][i], p['x0_lambdas'][i], x, x0)
+        h = ac_norm(x)
+        q = lin(pre + 'attn.c_q.weight', h).view(B, T, N_HEAD, HEAD_DIM)
+        k = lin(pre + 'attn.c_k.weight', h).view(B, T, N_HEAD, HEAD_DIM)
+        v = lin(pre + 'attn.c_v.weight', h).view(B, T, N_HEAD, HEAD_DIM)
+        if has_ve(i):
+            ve = bf(p[f'value_embeds.{i}.weight'])[idx].view(B, T, N_HEAD, HEAD_DIM)
+            v = ac_value_gate(v, lin(pre + 'attn.ve_gate.weight', h[..., :32]), ve)
+        q, k = ac_norm(ac_rotary(q, cos, sin)), ac_norm(ac_rotary(k, cos, sin))
+        y = attention_bf16(q, k, v, windows[i]).reshape(B, T, -1)
+        x = bf(x + lin(pre + 'attn.c_proj.weight', y))
+        m = F.relu(lin(pre + 'mlp.c_fc.weight', ac_norm(x))).square()
+        x = bf(x + lin(pre + 'mlp.c_proj.weight', m))
+    logits = lin('lm_head.weight', ac_norm(x))[..., :VOCAB]
+    logits = SOFTCAP * torch.tanh(logits / SOFTCAP)
+    if targets is None:
+        return logits
+    return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1), ignore_index=-1,
                            reduction=loss_reduction)
 
 

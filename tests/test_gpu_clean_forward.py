@@ -131,8 +131,16 @@ def test_clean_forward_sequences_and_logits_at_trained_scale():
     assert rel_err(logits, ref) < 1e-2, rel_err(logits, ref)
 
 
+def _bf16_tables(params):
+    """The reference's bf16 storage of the token and value embeddings on a GPU (utils/model.py:171-175)."""
+    for k in ['transformer.wte.weight'] + [k for k in params if k.startswith('value_embeds.')]:
+        params[k] = params[k].bfloat16().float()
+    return params
+
+
 def test_evaluate_score_matches_oracle_with_ragged_batches():
-    """utils/eval.py's evaluate: bf16 embedding storage, autocast head, fp64 sums over ragged batches."""
+    """utils/eval.py's evaluate: bf16 embedding storage, fp64 sums over ragged batches. The default rounding is
+    utils/eval.py's autocast (the autocast oracle); rounding='population' keeps the population path's."""
     from noise_amd.eval import evaluate
     model = make_model('cpu', 0)
     sd = model.state_dict()
@@ -140,9 +148,49 @@ def test_evaluate_score_matches_oracle_with_ragged_batches():
     rows = torch.stack([torch.cat([i, t[-1:]]) for i, t in (zipf_tokens(T, seed=61 + r) for r in range(n))])
     log_case(f'evaluate rows={n} T={T} batch 3')
     got = evaluate(sd, rows=rows, batch_size=3)
-    params = {k: v.detach().clone() for k, v in model.named_parameters()}
-    for k in ['transformer.wte.weight'] + [k for k in params if k.startswith('value_embeds.')]:
-        params[k] = params[k].bfloat16().float()  # the reference's bf16 embedding storage on a GPU
-    ref = torch.cat([om.population_loss(params, _zero_noise(params), torch.zeros(1), r[:-1], r[1:], mode='bf16',
-                                        head='bf16') for r in rows]).double().mean()
+    params = _bf16_tables({k: v.detach().clone() for k, v in model.named_parameters()})
+    ref = om.autocast_forward(params, rows[:, :-1], rows[:, 1:], 'none').double().mean()
     assert abs(got - float(ref)) < 1e-4, (got, float(ref))
+    got_pop = evaluate(sd, rows=rows, batch_size=3, rounding='population')
+    ref_pop = torch.cat([om.population_loss(params, _zero_noise(params), torch.zeros(1), r[:-1], r[1:], mode='bf16',
+                                            head='bf16') for r in rows]).double().mean()
+    assert abs(got_pop - float(ref_pop)) < 1e-4, (got_pop, float(ref_pop))
+
+
+@pytest.mark.parametrize('trained', [False, True])
+def test_autocast_forward_matches_the_autocast_oracle(trained):
+    """GPT.forward at utils/eval.py's rounding (bf16 autocast, bf16 tables) against oracle.model.autocast_forward.
+    Per token and for the mean: within twice the oracle's own floor (the distance to the same oracle accumulating
+    its GEMMs in fp64, an equally valid rounding) plus 1e-4; at the reference init that is the 1e-4 bar on the
+    mean. Logits within 1e-2 relative. Under torch.autocast('cuda', bfloat16) GPT.forward takes this path."""
+    from noise_amd.population import autocast_forward
+    torch.manual_seed(0)
+    model = trained_like(make_model('cpu', 0)) if trained else make_model('cpu', 0)
+    params = _bf16_tables({n: p.detach().clone() for n, p in model.named_parameters()})
+    B, T = 2, 256
+    idx, tgt = _batch(B, T, seed=71)
+    log_case(f'autocast_forward B={B} T={T} trained={trained}')
+    gm = _gpu_model(model)
+    di, dt = idx.to(DEV), tgt.to(DEV)
+    none = autocast_forward(gm, di, dt, 'none').cpu()
+    mean = autocast_forward(gm, di, dt, 'mean').cpu()
+    with torch.autocast('cuda', dtype=torch.bfloat16):
+        via_module = gm(di, dt).cpu()
+    assert torch.equal(via_module, mean)
+    ref = om.autocast_forward(params, idx, tgt, 'none')
+    ref64 = om.autocast_forward(params, idx, tgt, 'none', accumulate=torch.float64)
+    floor_tok = float((ref64 - ref).abs().max())
+    floor_mean = abs(float(ref64.double().mean() - ref.double().mean()))
+    err_tok = float((none - ref).abs().max())
+    err_mean = abs(float(mean) - float(ref.double().mean()))
+    assert err_tok <= 2 * floor_tok + 1e-4, (err_tok, floor_tok)
+    assert err_mean <= 2 * floor_mean + 1e-4, (err_mean, floor_mean)
+    if not trained:
+        assert err_mean < 1e-4, err_mean
+    # the logits are bf16 values (the head's autocast output): within 1e-2 relative, or twice the oracle's own floor
+    # where one-ulp flips upstream move more than that (reference init: 0.4e-2 of bf16 rounding per logit alone)
+    logits = autocast_forward(gm, di).cpu()
+    assert logits.shape == (B, T, 4096) and logits.dtype == torch.float32
+    ref_l = om.autocast_forward(params, idx)
+    floor_l = rel_err(om.autocast_forward(params, idx, accumulate=torch.float64), ref_l)
+    assert rel_err(logits, ref_l) <= max(1e-2, 2 * floor_l), (rel_err(logits, ref_l), floor_l)

@@ -398,15 +398,16 @@ def test_mlp_hidden_tile16_matches_rows():
     assert ((ya.cpu().float() - refa).abs() <= refa.abs() * 2 ** -7 + 1e-6).all()
 
 
-@pytest.mark.parametrize('qk_norm,qk_format', [(0, 0), (1, 0), (1, 1), (0, 1), (1, 2)])
+@pytest.mark.parametrize('qk_norm,qk_format', [(0, 0), (1, 0), (1, 1), (0, 1), (1, 2), (1, 3)])
 def test_attention_matches_oracle_and_moments(qk_norm, qk_format):
     """qk_norm = 0: any q, k (running-maximum softmax); qk_norm = 1: q, k RMS-normalised per head as the
     model's QK-norm leaves them (bounded scores, no running maximum), including rows scaled to the bound.
     qk_format 0: q and k bf16 (the credit reruns'), 1: fp16, 2: fp16 with q pre-multiplied by log2(e) / 8 (the
-    population forward's, as noise_qkv writes it); v fp16."""
+    population forward's, as noise_qkv writes it); v fp16. qk_format 3: q, k and v bf16 with bf16 probabilities
+    (the autocast clean forward's), against the oracle's bf16 attention."""
     g = torch.Generator().manual_seed(2)
     m, T = 2, 256
-    dt = torch.float16 if qk_format else torch.bfloat16
+    dt = torch.float16 if qk_format in (1, 2) else torch.bfloat16
     for window in (T, 100):
         log_case(f'attention m={m} T={T} window={window} qk_norm={qk_norm} qk_format={qk_format}')
         q, k, v = (torch.randn(m, T, 8, 64, generator=g) for _ in range(3))
@@ -414,7 +415,7 @@ def test_attention_matches_oracle_and_moments(qk_norm, qk_format):
             q, k = om.norm(q), om.norm(k)
             # extreme case: every key of the first head equal to its query direction (scores at the bound)
             k[:, :, 0] = q[:, :, 0]
-        q, k, v = q.to(dt), k.to(dt), v.half()
+        q, k, v = q.to(dt), k.to(dt), (v.bfloat16() if qk_format == 3 else v.half())
         q_in = (q.float() * (math.log2(math.e) / 8)).half() if qk_format == 2 else q
         if qk_format == 2:
             q = q_in.float() / (math.log2(math.e) / 8)  # the q the kernel sees, back in score units (fp32)
@@ -429,7 +430,10 @@ def test_attention_matches_oracle_and_moments(qk_norm, qk_format):
         _lib.call('noise_attention', qkv.data_ptr(), m, T, window, qk_norm, qk_format, bpd.data_ptr(), 0, y.data_ptr(),
                   up.data_ptr(), mom.data_ptr(), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
-        ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
+        if qk_format == 3:
+            ref = om.attention_bf16(q.float(), k.float(), v.float(), window)
+        else:
+            ref = om.bf(om.attention(q.float(), k.float(), v.float(), window))  # [m, T, 8, 64]
         got = y.cpu().float().view(m, T, 8, 64)
         assert rel_err(got, ref) < 1e-2
         assert (got - ref).abs().max() < 2e-2

@@ -413,3 +413,62 @@ def test_key_credit_through_a_permutation_filter_sums_key_gradients():
         (out_of(k)[:, (u + 1) % t] * hub[:, (u + 1) % t]).sum().backward()
         ref[:, u] = k.grad.sum(1)
     assert torch.allclose(est.double() / sigma, ref, rtol=2e-2, atol=2e-3 * float(ref.abs().max()))
+
+
+def test_autocast_helpers_equal_torch_bf16_arithmetic():
+    """The autocast oracle's elementwise rounding rules against torch's own bf16 arithmetic on the CPU, which torch
+    2.10's CUDA autocast reproduces bit for bit (checked on the MI355X box for the mix, rotary and value gate): a
+    lambda left in fp32, a dropped rounding of a product or a sum, or an eps of 2^-7 fails here."""
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(3, 16, 512, generator=g) * 0.7).bfloat16()
+    x0 = torch.randn(3, 16, 512, generator=g).bfloat16()
+    lam = torch.tensor([0.913, 0.1, 0.37])
+    assert torch.equal(om.ac_mix(lam[0], lam[2], x.float(), x0.float()), (lam[0] * x + lam[2] * x0).float())
+    # norm of a bf16 input: torch's rms_norm (fp32 compute, fp32 epsilon) -- including rows small enough for the
+    # epsilon to matter
+    small = (torch.randn(4, 512, generator=g) * 3e-4).bfloat16()
+    for t in (x, small):
+        assert torch.equal(om.ac_norm(t.float()), F.rms_norm(t, (t.shape[-1],)).float())
+    cos, sin = om.rotary_tables(16)
+    q = (torch.randn(3, 16, 8, 64, generator=g)).bfloat16()
+    c, s = cos[None, :, None, :], sin[None, :, None, :]
+    ref = torch.cat([q[..., :32] * c + q[..., 32:] * s, q[..., :32] * -s + q[..., 32:] * c], 3)
+    assert torch.equal(om.ac_rotary(q.float(), cos, sin), ref.float())
+    v = torch.randn(3, 16, 8, 64, generator=g).bfloat16()
+    z = torch.randn(3, 16, 8, generator=g).bfloat16()
+    ve = torch.randn(3, 16, 8, 64, generator=g).bfloat16()
+    ref = v + (2 * torch.sigmoid(z)).unsqueeze(-1) * ve
+    assert torch.equal(om.ac_value_gate(v.float(), z.float(), ve.float()), ref.float())
+
+
+@pytest.mark.parametrize('window', [3, 100])
+def test_bf16_attention_is_the_fp64_softmax_within_bf16_rounding(window):
+    """attention_bf16 = the fp64 masked softmax of the same bf16 q, k, v up to the bf16 probabilities and the bf16
+    output: within a few bf16 steps of the exact result, and exactly the bf16 rounding of it when the rounded
+    probabilities carry no error (one visible key per query)."""
+    g = torch.Generator().manual_seed(32)
+    B, T, H, D = 2, 9, 2, 8
+    q, k, v = (torch.randn(B, T, H, D, generator=g).bfloat16().float() for _ in range(3))
+    out = om.attention_bf16(q, k, v, window)
+    ref = om.attention(q.double(), k.double(), v.double(), window, dtype=torch.float64)
+    assert (out.double() - ref).abs().max() <= 4 * 2 ** -8 * ref.abs().max()
+    assert torch.equal(out[:, 0], om.bf(v[:, 0]))  # the first query sees only itself
+
+
+def test_autocast_forward_is_the_fp32_forward_within_bf16_rounding():
+    """The whole autocast forward against the golden-pinned fp32 forward: equal within the bf16 class at the
+    reference init (lm_head ~ N(0, 1e-6) keeps the losses near ln 4096) and at trained-scale weights, and really
+    rounded (not the fp32 forward itself)."""
+    from noise_amd.model import make_model
+    from noise_amd.synthetic import trained_like, zipf_tokens
+    torch.manual_seed(0)
+    idx, tgt = zipf_tokens(128, seed=33)
+    for model in (make_model('cpu', 0), trained_like(make_model('cpu', 0))):
+        p = {n: t.detach() for n, t in model.named_parameters()}
+        a = om.autocast_forward(p, idx[None], tgt[None], 'none')
+        b = om.gpt_forward(p, idx[None], tgt[None], 'none')
+        # per token the bf16 stream moves a trained-scale loss by up to ~0.1; the mean over tokens by ~1e-3
+        assert 0 < (a - b).abs().max() < 0.25, float((a - b).abs().max())
+        assert abs(float(a.mean() - b.mean())) < 5e-3
+    logits = om.autocast_forward(p, idx[None])
+    assert logits.dtype == torch.float32 and logits.abs().max() <= 15.0
