@@ -112,13 +112,17 @@ def run_step(args):
     from noise_amd.eggroll import Eggroll, LR, BETAS
     from noise_amd.model import make_model
     from noise_amd.optim import Adam
-    from noise_amd.synthetic import zipf_tokens
+    from noise_amd.synthetic import trained_like, zipf_tokens
 
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
     pairs = args.pairs
     P = 2 * pairs
     model = make_model(dev, 0)
+    if args.weights == 'trained':
+        # lm_head, ve_gate and the lambdas at trained-model scale (the seed-0 init leaves them degenerate: the MFMA
+        # clock depends on the operand data, so both step times are recorded)
+        trained_like(model)
     es = Eggroll(model, pairs, chunk=args.chunk, head=args.head, fitness=args.fitness, sigma=SIGMA)
     opt = Adam(model.parameters(), lr=LR, betas=BETAS, eps=1e-8)
     idx, tgt = zipf_tokens(T, seed=1)
@@ -156,7 +160,9 @@ def run_step(args):
         'scaling': 'weak',
         'vs_baseline': None,
         'dtype': 'bf16',
-        'data': 'synthetic (Zipf(1.1) tokens, seed-0 reference init, N(0,1) noise buffer)',
+        'data': 'synthetic (Zipf(1.1) tokens, ' + ('seed-0 reference init' if args.weights == 'init' else
+                                                   'seed-0 init with trained-scale lm_head, ve_gate and lambdas') +
+                ', N(0,1) noise buffer)',
         'config': {'workload': 'config4_population_step', 'members': P, 'pairs': pairs, 'tokens': T,
                    'model': '37.7M GPT (8 x 512, vocab 4096)',
                    'head': 'fp32 (bf16 hi/lo split on MFMA)' if args.head == 'fp32' else 'bf16 (autocast rounding)',
@@ -417,6 +423,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--fitness', choices=('rank', 'zscore'), default='rank',
                     help="config 4 names rank-normalised fitness; 'zscore' is the reference's (train/val/eggroll.py:151-152)")
+    ap.add_argument('--weights', choices=('init', 'trained'), default='init',
+                    help="config 4 weights: the reference's seed-0 init, or with trained-scale lm_head, ve_gate and "
+                         "lambdas (noise_amd.synthetic.trained_like)")
     ap.add_argument('--head', choices=('fp32', 'bf16'), default='fp32',
                     help="config 4 names an fp32 head; 'bf16' is the reference's autocast head (train/val/eggroll.py:99 "
                          "under :144), for comparison")
