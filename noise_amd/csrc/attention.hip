@@ -80,6 +80,36 @@ __device__ __forceinline__ int key_of_krow(int R) {
 // where rows of one parity share a bank half).
 __device__ __forceinline__ int vsw(int R) { return 2 * (((R >> 1) & 1) | ((((R >> 3) ^ R) & 1) << 1)); }
 
+// Edge-block masks as lane masks. A lane (query row r = lane % 16, lane group g = lane / 16) holds, for MFMA key block
+// kb and element e, the key kstart + 8 g + ko with ko = 32 (kb / 2) + 4 (kb % 2) + e. Against its query
+// q0 + 32 wave + 16 qb + r the causal test key <= q reads v >= t with v = r - 8 g (a per-lane constant, -24 .. 15) and
+// t = ko + t0, t0 = kstart - q0 - 32 wave - 16 qb (uniform); the window test key >= q - window reads the complement
+// v < t + window + 1. The set of lanes with v >= t depends on t alone: LANES_GE[t + 64] holds it as a 64-bit lane
+// mask for t in [-64, 80) (all lanes below -24, none above 15), so a block's 16 masks per query block come from two
+// scalar loads of 8 consecutive entries (ko = 0..7 and 32..39, t0 clamped to [-64, 40] where the masks saturate) and
+// each score costs one v_cndmask on an SGPR-pair condition instead of a compare and a select.
+constexpr int LANES_T0 = -64, LANES_N = 144;
+struct LaneMaskTable {
+  uint64_t m[LANES_N];
+};
+constexpr LaneMaskTable make_lane_masks() {
+  LaneMaskTable t{};
+  for (int i = 0; i < LANES_N; ++i) {
+    uint64_t m = 0;
+    for (int l = 0; l < 64; ++l)
+      if ((l & 15) - 8 * (l >> 4) >= i + LANES_T0) m |= uint64_t(1) << l;
+    t.m[i] = m;
+  }
+  return t;
+}
+__constant__ LaneMaskTable LANES_GE = make_lane_masks();
+// v in the lanes whose bit of `lanes` is set, w in the others
+__device__ __forceinline__ float select_lanes(float v, float w, uint64_t lanes) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(v), "s"(lanes));
+  return r;
+}
+
 __device__ __forceinline__ unsigned pack2(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
   return *reinterpret_cast<unsigned*>(&p);
@@ -188,27 +218,27 @@ __global__ void __launch_bounds__(NTH, 4) attention_kernel(AttnArgs g) {
   const pt8 ones = {(PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f};
 
   // Scores of keys a query may not see become -inf (branch-free): keys after it when the block touches the
-  // causal edge, keys more than `window` before it when the block touches the window edge. Key
-  // kstart + 8 grp + ko(kb, e) of a lane, ko = 32 (kb / 2) + 4 (kb % 2) + e a constant, is compared with
-  // dq = q - kstart - 8 grp.
+  // causal edge, keys more than `window` before it when the block touches the window edge (the lane masks of
+  // LANES_GE).
+  const float neg_inf = -INFINITY;
+  auto mask_edge = [&](f32x4 (&sq)[KB], int t0, bool keep_ge) {
+    // masks of t = t0 + ko: entries t0 .. t0 + 7 (kb 0, 1) and t0 + 32 .. t0 + 39 (kb 2, 3)
+    const uint64_t* lm = LANES_GE.m + (min(max(t0, LANES_T0), 40) - LANES_T0);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t m = lm[32 * (kb >> 1) + 4 * (kb & 1) + e];
+        sq[kb][e] = keep_ge ? select_lanes(sq[kb][e], neg_inf, m) : select_lanes(neg_inf, sq[kb][e], m);
+      }
+  };
   auto apply_mask = [&](f32x4 (&s)[2][KB], int kstart, bool causal_edge, bool window_edge) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      const int dq = q0 + 32 * wave + 16 * qb + (lane & 15) - kstart - 8 * grp, dw = dq - g.window;
-      if (causal_edge) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[qb][kb][e] = 32 * (kb >> 1) + 4 * (kb & 1) + e > dq ? -INFINITY : s[qb][kb][e];
-      }
-      if (window_edge) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[qb][kb][e] = 32 * (kb >> 1) + 4 * (kb & 1) + e < dw ? -INFINITY : s[qb][kb][e];
-      }
+      const int t0 = kstart - q0 - 32 * wave - 16 * qb;
+      // causal: keep the lanes with v >= t; window: drop the lanes with v >= t + window + 1
+      if (causal_edge) mask_edge(s[qb], t0, true);
+      if (window_edge) mask_edge(s[qb], t0 + g.window + 1, false);
     }
   };
   // Online softmax of one key block for query block qb of this wave.
