@@ -151,7 +151,7 @@ int grid_of(long M) { return (int)((M + 3) / 4); }
 }  // namespace
 
 int ac_stream_launch(const AcStreamArgs& g, hipStream_t s) {
-  if (g.M <= 0 || g.T <= 0 || (long)g.M + 3 > 0x7fffffffL * 4L) return NOISE_EINVAL;
+  if (g.M <= 0 || g.T <= 0) return NOISE_EINVAL;
   const bool need_x0 = !g.x_in || g.lambda_r;
   if (need_x0 && (!g.emb_w || !g.idx || g.V <= 0 || g.idx_mstride < 0)) return NOISE_EINVAL;
   if ((g.lambda_r == nullptr) != (g.lambda_0 == nullptr)) return NOISE_EINVAL;
