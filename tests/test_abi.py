@@ -82,6 +82,20 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     ptr, count, _keep = _lib.adam_tensors([good] * 70 + [(16, 16, 16, 16, 256, 1e-3, 0.0)])  # bc2_sqrt must be > 0
     assert lib.noise_adam_batch(ptr, count, .5, .95, 1e-8, None) == EINVAL
     assert lib.noise_attention(1, 1, 100, 50, 0, 1, None, 0, 1, None, None, None, 0, None) == EINVAL  # T % 128
+    # bf16 q, k, v with bf16 probabilities exists only for RMS-normalised q, k (the bounded-score softmax)
+    assert lib.noise_attention(16, 1, 128, 50, 0, 3, None, 0, 16, None, None, None, 0, None) == EINVAL
+    # the autocast row kernels: rows a multiple of T, something to write, lambdas in pairs, 16-byte alignment, the
+    # embedding table and ids whenever x0 is needed
+    ac = lambda x_in, wte, idx, lr, l0, x_out, h, rows=256, T=128, gate_w=None, gate=None: lib.noise_ac_stream(  # noqa
+        x_in, wte, 4096, idx, 128, None, None, lr, l0, x_out, h, gate_w, gate, rows, T, None)
+    assert ac(16, None, None, None, None, 16, 16, rows=200) == EINVAL
+    assert ac(16, None, None, None, None, None, None) == EINVAL
+    assert ac(16, 16, 16, 16, None, 16, 16) == EINVAL
+    assert ac(None, None, None, None, None, 16, 16) == EINVAL           # x0 from the table, but no table
+    assert ac(8, None, None, None, None, 16, 16) == EINVAL              # misaligned stream
+    assert ac(16, None, None, None, None, 16, None, gate_w=16, gate=16) == EINVAL  # the gate needs h
+    assert lib.noise_ac_qkv(None, 16, 16, None, None, 0, None, 0, 256, 128, None) == EINVAL
+    assert lib.noise_ac_qkv(16, 16, 16, 16, None, 4096, 16, 128, 256, 128, None) == EINVAL  # gate without table
     # the allocation-free attention refuses moments beyond its fixed array (1024 x 2048 needs 16 Mi partials)
     assert lib.noise_attention_noalloc(1, 1024, 2048, 2048, 1, 1, None, 0, 1, None, 1, None) == ENOSPC
     assert lib.noise_attention_noalloc(1, 0, 2048, 2048, 1, 1, None, 0, 1, None, 1, None) == EINVAL
