@@ -25,15 +25,17 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950), the same rounding torch uses.
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
-__device__ __forceinline__ float bf16r(float x) { return (float)(bf16)x; }
-// bf16r of two values with one v_cvt_pk_bf16_f32 for the pair, widened back by a shift and a mask. The
-// conversion is issued from inline assembly: from C++ the compiler splits the pair back into one conversion and
-// one shift per value.
-__device__ __forceinline__ void bf16r2(float a, float b, float& ra, float& rb) {
+// float(bf16(x)) in one instruction: v_cvt_pk_bf16_f32 with +0 as the low half leaves bf16(x) in the high half
+// and zeros below it, which are the fp32 bits of bf16(x). (From C++ the compiler emits a conversion and a shift.)
+__device__ __forceinline__ float bf16r(float x) {
   unsigned u;
-  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
-  ra = __uint_as_float(u << 16);
-  rb = __uint_as_float(u & 0xffff0000u);
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(u) : "v"(x));
+  return __uint_as_float(u);
+}
+// bf16r of two values (one instruction each).
+__device__ __forceinline__ void bf16r2(float a, float b, float& ra, float& rb) {
+  ra = bf16r(a);
+  rb = bf16r(b);
 }
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 // The bf16 pair {bf16(relu(a)^2), bf16(relu(b)^2)} (low half a): a |a| and b |b| rounded as a pair, whose halves
