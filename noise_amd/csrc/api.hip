@@ -456,6 +456,7 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
   c.take<float>(M);                                // h . b
   c.take<float>(M * lowrank_gemm_parts(vocab));    // partial sums of exp(z')
   c.take<float>(M);                                // z' at the target
+  if (fp32_head) c.take<bf16>((size_t)vocab * 3 * DM);  // the weight in WTILE
   *bytes = c.used;
   return NOISE_OK;
 }
@@ -480,13 +481,23 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   float* u = c.take<float>(M);
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
-  // Both operands stay row-major: WTILE / TILE16 copies of them (whole-line loads) measured 1-2% slower on this
-  // GEMM, whose column tiles of one XCD read the same weight blocks at the same time.
+  // The fp32 head's operands reach the GEMM as whole 128-byte lines: the norm writes [hi | lo] in TILE16 and the
+  // weight is copied into WTILE in the workspace (config 3: 14.06 -> 13.70 ms against row-major operands, whose
+  // 32-deep stages load half lines). Rows that do not fill whole 16-row groups, or a weight that is not 16-byte
+  // aligned, stay row-major.
+  const bool tiled = fp32_head && M % 16 == 0 && T % 16 == 0 && !((uintptr_t)w_head & 15);
+  bf16* wt = fp32_head ? c.take<bf16>((size_t)vocab * K) : nullptr;
   HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
+  hn.tiled = tiled ? 1 : 0;
   if (int rc = copy_pending(pend, npend, hn.pend)) return rc;
   hn.npend = npend;
   if (int rc = head_norm_launch(hn, s)) return rc;
-  LowrankGemmArgs g = base_args(hop, lda, (long)T * lda, w_head, K, vocab, a, sign, members, T, pair_shift);
+  if (tiled)
+    if (int rc = weight_tiles_launch(static_cast<const bf16*>(w_head), K, vocab, K, wt, s)) return rc;
+  LowrankGemmArgs g =
+      base_args(hop, lda, (long)T * lda, tiled ? wt : w_head, K, vocab, a, sign, members, T, pair_shift);
+  g.a_tiled = tiled ? 1 : 0;
+  g.w_tiled = tiled ? 1 : 0;
   g.a_fold = fp32_head ? DM : 0;
   g.u = u;
   g.u_parts = 1;

@@ -611,7 +611,7 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     if (xs_dense_supported(g)) return xs_dense_launch(g, stream);
     return launch_epi<EPI_DENSE>(g, stream);
   }
-  if (g.a_fold && (epi != EPI_CE || g.a_tiled || g.a_fold < 0 || g.a_fold % 64 || g.a_fold >= g.K))
+  if (g.a_fold && (epi != EPI_CE || g.a_fold < 0 || g.a_fold % 64 || g.a_fold >= g.K))
     return NOISE_EINVAL;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || (!g.w_tiled && (g.ldw % 8 || g.ldw < g.K)) || g.a_mstride % 8 ||

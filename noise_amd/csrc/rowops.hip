@@ -252,9 +252,18 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     Row8 lo;
 #pragma unroll
     for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
-    bf16* o = g.h + row * (2 * D) + lane * 8;
-    store8_bf16(o, x);
-    store8_bf16(o + D, lo);
+    if (g.tiled) {
+      // TILE16 of the [M, 1024] operand: element (r, c) at (r / 16) 16 1024 + (c / 32) 512 + 8 p + c % 8 with
+      // p = 4 (r % 16) + ((c % 32) / 8 ^ ((r % 16) / 2) % 4); the lane's 8 columns are one 16-byte unit
+      const int r16 = (int)(row & 15), j = lane & 3;
+      bf16* o = g.h + (row >> 4) * (16 * 2 * D) + (lane >> 2) * 512 + 8 * (4 * r16 + (j ^ ((r16 >> 1) & 3)));
+      store8_bf16(o, x);
+      store8_bf16(o + 16 * 512, lo);
+    } else {
+      bf16* o = g.h + row * (2 * D) + lane * 8;
+      store8_bf16(o, x);
+      store8_bf16(o + D, lo);
+    }
     const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
     float acc = 0.f;
 #pragma unroll
