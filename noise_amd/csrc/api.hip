@@ -456,7 +456,7 @@ int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, s
   c.take<float>(M);                                // h . b
   c.take<float>(M * lowrank_gemm_parts(vocab));    // partial sums of exp(z')
   c.take<float>(M);                                // z' at the target
-  if (fp32_head) c.take<bf16>((size_t)vocab * 3 * DM);  // the weight in WTILE
+  c.take<bf16>((size_t)vocab * (fp32_head ? 3 : 1) * DM);  // the weight in WTILE
   *bytes = c.used;
   return NOISE_OK;
 }
@@ -481,12 +481,11 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   float* u = c.take<float>(M);
   float* part = c.take<float>(M * parts);
   float* tgt = c.take<float>(M);
-  // The fp32 head's operands reach the GEMM as whole 128-byte lines: the norm writes [hi | lo] in TILE16 and the
-  // weight is copied into WTILE in the workspace (config 3: 14.06 -> 13.70 ms against row-major operands, whose
-  // 32-deep stages load half lines). Rows that do not fill whole 16-row groups, or a weight that is not 16-byte
-  // aligned, stay row-major.
-  const bool tiled = fp32_head && M % 16 == 0 && T % 16 == 0 && !((uintptr_t)w_head & 15);
-  bf16* wt = fp32_head ? c.take<bf16>((size_t)vocab * K) : nullptr;
+  // The head's operands reach the GEMM as whole 128-byte lines: the norm writes its rows ([hi | lo] for the fp32
+  // head) in TILE16 and the weight is copied into WTILE in the workspace (row-major operands' 32-deep stages load
+  // half lines). Rows that do not fill whole 16-row groups, or a weight that is not 16-byte aligned, stay row-major.
+  const bool tiled = M % 16 == 0 && T % 16 == 0 && !((uintptr_t)w_head & 15);
+  bf16* wt = c.take<bf16>((size_t)vocab * K);
   HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
   hn.tiled = tiled ? 1 : 0;
   if (int rc = copy_pending(pend, npend, hn.pend)) return rc;

@@ -87,7 +87,7 @@ struct HeadNormArgs {
   // deferred residuals added (in order) to x (fp32 only) before the norm
   Pending pend[MAX_PENDING];
   int npend;
-  int tiled;             // fp32 head: [hi | lo] written in TILE16 (16-row groups of 1 KiB tiles)
+  int tiled;             // the operand rows written in TILE16 (M % 16 == 0)
 };
 
 // Reductions of the per-token losses logsumexp(z'_t) - z'_t[target_t].

@@ -226,11 +226,8 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
 // split [hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)); the head GEMM reads them as [hi | hi | lo] (its
 // a_fold) against [W_hi | W_lo | W_hi], so one bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16
 // relative; the dot h.b is fp32. bf16 head: the operand is bf16(h) and the dot follows autocast.
-__global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
-  const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= g.M) return;
-  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+// One row of the head's norm: x (plus the deferred residuals), RMSNorm, the optional gain; 8 values per lane.
+__device__ __forceinline__ Row8 head_row(const HeadNormArgs& g, long row, int lane, int p, int dir) {
   Row8 x;
   if (g.x_bf16) {
     const bf16x8 xv = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(g.x) + row * D + lane * 8);
@@ -248,22 +245,28 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x.v[e] *= gv.v[e];
   }
+  return x;
+}
+__device__ __forceinline__ u32x4 pack_row_x4(const Row8& r) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = to_bf16(r.v[e]);
+  return __builtin_bit_cast(u32x4, o);
+}
+
+__global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  const Row8 x = head_row(g, row, lane, p, dir);
   if (g.fp32_head) {
     Row8 lo;
 #pragma unroll
     for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
-    if (g.tiled) {
-      // TILE16 of the [M, 1024] operand: element (r, c) at (r / 16) 16 1024 + (c / 32) 512 + 8 p + c % 8 with
-      // p = 4 (r % 16) + ((c % 32) / 8 ^ ((r % 16) / 2) % 4); the lane's 8 columns are one 16-byte unit
-      const int r16 = (int)(row & 15), j = lane & 3;
-      bf16* o = g.h + (row >> 4) * (16 * 2 * D) + (lane >> 2) * 512 + 8 * (4 * r16 + (j ^ ((r16 >> 1) & 3)));
-      store8_bf16(o, x);
-      store8_bf16(o + 16 * 512, lo);
-    } else {
-      bf16* o = g.h + row * (2 * D) + lane * 8;
-      store8_bf16(o, x);
-      store8_bf16(o + D, lo);
-    }
+    bf16* o = g.h + row * (2 * D) + lane * 8;
+    store8_bf16(o, x);
+    store8_bf16(o + D, lo);
     const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
     float acc = 0.f;
 #pragma unroll
@@ -275,6 +278,46 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
     store_bf(g.h + row * D + lane * 8, hb);
     const float u = dot_bf16(hb, load8(g.b + (long)dir * D + lane * 8));
     if (lane == 0) g.u[row] = u;
+  }
+}
+
+// The same rows written in TILE16 (the tile GEMM's whole-line operand layout): element (r, c) of the [M, W]
+// operand (W = 1024 for [hi | lo], 512 for the bf16 head) at (r / 16) 16 W + (c / 32) 512 + 8 q + c % 8 with
+// q = 4 (r % 16) + ((c % 32) / 8 ^ ((r % 16) / 2) % 4). A workgroup of 16 waves normalises one 16-row group, a row
+// per wave as above, into LDS, then writes the group's 16 W bf16 (one contiguous 32 or 16 KiB run) as whole lines:
+// row by row, four lanes would fill half a line each and the stores would scatter over 16 or 32 tiles.
+__global__ void __launch_bounds__(1024) head_norm_tiled_kernel(HeadNormArgs g) {
+  constexpr int UNITS = 2 * D / 8;           // 16-byte units per row of [hi | lo]
+  __shared__ u32x4 rows16[16][UNITS + 1];    // + 1: rows 16 bytes apart in the banks
+  const int lane = threadIdx.x & 63, r16 = threadIdx.x >> 6;
+  const long r0 = (long)blockIdx.x * 16, row = r0 + r16;
+  const int W = g.fp32_head ? 2 * D : D, units = W / 8;
+  const int p = (int)(row / g.T), dir = p >> g.pair_shift;
+  const Row8 x = head_row(g, row, lane, p, dir);
+  if (g.fp32_head) {
+    Row8 lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
+    rows16[r16][lane] = pack_row_x4(x);
+    rows16[r16][64 + lane] = pack_row_x4(lo);
+    const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += x.v[e] * bv.v[e];
+    acc = group_sum<64>(acc);
+    if (lane == 0) g.u[row] = acc;
+  } else {
+    const RowBf hb = pack_row(x);
+    rows16[r16][lane] = u32x4{hb.p[0], hb.p[1], hb.p[2], hb.p[3]};
+    const float u = dot_bf16(hb, load8(g.b + (long)dir * D + lane * 8));
+    if (lane == 0) g.u[row] = u;
+  }
+  __syncthreads();
+  // unit n of the group: tile n / 64, q = n % 64 -> row q / 4, 8-column chunk (q % 4) ^ ((q / 8) % 4) of the tile
+  bf16* out = g.h + r0 * W;
+  for (int n = threadIdx.x; n < 16 * units; n += 1024) {
+    const int q = n & 63, rq = q >> 2, ch = (q & 3) ^ ((rq >> 1) & 3);
+    store_stream_x4(out + 8L * n, rows16[rq][4 * (n >> 6) + ch]);
   }
 }
 
@@ -450,7 +493,12 @@ int head_norm_launch(const HeadNormArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign || bad_pending(g.pend, g.npend) ||
       (g.x_bf16 && g.npend))
     return NOISE_EINVAL;
-  hipLaunchKernelGGL(head_norm_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  if (g.tiled) {
+    if (g.M % 16) return NOISE_EINVAL;
+    hipLaunchKernelGGL(head_norm_tiled_kernel, dim3((unsigned)(g.M / 16)), dim3(1024), 0, s, g);
+  } else {
+    hipLaunchKernelGGL(head_norm_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  }
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
