@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
 // row by row, four lanes would fill half a line each and the stores would scatter over 16 or 32 tiles.
 __global__ void __launch_bounds__(1024) head_norm_tiled_kernel(HeadNormArgs g) {
   constexpr int UNITS = 2 * D / 8;           // 16-byte units per row of [hi | lo]
-  __shared__ u32x4 rows16[16][UNITS + 1];    // + 1: rows 16 bytes apart in the banks
+  // + 4 units: consecutive rows start 16 banks apart, so the 4 rows of one 16-lane read pass cover all 64 banks
+  __shared__ u32x4 rows16[16][UNITS + 4];
   const int lane = threadIdx.x & 63, r16 = threadIdx.x >> 6;
   const long r0 = (long)blockIdx.x * 16, row = r0 + r16;
   const int W = g.fp32_head ? 2 * D : D, units = W / 8;
