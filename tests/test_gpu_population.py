@@ -507,6 +507,42 @@ def test_head_ce_other_vocab_and_partial_row_tile(fp32, T):
         assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
 
 
+@pytest.mark.parametrize('fp32', [1, 0])
+def test_head_ce_tiled_and_row_major_operands_agree_bit_for_bit(fp32):
+    """The head's whole-line path (operand rows in TILE16, weight in WTILE: rows in whole 16-row groups) and its
+    row-major path (taken when T is not a multiple of 16) on the same 384 rows: 4 members x 96 tokens against 48
+    members x 8 tokens whose per-member vectors repeat the original member's. Both stage the same LDS contents and
+    contract in the same order, so the per-token losses are equal bit for bit."""
+    g = torch.Generator().manual_seed(21)
+    m, T, V, rep = 4, 96, 768, 12
+    x = torch.randn(m * T, 512, generator=g) * 3
+    W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
+    tok = torch.randint(0, V, (m * T,), generator=g)
+    s = torch.cuda.current_stream().cuda_stream
+    xd, Wd, td = x.to(DEV), W.to(DEV), tok.to(DEV)
+    wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+
+    def run(members, t, a_, b_, sign_):
+        log_case(f'head_ce members={members} T={t} fp32_head={fp32} per-token losses')
+        ad, bd, sd = (v.contiguous().to(DEV) for v in (a_, b_, sign_))
+        loss = torch.empty(members * t, device=DEV)
+        ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', members, t, V, fp32), device=DEV,
+                         dtype=torch.uint8)
+        _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
+                  sd.data_ptr(), td.data_ptr(), t, members, t, 0, _lib.CE_NONE, loss.data_ptr(), None, ws.data_ptr(),
+                  ws.numel(), None, 0, s)
+        torch.cuda.synchronize()
+        return loss.cpu()
+
+    tiled = run(m, T, a, b, sign)
+    rows = run(m * rep, T // rep, a.repeat_interleave(rep, 0), b.repeat_interleave(rep, 0), sign.repeat_interleave(rep))
+    assert torch.isfinite(tiled).all()
+    assert torch.equal(tiled, rows), (tiled - rows).abs().max()
+
+
 def test_head_ce_config3_bf16_input_with_gain():
     """Config 3: bf16 hidden states, RMSNorm gain ~ U(0.9, 1.1), fp32 head with rank-1 perturbation."""
     g = torch.Generator().manual_seed(12)
