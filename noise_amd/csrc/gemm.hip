@@ -184,14 +184,25 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
       if (g.a_fold && kt * BK >= g.a_fold) ks -= g.a_fold / BK;
     }
     const long ka = ks * a_step, kw = kt * w_step;
+    // The dense product issues its loads from inline assembly, which the compiler's wait insertion does not see:
+    // with the builtin it waits vmcnt(0) before the next LDS read at a tile's first and last steps (measured: MLP
+    // pair 23.83 -> 23.62 ms). The loop's own waits (open) order every stage read after its loads. The other
+    // epilogues keep the builtin: their M0 saves and restores cost more than the waits (config 3 13.27 -> 13.75 ms).
+    if constexpr (EPI == EPI_DENSE) {
 #pragma unroll
-    for (int d = 0; d < C::LA; ++d)
-      __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
-                                       (lds_void_t*)(sx + (wave * C::LA + d) * 512), 16, 0, 0);
+      for (int d = 0; d < C::LA; ++d) dma_x4(g.A + a_src[d] + ka, sx + (wave * C::LA + d) * 512);
 #pragma unroll
-    for (int d = 0; d < C::LB; ++d)
-      __builtin_amdgcn_global_load_lds((const void*)(b_src[d] + kw),
-                                       (lds_void_t*)(sw + (wave * C::LB + d) * 512), 16, 0, 0);
+      for (int d = 0; d < C::LB; ++d) dma_x4(b_src[d] + kw, sw + (wave * C::LB + d) * 512);
+    } else {
+#pragma unroll
+      for (int d = 0; d < C::LA; ++d)
+        __builtin_amdgcn_global_load_lds((const void*)(g.A + a_src[d] + ka),
+                                         (lds_void_t*)(sx + (wave * C::LA + d) * 512), 16, 0, 0);
+#pragma unroll
+      for (int d = 0; d < C::LB; ++d)
+        __builtin_amdgcn_global_load_lds((const void*)(b_src[d] + kw),
+                                         (lds_void_t*)(sw + (wave * C::LB + d) * 512), 16, 0, 0);
+    }
   };
 
   // ---- epilogue vectors of a tile, loaded into registers ahead of time and staged through LDS.
