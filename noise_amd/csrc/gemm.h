@@ -45,8 +45,10 @@ struct LowrankGemmArgs {
   // A operand: row r (member p = r / T, token t = r % T) starts at A + p * a_mstride + t * lda.
   // a_mstride = T * lda for per-member activations, 0 for one activation broadcast to all members.
   // a_tiled: A is TILE16 with leading dimension lda over all M rows (requires a_mstride = T * lda).
-  // a_fold > 0: the contraction index k >= a_fold reads A column k - a_fold (the fp32 head's [hi | lo] rows
-  // serve the K = 1536 product [hi | hi | lo] . [W_hi | W_lo | W_hi] without a stored second copy of hi).
+  // a_fold > 0 (the fp32 head, K = 3 a_fold): A rows are [hi | lo] and W rows [W_hi | W_lo | W_hi]; the GEMM
+  // forms hi W_hi + hi W_lo + lo W_hi with the three products interleaved per 32-deep block b: stage 3 b reads A
+  // block b and W block b, stage 3 b + 1 A block b and W block a_fold / 32 + b, stage 3 b + 2 A block
+  // a_fold / 32 + b and W block b (no stored second copy of hi; the repeated blocks come from L2).
   const __bf16* A;
   long lda;
   long a_mstride;

@@ -178,12 +178,18 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   auto issue = [&](int kt, int buf) {
     bf16* sx = smem + buf * C::STAGE;
     bf16* sw = sx + BM * BK;
-    // A stage of this k stage (a_fold, the head only: the contraction index k >= a_fold reads column k - a_fold)
-    int ks = kt;
+    // The fp32 head (a_fold): A = [hi | lo] and W = [W_hi | W_lo | W_hi]; its three products hi W_hi, hi W_lo and
+    // lo W_hi run interleaved per 32-deep block b (stages 3 b, 3 b + 1, 3 b + 2), so the second read of an A_hi
+    // block and of a W_hi block comes one or two stages after the first, from L2.
+    int ks = kt, kwt = kt;
     if constexpr (EPI == EPI_CE) {
-      if (g.a_fold && kt * BK >= g.a_fold) ks -= g.a_fold / BK;
+      if (g.a_fold) {
+        const int blk = kt / 3, pass = kt - 3 * blk, nb = g.a_fold / BK;
+        ks = pass == 2 ? nb + blk : blk;
+        kwt = pass == 1 ? nb + blk : blk;
+      }
     }
-    const long ka = ks * a_step, kw = kt * w_step;
+    const long ka = ks * a_step, kw = kwt * w_step;
     // The dense product issues its loads from inline assembly, which the compiler's wait insertion does not see:
     // with the builtin it waits vmcnt(0) before the next LDS read at a tile's first and last steps (measured: MLP
     // pair 23.83 -> 23.62 ms). The loop's own waits (open) order every stage read after its loads. The other
@@ -622,7 +628,7 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     if (xs_dense_supported(g)) return xs_dense_launch(g, stream);
     return launch_epi<EPI_DENSE>(g, stream);
   }
-  if (g.a_fold && (epi != EPI_CE || g.a_fold < 0 || g.a_fold % 64 || g.a_fold >= g.K))
+  if (g.a_fold && (epi != EPI_CE || g.a_fold < 0 || g.a_fold % 64 || g.K != 3 * g.a_fold))
     return NOISE_EINVAL;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || (!g.w_tiled && (g.ldw % 8 || g.ldw < g.K)) || g.a_mstride % 8 ||

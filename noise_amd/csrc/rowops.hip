@@ -223,9 +223,9 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
 }
 
 // Final norm feeding the head (train/val/eggroll.py:94-99). fp32 head: the operand rows are the bf16
-// split [hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)); the head GEMM reads them as [hi | hi | lo] (its
-// a_fold) against [W_hi | W_lo | W_hi], so one bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16
-// relative; the dot h.b is fp32. bf16 head: the operand is bf16(h) and the dot follows autocast.
+// split [hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)); the head GEMM forms hi W_hi + hi W_lo + lo W_hi from
+// them (its a_fold), so one bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16 relative; the dot h.b is fp32.
+// bf16 head: the operand is bf16(h) and the dot follows autocast.
 // One row of the head's norm: x (plus the deferred residuals), RMSNorm, the optional gain; 8 values per lane.
 __device__ __forceinline__ Row8 head_row(const HeadNormArgs& g, long row, int lane, int p, int dir) {
   Row8 x;
