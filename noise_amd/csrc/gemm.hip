@@ -106,8 +106,6 @@ __device__ __forceinline__ void store_f4(void* p, float a, float b, float c, flo
   *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
 }
 
-__device__ __forceinline__ float bf16_lo(unsigned v) { return __uint_as_float(v << 16); }
-__device__ __forceinline__ float bf16_hi(unsigned v) { return __uint_as_float(v & 0xffff0000u); }
 __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   bf16x2 p = {to_bf16(a), to_bf16(b)};
   return *reinterpret_cast<unsigned*>(&p);
