@@ -134,9 +134,10 @@ __global__ void __launch_bounds__(512, 2) xs_kernel(const LowrankGemmArgs g) {
   constexpr int FIRST_STORE = QK ? 2 : 1;
   __shared__ __attribute__((aligned(16))) char smem[NB * XBYTES];
   __shared__ __attribute__((aligned(16))) char svec[NB][NW][VEC];
-  __shared__ __attribute__((aligned(16))) float red[2][R][NW];
+  // per-row partials padded to 12 floats: the 16 rows one instruction touches fall in distinct banks
+  __shared__ __attribute__((aligned(16))) float red[2][R][NW + 4];
   __shared__ __attribute__((aligned(16))) QkVec qv[NB];
-  __shared__ __attribute__((aligned(16))) float ssq[2][R][NW];  // q|k: per-row partial sums of squares
+  __shared__ __attribute__((aligned(16))) float ssq[2][R][NW + 4];  // q|k: per-row partial sums of squares
   __shared__ __attribute__((aligned(16))) float qpad[R][4];     // q|k: landing area of the padding loads
   __shared__ __attribute__((aligned(16))) VeVec vv[NB];         // value embedding: per-block vectors
   __shared__ __attribute__((aligned(16))) VeRows ver[NW];       // value embedding: each wave's gathered rows
