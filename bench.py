@@ -164,10 +164,10 @@ def run_step(args):
                                                    'seed-0 init with trained-scale lm_head, ve_gate and lambdas') +
                 ', N(0,1) noise buffer)',
         'config': {'workload': 'config4_population_step', 'members': P, 'pairs': pairs, 'tokens': T,
-                   'model': '37.7M GPT (8 x 512, vocab 4096)',
+                   'layers': 8, 'd_model': 512, 'vocab': 4096,
                    'head': 'fp32 (bf16 hi/lo split on MFMA)' if args.head == 'fp32' else 'bf16 (autocast rounding)',
                    'sigma': SIGMA, 'fitness': args.fitness, 'optimizer': 'Adam (HIP)', 'chunk_members': args.chunk,
-                   'parallelism': 'single GPU'},
+                   'gpus': 1},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': roofline_traffic(args.chunk),
                      'kernel': 'fused relu^2 MLP: xs_relu2_kernel (c_fc, weight-resident) + lowrank_gemm<EPI_DENSE> (c_proj)',
@@ -221,7 +221,7 @@ def run_mlp(args):
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
         'config': {'workload': 'config1_fused_relu2_mlp_rank1', 'members': P, 'pairs': pairs, 'tokens': T,
                    'd_model': D, 'd_hidden': F, 'sigma': SIGMA, 'x': 'shared [2048, 512]', 'output': 'bf16',
-                   'parallelism': 'single GPU'},
+                   'gpus': 1},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None,
                      'kernel': 'noise_lowrank_mlp (rowdot + xs_relu2_kernel + lowrank_gemm<EPI_STORE> proj)',
@@ -284,7 +284,7 @@ def run_attention(args):
                    {'workload': 'config2_attention_moments', 'members': P, 'heads': 8, 'tokens': T, 'head_dim': 64,
                     'window': window, 'q_k': 'RMS-normalised rows (QK-norm)' if args.qk_norm else 'N(0,1)',
                     'outputs': 'y bf16, c_proj dot partials, per-head mean of y and y^2',
-                    'parallelism': 'single GPU'},
+                    'gpus': 1},
                    {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None, 'kernel': 'attention_kernel + moments_reduce',
                     'flop_per_launch': flop, 'ms_per_launch': ms_launch})
@@ -319,7 +319,7 @@ def run_head(args):
     achieved = flop / (ms_launch * 1e-3) / 1e12
     return _common(args, P * T / (ms_step * 1e-3), ms_step,
                    {'workload': 'config3_norm_head_ce', 'members': P, 'tokens': T, 'd_model': D, 'vocab': V,
-                    'head': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'sigma': SIGMA, 'parallelism': 'single GPU'},
+                    'head': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'sigma': SIGMA, 'gpus': 1},
                    {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None,
                     'kernel': 'head_norm + lowrank_gemm<EPI_CE> + ce_finalize', 'flop_per_launch': flop,
