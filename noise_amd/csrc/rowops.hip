@@ -134,6 +134,8 @@ __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
 
 // Block entry (train/val/eggroll.py:77-88): x = (l_r + s e_r) x + (l_0 + s e_0) x0; h = norm(x);
 // q/k/v input-side dots; the value-embedding gate 2 sigmoid(lowrank(h[:32], ve_gate)).
+// FIRST: block 0 (no incoming stream, no deferred residuals, x0 recomputed): fewer live registers, twice the waves
+template <bool FIRST>
 __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -143,7 +145,7 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   // loads, the token id before the embedding row, not for the sum of all of them).
   // x0: stored, or recomputed from the embedding (2 KiB gathered from an L2-resident table instead of 2 KiB
   // streamed from HBM); block 0 mixes x0 with itself
-  const bool recompute = !g.x0;
+  const bool recompute = FIRST || !g.x0;
   long tok = 0;
   Row8 x0, xin, eb, bqkv[3];
   if (recompute) {
@@ -152,19 +154,20 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   } else {
     x0 = load8(g.x0 + row * D + lane * 8);
   }
-  if (g.x_in) xin = load8(g.x_in + row * D + lane * 8);
+  if (!FIRST && g.x_in) xin = load8(g.x_in + row * D + lane * 8);
   PendRow pr;
-  load_pending(pr, g.pend, g.npend, row, dir, lane);
+  if (!FIRST) load_pending(pr, g.pend, g.npend, row, dir, lane);
 #pragma unroll
   for (int k = 0; k < 3; ++k) bqkv[k] = load8(g.b_qkv[k] + (long)dir * D + lane * 8);
   const float s = g.sign[p];
   const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
   if (recompute) x0 = embed_finish(g.emb, tok, dir, s, eb, lane);
-  Row8 x = g.x_in ? xin : x0;
-  add_pending(x, pr, g.pend, g.npend, s);
+  Row8 x = (!FIRST && g.x_in) ? xin : x0;
+  if (!FIRST) add_pending(x, pr, g.pend, g.npend, s);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) x.v[e] = lr * x.v[e] + l0 * x0.v[e];
+  // one fixed contraction (an fma with the x0 product rounded first), the same in both instances
+  for (int e = 0; e < 8; ++e) x.v[e] = fmaf(lr, x.v[e], l0 * x0.v[e]);
   store8(g.x_out + row * D + lane * 8, x);
   rms_norm_row(x);
   const RowBf hb = pack_row(x);
@@ -477,7 +480,10 @@ int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
   if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate || (((uintptr_t)g.gate_w | (uintptr_t)g.gate_b) & 15)))
     return NOISE_EINVAL;
   if (bad_pending(g.pend, g.npend)) return NOISE_EINVAL;
-  hipLaunchKernelGGL(block_entry_kernel, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  if (!g.x_in && !g.x0 && !g.npend)
+    hipLaunchKernelGGL(block_entry_kernel<true>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(block_entry_kernel<false>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
