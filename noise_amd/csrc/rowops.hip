@@ -78,16 +78,22 @@ struct PendRow {
   float uq[MAX_PENDING];  // lane q: partial q
   Row8 a[MAX_PENDING];
 };
-__device__ __forceinline__ void load_pending(PendRow& L, const Pending* pend, int npend, long row, int dir, int lane) {
+// a0, a1: the deferred residuals' a vectors of the row's direction
+__device__ __forceinline__ void load_pending(PendRow& L, const Pending* pend, int npend, long row, int lane,
+                                             const float* a0, const float* a1) {
 #pragma unroll
   for (int k = 0; k < MAX_PENDING; ++k) {
     if (k < npend) {
       const Pending& pd = pend[k];
       L.y[k] = *reinterpret_cast<const bf16x8*>(pd.y + row * D + lane * 8);
       L.uq[k] = lane < pd.u_parts ? pd.u[row * pd.u_ld + lane * pd.u_qstride] : 0.f;
-      L.a[k] = load8(pd.a + (long)dir * D + lane * 8);
+      if (k ? a1 : a0) L.a[k] = load8((k ? a1 : a0) + lane * 8);
     }
   }
+}
+__device__ __forceinline__ void load_pending(PendRow& L, const Pending* pend, int npend, long row, int dir, int lane) {
+  load_pending(L, pend, npend, row, lane, npend > 0 ? pend[0].a + (long)dir * D : nullptr,
+               npend > 1 ? pend[1].a + (long)dir * D : nullptr);
 }
 __device__ __forceinline__ void add_pending(Row8& x, const PendRow& L, const Pending* pend, int npend, float s) {
 #pragma unroll
@@ -134,12 +140,14 @@ __global__ void __launch_bounds__(256) embed_norm_kernel(EmbedNormArgs g) {
 
 // Block entry (train/val/eggroll.py:77-88): x = (l_r + s e_r) x + (l_0 + s e_0) x0; h = norm(x);
 // q/k/v input-side dots; the value-embedding gate 2 sigmoid(lowrank(h[:32], ve_gate)).
-// FIRST: block 0 (no incoming stream, no deferred residuals, x0 recomputed): fewer live registers, twice the waves
-template <bool FIRST>
-__global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
-  const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= g.M) return;
+// One row per wave. FIRST: block 0 (no incoming stream, no deferred residuals, x0 recomputed): fewer live registers,
+// twice the waves.
+// LATE: the vectors live in LDS and each is read just before its use (compiler barriers keep the reads there), so
+// a wave holds only its row's data.
+template <bool FIRST, bool LATE = false>
+__device__ __forceinline__ void block_entry_row(const BlockEntryArgs& g, long row, int lane, const float* const (&vec)[6]) {
+  // vec: the member's vectors for this row (global memory or the workgroup's LDS copy): the embedding's b, b_q,
+  // b_k, b_v, and the deferred residuals' a
   const int p = (int)(row / g.T), t = (int)(row % g.T), dir = p >> g.pair_shift;
   // Every load that depends on no other is issued first (the row then waits for its longest chain of dependent
   // loads, the token id before the embedding row, not for the sum of all of them).
@@ -150,31 +158,41 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   Row8 x0, xin, eb, bqkv[3];
   if (recompute) {
     tok = g.emb.idx[(long)p * g.emb.mstride + t];
-    eb = load8(g.emb.b + (long)dir * D + lane * 8);
+    if (!LATE) eb = load8(vec[0] + lane * 8);
   } else {
     x0 = load8(g.x0 + row * D + lane * 8);
   }
   if (!FIRST && g.x_in) xin = load8(g.x_in + row * D + lane * 8);
   PendRow pr;
-  if (!FIRST) load_pending(pr, g.pend, g.npend, row, dir, lane);
+  if (!FIRST) load_pending(pr, g.pend, g.npend, row, lane, LATE ? nullptr : vec[4], LATE ? nullptr : vec[5]);
+  if (!LATE) {
 #pragma unroll
-  for (int k = 0; k < 3; ++k) bqkv[k] = load8(g.b_qkv[k] + (long)dir * D + lane * 8);
+    for (int k = 0; k < 3; ++k) bqkv[k] = load8(vec[1 + k] + lane * 8);
+  }
   const float s = g.sign[p];
   const float lr = g.lambda_r[0] + s * g.eps_r[(long)dir * g.eps_ld];
   const float l0 = g.lambda_0[0] + s * g.eps_0[(long)dir * g.eps_ld];
-  if (recompute) x0 = embed_finish(g.emb, tok, dir, s, eb, lane);
+  if (LATE) asm volatile("" ::: "memory");
+  if (recompute) x0 = embed_finish(g.emb, tok, dir, s, LATE ? load8(vec[0] + lane * 8) : eb, lane);
   Row8 x = (!FIRST && g.x_in) ? xin : x0;
-  if (!FIRST) add_pending(x, pr, g.pend, g.npend, s);
+  if (LATE) {
+    asm volatile("" ::: "memory");
 #pragma unroll
-  // one fixed contraction (an fma with the x0 product rounded first), the same in both instances
+    for (int k = 0; k < MAX_PENDING; ++k)
+      if (k < g.npend) pr.a[k] = load8(vec[4 + k] + lane * 8);
+  }
+  if (!FIRST) add_pending(x, pr, g.pend, g.npend, s);
+  // one fixed contraction (an fma with the x0 product rounded first), the same in every instance
+#pragma unroll
   for (int e = 0; e < 8; ++e) x.v[e] = fmaf(lr, x.v[e], l0 * x0.v[e]);
   store8(g.x_out + row * D + lane * 8, x);
   rms_norm_row(x);
   const RowBf hb = pack_row(x);
   store_bf(g.h + row * D + lane * 8, hb);
   float u[3];
+  if (LATE) asm volatile("" ::: "memory");
 #pragma unroll
-  for (int k = 0; k < 3; ++k) u[k] = dot_bf16(hb, bqkv[k]);
+  for (int k = 0; k < 3; ++k) u[k] = dot_bf16(hb, LATE ? load8(vec[1 + k] + lane * 8) : bqkv[k]);
   if (lane == 0) {
     float* ur = g.u_qkv + row * 4;
     ur[0] = u[0], ur[1] = u[1], ur[2] = u[2], ur[3] = s;  // the member's sign rides with the dots
@@ -203,6 +221,44 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
       const float gl = bf16r(z) + s * bf16r(ub) * g.gate_a[(long)dir * 8 + hh];
       g.gate[row * 8 + hh] = 2.f / (1.f + __expf(-gl));
     }
+  }
+}
+template <bool FIRST>
+__global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  const int dir = (int)(row / g.T) >> g.pair_shift;
+  const long vo = (long)dir * D;
+  const float* const vec[6] = {!g.x0 ? g.emb.b + vo : nullptr, g.b_qkv[0] + vo, g.b_qkv[1] + vo,
+                               g.b_qkv[2] + vo, g.npend > 0 ? g.pend[0].a + vo : nullptr,
+                               g.npend > 1 ? g.pend[1].a + vo : nullptr};
+  block_entry_row<FIRST>(g, row, lane, vec);
+}
+// GROUP_ROWS rows of one member per workgroup (T % GROUP_ROWS == 0), GROUP_ROWS / 4 per wave in turn: the member's
+// six vectors (12 KiB) are staged in LDS once per workgroup (384 B per row) instead of being read from L2 by every
+// row (12 KiB per row). Layers after the first take this instance; the result is bit for bit the per-row kernel's.
+constexpr int GROUP_ROWS = 32;
+__global__ void __launch_bounds__(256) block_entry_group_kernel(BlockEntryArgs g) {
+  __shared__ __attribute__((aligned(16))) float svec[6][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long row0 = (long)blockIdx.x * GROUP_ROWS;
+  const int dir = (int)(row0 / g.T) >> g.pair_shift;
+  const long vo = (long)dir * D;
+  const float* src[6] = {!g.x0 ? g.emb.b : nullptr, g.b_qkv[0], g.b_qkv[1], g.b_qkv[2],
+                         g.npend > 0 ? g.pend[0].a : nullptr, g.npend > 1 ? g.pend[1].a : nullptr};
+  for (int i = threadIdx.x; i < 6 * (D / 4); i += 256) {
+    const int v = i / (D / 4), q = i - v * (D / 4);
+    if (src[v]) *reinterpret_cast<float4*>(&svec[v][4 * q]) = *reinterpret_cast<const float4*>(src[v] + vo + 4 * q);
+  }
+  __syncthreads();
+  const float* const vec[6] = {svec[0], svec[1], svec[2], svec[3], svec[4], svec[5]};
+  // one row at a time; the compiler barrier keeps each row's vector reads from LDS inside its iteration (hoisted, the
+  // six vectors would stay live in registers across the loop)
+#pragma unroll 1
+  for (int k = 0; k < GROUP_ROWS / 4; ++k) {
+    asm volatile("" ::: "memory");
+    block_entry_row<false, true>(g, row0 + wave * (GROUP_ROWS / 4) + k, lane, vec);
   }
 }
 
@@ -482,6 +538,8 @@ int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
   if (bad_pending(g.pend, g.npend)) return NOISE_EINVAL;
   if (!g.x_in && !g.x0 && !g.npend)
     hipLaunchKernelGGL(block_entry_kernel<true>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
+  else if (g.T % GROUP_ROWS == 0 && g.M % GROUP_ROWS == 0)
+    hipLaunchKernelGGL(block_entry_group_kernel, dim3((unsigned)(g.M / GROUP_ROWS)), dim3(256), 0, s, g);
   else
     hipLaunchKernelGGL(block_entry_kernel<false>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();

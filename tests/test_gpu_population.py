@@ -335,6 +335,61 @@ def test_deferred_residuals_match_eager_lowrank():
     # x itself is not written by the MLP entry
     assert torch.equal(dev['x'].cpu(), x)
 
+
+def test_block_entry_grouped_and_per_row_instances_agree_bit_for_bit():
+    """The block entry at T = 96 (workgroups of 32 rows of one member, the member's vectors staged in LDS) and the
+    same rows cut into T = 8 members (one row per wave, vectors read per row) write the same x, h, dots and gates,
+    bit for bit: with deferred residuals, the value-embedding gate and x0 both stored and recomputed."""
+    g = torch.Generator().manual_seed(21)
+    m, T, D, V, R = 4, 96, 512, 4096, 12  # R: members of the cut layout per member
+    M = m * T
+    x, x0 = torch.randn(M, D, generator=g) * 3, torch.randn(M, D, generator=g)
+    y1, y2 = (torch.randn(M, D, generator=g).bfloat16() for _ in range(2))
+    u1, u2 = torch.randn(M, 8, generator=g), torch.randn(8, M, generator=g)
+    sign = antithetic_signs(m, 0.05)
+    lr, l0 = torch.tensor([0.9]), torch.tensor([0.3])
+    # per-direction vectors of the grouped layout (pair_shift 1: m // 2 directions)
+    vec = dict(a1=torch.randn(m // 2, D, generator=g), a2=torch.randn(m // 2, D, generator=g),
+               er=torch.randn(m // 2, 8, generator=g), e0=torch.randn(m // 2, 8, generator=g),
+               bq=torch.randn(m // 2, D, generator=g), bk=torch.randn(m // 2, D, generator=g),
+               bv=torch.randn(m // 2, D, generator=g), ga=torch.randn(m // 2, 8, generator=g),
+               gb=torch.randn(m // 2, 32, generator=g), eb=torch.randn(m // 2, D, generator=g))
+    gw = torch.randn(8, 32, generator=g) * 0.2
+    w, ea = torch.randn(V, D, generator=g), torch.randn(m // 2, V, generator=g)
+    idx, _ = zipf_tokens(T, seed=5)
+    idx = idx.repeat(m)  # a sequence per member: member p reads idx[p T .. p T + T)
+    s = torch.cuda.current_stream().cuda_stream
+    common = {k: t.to(DEV) for k, t in dict(x=x, x0=x0, y1=y1, y2=y2, u1=u1, u2=u2, lr=lr, l0=l0, gw=gw, w=w,
+                                             idx=idx).items()}
+    out = {}
+    for layout, (mm, TT, ps, rep) in dict(grouped=(m, T, 1, 1), per_row=(m * R, T // R, 0, 2 * R)).items():
+        # the cut layout's member p' = R p + j is its own direction (pair_shift 0) carrying direction p // 2's vectors
+        d = {k: v.repeat_interleave(rep, 0).to(DEV) for k, v in vec.items()}
+        d['ea'] = ea.repeat_interleave(rep, 0).to(DEV)
+        d['sign'] = sign.repeat_interleave(R if layout == 'per_row' else 1).to(DEV)
+        p1 = (common['y1'].data_ptr(), common['u1'].data_ptr(), 8, 8, 1, d['a1'].data_ptr())
+        p2 = (common['y2'].data_ptr(), common['u2'].data_ptr(), 8, 1, M, d['a2'].data_ptr())
+        pend, npend = _lib.pending(p1, p2)
+        emb, emb_ptr = _lib.embed(common['w'].data_ptr(), V, d['ea'].data_ptr(), d['eb'].data_ptr(),
+                                  common['idx'].data_ptr(), TT)
+        for x0_mode in ('stored', 'recomputed'):
+            log_case(f'block_entry {layout} m={mm} T={TT} x0 {x0_mode}')
+            stored = x0_mode == 'stored'
+            xo, h = torch.empty(M, D, device=DEV), torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
+            u, gate = torch.empty(M, 4, device=DEV), torch.empty(M, 8, device=DEV)
+            _lib.call('noise_block_entry', common['x'].data_ptr(), common['x0'].data_ptr() if stored else None,
+                      xo.data_ptr(), h.data_ptr(), u.data_ptr(), d['bq'].data_ptr(), d['bk'].data_ptr(),
+                      d['bv'].data_ptr(), common['lr'].data_ptr(), common['l0'].data_ptr(), d['er'].data_ptr() + 4 * 3,
+                      d['e0'].data_ptr() + 4 * 3, 8, common['gw'].data_ptr(), d['ga'].data_ptr(), d['gb'].data_ptr(),
+                      gate.data_ptr(), d['sign'].data_ptr(), mm, TT, ps, pend, npend, None if stored else emb_ptr, s)
+            torch.cuda.synchronize()
+            out[layout, x0_mode] = (xo.cpu(), h.cpu(), u.cpu(), gate.cpu())
+    for x0_mode in ('stored', 'recomputed'):
+        for a_, b_ in zip(out['grouped', x0_mode], out['per_row', x0_mode]):
+            assert torch.equal(a_, b_), x0_mode
+    # the recomputed x0 is a different x0 from the stored one: the two modes must differ
+    assert not torch.equal(out['grouped', 'stored'][0], out['grouped', 'recomputed'][0])
+
 def test_mlp_hidden_tile16_matches_rows():
     """noise_mlp_fc writes the same hidden (bit for bit, up to the layout) and the same partials in TILE16 as in
     ROWS, and noise_dense_bf16 on the TILE16 hidden returns exactly its result on the row-major one, with the
