@@ -34,6 +34,10 @@ METRIC = 'perturbed member-tokens/sec on 1 GPU; fused-MLP MFMA % of bf16 peak'
 PEAK_BF16_TFLOPS = 2500.0         # MI355X dense bf16 MFMA
 D, F, T, V, L = 512, 2048, 2048, 4096, 8
 SIGMA = 1e-3
+# head formats (noise_head_ce's NOISE_HEAD_*) and how each runs
+HEAD_FORMAT = {'fp32': 2, 'fp32_split': 1, 'bf16': 0}
+HEAD_DESC = {'fp32': 'fp32 (fp16 h x fp16 hi/lo weight: 2 MFMA passes)',
+             'fp32_split': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'bf16': 'bf16 (autocast rounding)'}
 MLP_FLOP_PER_MEMBER_TOKEN = 2 * (2 * D * F)  # both MLP GEMMs, counted per member
 # per member-token algorithmic FLOPs of the forward: dense GEMMs (q, k, v, proj, fc, mlp proj per layer,
 # ve_gate, head) and window-aware attention at T = 2048 (QK^T and PV over the visible keys)
@@ -165,7 +169,7 @@ def run_step(args):
                 ', N(0,1) noise buffer)',
         'config': {'workload': 'config4_population_step', 'members': P, 'pairs': pairs, 'tokens': T,
                    'layers': 8, 'd_model': 512, 'vocab': 4096,
-                   'head': 'fp32 (bf16 hi/lo split on MFMA)' if args.head == 'fp32' else 'bf16 (autocast rounding)',
+                   'head': HEAD_DESC[args.head],
                    'sigma': SIGMA, 'fitness': args.fitness, 'optimizer': 'Adam (HIP)', 'chunk_members': args.chunk,
                    'gpus': 1},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
@@ -305,24 +309,29 @@ def run_head(args):
     sign = antithetic_signs(P, SIGMA).to(dev)
     tgt = zipf_tokens(T, seed=1)[1].to(dev)
     s = torch.cuda.current_stream().cuda_stream
-    wsplit = torch.empty(V, 3 * D, device=dev, dtype=torch.bfloat16)
-    _lib.call('noise_cast_bf16', W.data_ptr(), wsplit.data_ptr(), W.numel(), D, s)
+    fmt = HEAD_FORMAT[args.head]
+    if fmt == _lib.HEAD_FP32:
+        w_op = W  # the call derives its fp16 operand from the fp32 weight
+    else:
+        w_op = torch.empty(V, 3 * D if fmt == _lib.HEAD_FP32_SPLIT else D, device=dev, dtype=torch.bfloat16)
+        _lib.call('noise_cast_bf16', W.data_ptr(), w_op.data_ptr(), W.numel(), D if fmt == _lib.HEAD_FP32_SPLIT else 0, s)
     loss = torch.empty(P, device=dev)
-    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', P, T, V, 1), device=dev, dtype=torch.uint8)
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', P, T, V, fmt), device=dev, dtype=torch.uint8)
 
     def step():
-        _lib.call('noise_head_ce', h.data_ptr(), 1, gain.data_ptr(), wsplit.data_ptr(), V, 1, a.data_ptr(),
+        _lib.call('noise_head_ce', h.data_ptr(), 1, gain.data_ptr(), w_op.data_ptr(), V, fmt, a.data_ptr(),
                   b.data_ptr(), sign.data_ptr(), tgt.data_ptr(), 0, P, T, 1, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None,
                   ws.data_ptr(), ws.numel(), None, 0, s)
     ms_step, ms_launch = _timed(step, args.steps, args.warmup)
-    flop = 2 * D * V * P * T  # algorithmic fp32 head FLOPs (run as 3 bf16 MFMA passes)
+    flop = 2 * D * V * P * T  # algorithmic fp32 head FLOPs (run as 2 fp16 or 3 bf16 MFMA passes)
     achieved = flop / (ms_launch * 1e-3) / 1e12
     return _common(args, P * T / (ms_step * 1e-3), ms_step,
                    {'workload': 'config3_norm_head_ce', 'members': P, 'tokens': T, 'd_model': D, 'vocab': V,
-                    'head': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'sigma': SIGMA, 'gpus': 1},
+                    'head': HEAD_DESC[args.head], 'sigma': SIGMA, 'gpus': 1},
                    {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                     'frac': achieved / PEAK_BF16_TFLOPS, 'traffic': None,
-                    'kernel': 'head_norm + lowrank_gemm<EPI_CE> + ce_finalize', 'flop_per_launch': flop,
+                    'kernel': 'head_norm + lowrank_gemm<EPI_CE%s> + ce_finalize' % ('_F16' if fmt == _lib.HEAD_FP32 else ''),
+                    'flop_per_launch': flop,
                     'ms_per_launch': ms_launch})
 
 
@@ -426,9 +435,10 @@ def main():
     ap.add_argument('--weights', choices=('init', 'trained'), default='init',
                     help="config 4 weights: the reference's seed-0 init, or with trained-scale lm_head, ve_gate and "
                          "lambdas (noise_amd.synthetic.trained_like)")
-    ap.add_argument('--head', choices=('fp32', 'bf16'), default='fp32',
-                    help="config 4 names an fp32 head; 'bf16' is the reference's autocast head (train/val/eggroll.py:99 "
-                         "under :144), for comparison")
+    ap.add_argument('--head', choices=tuple(HEAD_DESC), default='fp32',
+                    help="configs 3 and 4 name an fp32 head: 'fp32' (fp16 h against a 22-bit fp16 hi/lo weight) or "
+                         "'fp32_split' (bf16 hi/lo, ~2^-16); 'bf16' is the reference's autocast head "
+                         "(train/val/eggroll.py:99 under :144), for comparison")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: every box in this build has a single MI355X; --gpus {args.gpus} '

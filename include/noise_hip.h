@@ -39,6 +39,14 @@ extern "C" {
 #define NOISE_CE_SUM 2         /* loss[1]: sum over the tokens whose target is not -1 */
 #define NOISE_CE_MEAN 3        /* loss[1]: that sum over their count (NaN when none is valid) */
 
+/* Head formats of noise_head_ce (its fp32_head argument). */
+#define NOISE_HEAD_BF16 0       /* w_head bf16 [vocab, 512]: the reference's autocast head (one bf16 GEMM) */
+#define NOISE_HEAD_FP32_SPLIT 1 /* w_head bf16 [vocab, 1536] from noise_cast_bf16(split_cols = 512): fp32 head as three
+                                 * bf16 products, ~2^-16 relative */
+#define NOISE_HEAD_FP32 2       /* w_head fp32 [vocab, 512] (16-byte aligned): fp32 head as two fp16 products, h
+                                 * rounded once to fp16 (11 significant bits, TF32's) against a 22-bit split of
+                                 * the weight */
+
 typedef void* noise_stream_t; /* hipStream_t */
 
 /* Layouts of a bf16 activation [rows, cols] exchanged between entry points. */
@@ -269,9 +277,8 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
  * [members*T, vocab] (GPT.forward without targets); targets and loss may then both be null.
  *   x       [members*T, 512] fp32 (x_bf16 == 0) or bf16 (x_bf16 != 0)
  *   gain    [512] fp32 or null
- *   fp32_head != 0: w_head is the [vocab, 1536] split operand from noise_cast_bf16(split_cols = 512)
- *                   and the head is fp32-accurate (~2^-16 relative); 0: w_head bf16 [vocab, 512]
- *                   with the reference's autocast rounding points.
+ *   fp32_head  NOISE_HEAD_*: the format of w_head and the precision of z (the fp32 formats keep the dot h . b
+ *              and the rank-1 term in fp32; NOISE_HEAD_BF16 follows the reference's autocast rounding points).
  * vocab % 256 == 0. Workspace: noise_head_ce_workspace_size(). The npend (<= 2) deferred residuals in
  * pend are added to an fp32 x, in order, before the norm (the last block's c_proj outputs). */
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes);

@@ -20,6 +20,7 @@ FITNESS_ZSCORE, FITNESS_RANK = 0, 1
 QK_BF16, QK_F16, QK_F16_Q_LOG2, QK_BF16_V_BF16 = 0, 1, 2, 3
 LAYOUT_ROWS, LAYOUT_TILE16, LAYOUT_WTILE = 0, 1, 2
 CE_MEMBER_MEAN, CE_NONE, CE_SUM, CE_MEAN = 0, 1, 2, 3
+HEAD_BF16, HEAD_FP32_SPLIT, HEAD_FP32 = 0, 1, 2  # noise_head_ce's weight formats (NOISE_HEAD_*)
 
 # name -> argtypes in declaration order; every entry point returns int. Pointers (device buffers,
 # the stream) are c_void_p.

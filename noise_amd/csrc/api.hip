@@ -449,14 +449,18 @@ int noise_mlp_fc(const void* h, const void* w_fc, int d, int f, const float* a_f
 
 int noise_head_ce_workspace_size(int members, int T, int vocab, int fp32_head, size_t* bytes) {
   // the CE finalisation reads each row's partials four at a time: vocab / 64 partials, a multiple of 4
-  if (members <= 0 || T <= 0 || !bytes || vocab <= 0 || vocab % 256 || !lowrank_gemm_parts(vocab)) return NOISE_EINVAL;
+  if (members <= 0 || T <= 0 || !bytes || vocab <= 0 || vocab % 256 || !lowrank_gemm_parts(vocab) ||
+      fp32_head < NOISE_HEAD_BF16 || fp32_head > NOISE_HEAD_FP32)
+    return NOISE_EINVAL;
   const size_t M = (size_t)members * T;
+  const int split = fp32_head == NOISE_HEAD_FP32_SPLIT;
   Carve c(nullptr);
-  c.take<bf16>(M * (fp32_head ? 2 : 1) * DM);      // head operand ([hi | lo] rows for the fp32 head)
+  c.take<bf16>(M * (split ? 2 : 1) * DM);          // head operand ([hi | lo] rows for the split fp32 head)
   c.take<float>(M);                                // h . b
   c.take<float>(M * lowrank_gemm_parts(vocab));    // partial sums of exp(z')
   c.take<float>(M);                                // z' at the target
-  c.take<bf16>((size_t)vocab * (fp32_head ? 3 : 1) * DM);  // the weight in WTILE
+  c.take<bf16>((size_t)vocab * (split ? 3 : fp32_head ? 2 : 1) * DM);  // the weight (WTILE or row-major)
+  c.take<float>(vocab);                            // NOISE_HEAD_FP32: the weight rows' scales
   *bytes = c.used;
   return NOISE_OK;
 }
@@ -475,7 +479,8 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   if (!workspace || workspace_bytes < need) return NOISE_ENOSPC;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t M = (size_t)members * T;
-  const int K = (fp32_head ? 3 : 1) * DM, lda = (fp32_head ? 2 : 1) * DM, parts = lowrank_gemm_parts(vocab);
+  const bool split = fp32_head == NOISE_HEAD_FP32_SPLIT, f16 = fp32_head == NOISE_HEAD_FP32;
+  const int K = (split ? 3 : f16 ? 2 : 1) * DM, lda = (split ? 2 : 1) * DM, parts = lowrank_gemm_parts(vocab);
   Carve c(workspace);
   bf16* hop = c.take<bf16>(M * lda);
   float* u = c.take<float>(M);
@@ -484,20 +489,29 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   // The head's operands reach the GEMM as whole 128-byte lines: the norm writes its rows ([hi | lo] for the fp32
   // head) in TILE16 and the weight is copied into WTILE in the workspace (row-major operands' 32-deep stages load
   // half lines). Rows that do not fill whole 16-row groups, or a weight that is not 16-byte aligned, stay row-major.
+  // NOISE_HEAD_FP32: the fp32 weight (16-byte aligned) becomes the fp16 split operand in the workspace, in either
+  // layout.
+  if (f16 && (((uintptr_t)w_head | (uintptr_t)gain) & 15)) return NOISE_EINVAL;
   const bool tiled = M % 16 == 0 && T % 16 == 0 && !((uintptr_t)w_head & 15);
   bf16* wt = c.take<bf16>((size_t)vocab * K);
-  HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head ? 1 : 0};
+  float* wscale = c.take<float>(vocab);
+  HeadNormArgs hn{x, x_bf16 ? 1 : 0, gain, hop, b, u, sign, (int)M, T, pair_shift, fp32_head};
   hn.tiled = tiled ? 1 : 0;
   if (int rc = copy_pending(pend, npend, hn.pend)) return rc;
   hn.npend = npend;
   if (int rc = head_norm_launch(hn, s)) return rc;
-  if (tiled)
+  if (f16) {
+    if (int rc = head_weight_f16_launch(static_cast<const float*>(w_head), DM, gain, vocab, tiled ? 1 : 0, wt, wscale, s))
+      return rc;
+  } else if (tiled) {
     if (int rc = weight_tiles_launch(static_cast<const bf16*>(w_head), K, vocab, K, wt, s)) return rc;
+  }
   LowrankGemmArgs g =
-      base_args(hop, lda, (long)T * lda, tiled ? wt : w_head, K, vocab, a, sign, members, T, pair_shift);
+      base_args(hop, lda, (long)T * lda, tiled || f16 ? wt : w_head, K, vocab, a, sign, members, T, pair_shift);
   g.a_tiled = tiled ? 1 : 0;
   g.w_tiled = tiled ? 1 : 0;
   g.a_fold = fp32_head ? DM : 0;
+  g.col_scale = f16 ? wscale : nullptr;
   g.u = u;
   g.u_parts = 1;
   g.u_ld = 1;
@@ -509,7 +523,7 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
   g.upart_out = part;
   g.upart_ld = parts;
   g.ldo = vocab;
-  if (int rc = lowrank_gemm_launch(EPI_CE, g, s)) return rc;
+  if (int rc = lowrank_gemm_launch(f16 ? EPI_CE_F16 : EPI_CE, g, s)) return rc;
   if (!targets) return NOISE_OK;
   CeFinalizeArgs f{part, tgt, parts, members, T, loss, targets, tgt_mstride, reduction};
   return ce_finalize_launch(f, s);

@@ -15,6 +15,8 @@ enum : int {
                   // and z at the target column             -> fp32 partials
   EPI_DENSE = 5,  // y = bf16(x W^T) only: the rank-1 term and the residual add are left to the row kernel
                   // that consumes y (a deferred residual)  -> bf16 store
+  EPI_CE_F16 = 6, // EPI_CE on fp16 operands: A = fp16 h [M, a_fold], W = fp16 [W_hi | W_lo] (K = 2 a_fold), row n
+                  // of W scaled by col_scale[n] (a power of two); the fp32 head at an 11-bit h and a 22-bit W
 };
 
 // TILE16 layout of a bf16 matrix [rows, cols] with leading dimension ld (rows % 16 == 0, ld % 32 == 0):
@@ -49,6 +51,8 @@ struct LowrankGemmArgs {
   // forms hi W_hi + hi W_lo + lo W_hi with the three products interleaved per 32-deep block b: stage 3 b reads A
   // block b and W block b, stage 3 b + 1 A block b and W block a_fold / 32 + b, stage 3 b + 2 A block
   // a_fold / 32 + b and W block b (no stored second copy of hi; the repeated blocks come from L2).
+  // EPI_CE_F16 (K = 2 a_fold): A rows are fp16 h and W rows [W_hi | W_lo]; stage 2 b reads A block b and W block
+  // b, stage 2 b + 1 A block b again and W block a_fold / 32 + b.
   const __bf16* A;
   long lda;
   long a_mstride;
@@ -103,10 +107,18 @@ struct LowrankGemmArgs {
   float* ce_tgt;
   long tok_mstride;      // 0: one sequence shared by every member; T: one sequence per member
   float* logits;
+  // EPI_CE_F16: W row n holds the weight row times col_scale[n] (a power of two), so that its fp16 halves keep
+  // 22 significant bits whatever the row's magnitude; the epilogue divides it out exactly.
+  const float* col_scale;
 };
 
 // WTILE copy (out, N * K bf16) of a row-major bf16 weight in [N, K] with row stride ld.
 int weight_tiles_launch(const __bf16* in, long ld, int N, int K, __bf16* out, hipStream_t stream);
+// The fp16 operand of EPI_CE_F16 from an fp32 weight w [N, 512] (row stride ldw) and an optional gain [512]
+// folded in along K: row n of (w * gain) times scale[n] = 2^e (its largest magnitude in [2^14, 2^15)), split into
+// fp16 hi = fp16(row) and lo = fp16(row - hi): out [N, 1024] = [hi | lo], WTILE when tiled, else row-major.
+int head_weight_f16_launch(const float* w, long ldw, const float* gain, int N, int tiled, __bf16* out,
+                           float* scale, hipStream_t stream);
 
 // Number of per-row partials EPI_CE writes for an N-column output (0: N unsupported).
 int lowrank_gemm_parts(int N);

@@ -43,6 +43,7 @@
 
 namespace {
 
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
 struct Cfg {
@@ -123,8 +124,11 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   using C = Cfg<BM, BN, BK, STAGES, WGM, WGN>;
   constexpr int FM = C::FM, FN = C::FN, WM = C::WM, WN = C::WN, CW = C::CW;
   constexpr int SUB = BK / 32;
+  // the head's cross-entropy epilogue, on bf16 or (F16) fp16 operands
+  constexpr bool CE = EPI == EPI_CE || EPI == EPI_CE_F16, F16 = EPI == EPI_CE_F16;
   __shared__ __attribute__((aligned(1024))) bf16 smem[STAGES * C::STAGE];
-  __shared__ __attribute__((aligned(16))) float ep_a[BN];             // a_p over the tile's columns
+  __shared__ __attribute__((aligned(16))) float ep_a[BN];             // a_p over the tile's columns (F16: a_p scaled)
+  __shared__ __attribute__((aligned(16))) float ep_m[F16 ? BN : 4];   // F16: the exp argument's factor per column
   __shared__ float ep_u[C::UGROUPS][BM];                               // partial sums of x.b per row
   __shared__ float ep_sign;
 
@@ -186,6 +190,11 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         ks = pass == 2 ? nb + blk : blk;
         kwt = pass == 1 ? nb + blk : blk;
       }
+    } else if constexpr (F16) {
+      // h W_hi and h W_lo interleaved per 32-deep block: the second read of each A block comes from L2
+      const int blk = kt >> 1;
+      ks = blk;
+      kwt = (kt & 1) ? g.a_fold / BK + blk : blk;
     }
     const long ka = ks * a_step, kw = kwt * w_step;
     // The dense product issues its loads from inline assembly, which the compiler's wait insertion does not see:
@@ -212,13 +221,14 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // ---- epilogue vectors of a tile, loaded into registers ahead of time and staged through LDS.
   // Thread tid sums x.b partial group tid / BM of row tid % BM; threads [0, BN/4) fetch a float4 of
   // a_p, threads [BN/4, BN/2) a float4 of b_next; thread 0 the sign (whole tile in one member only).
-  float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f), pre_sc = make_float4(1.f, 1.f, 1.f, 1.f);
   float pre_u = 0.f, pre_sign = 0.f;
   auto prefetch_ep = [&](int m0, int n0) {
     if constexpr (EPI == EPI_DENSE) return;
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
     const int dir = pfirst >> g.pair_shift, sl = n0 / g.seg_n, seg = g.seg0 + sl, ncol = n0 - sl * g.seg_n;
     if (tid < BN / 4) pre_ab = *reinterpret_cast<const float4*>(g.ra[seg] + (long)dir * g.ra_ld + ncol + 4 * tid);
+    if (F16 && tid < BN / 4) pre_sc = *reinterpret_cast<const float4*>(g.col_scale + n0 + 4 * tid);
     if (tid == 0) pre_sign = pfirst == plast ? g.sign[pfirst] : 0.f;
     const int row = min(m0 + tid % BM, g.M - 1), grp = tid / BM;
     const int q0 = grp * g.u_parts / C::UGROUPS, q1 = (grp + 1) * g.u_parts / C::UGROUPS;
@@ -229,7 +239,18 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   };
   auto stage_ep = [&]() {
     if constexpr (EPI == EPI_DENSE) return;
-    if (tid < BN / 4) *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
+    if constexpr (F16) {
+      // the weight rows arrive scaled by sc (a power of two): a sc and the exp argument's factor / sc are exact
+      constexpr float K2 = 2.f * 1.4426950408889634f / 15.f;
+      if (tid < BN / 4) {
+        *reinterpret_cast<float4*>(&ep_a[4 * tid]) =
+            make_float4(pre_ab.x * pre_sc.x, pre_ab.y * pre_sc.y, pre_ab.z * pre_sc.z, pre_ab.w * pre_sc.w);
+        *reinterpret_cast<float4*>(&ep_m[4 * tid]) =
+            make_float4(K2 / pre_sc.x, K2 / pre_sc.y, K2 / pre_sc.z, K2 / pre_sc.w);
+      }
+    } else {
+      if (tid < BN / 4) *reinterpret_cast<float4*>(&ep_a[4 * tid]) = pre_ab;
+    }
     if (tid == 0) ep_sign = pre_sign;
     ep_u[tid / BM][tid % BM] = pre_u;
   };
@@ -237,6 +258,14 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // ---- MFMA operands of one 32-deep k step: x rows wm*WM + 16 i + (lane & 15) and W rows
   // wn*WN + 16 j + (lane & 15), k chunk kk * 4 + lane / 16.
   const int xrow0 = wm * WM + (lane & 15), wrow0 = wn * WN + (lane & 15);
+  // the MFMA of the operand type (the registers hold 8 raw 16-bit elements either way)
+  auto mma = [](const bf16x8& w, const bf16x8& x, const f32x4& c) {
+    if constexpr (F16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, w), __builtin_bit_cast(h16x8, x), c, 0,
+                                                     0, 0);
+    else
+      return mfma16x16x32(w, x, c);
+  };
   auto read_w = [&](bf16x8 (&w)[FN], int buf, int kk) {
     const bf16* sw = smem + buf * C::STAGE + BM * BK;
     const int c = kk * 4 + (lane >> 4);
@@ -272,7 +301,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   constexpr std::false_type general{};
   // the dense product and the head run their steady steps from a loop of their own; the other epilogues keep
   // one loop (with a second one, config 1's EPI_STORE product measured 4% slower)
-  constexpr bool STEADY_LOOP = SUB == 1 && (EPI == EPI_DENSE || EPI == EPI_CE);
+  constexpr bool STEADY_LOOP = SUB == 1 && (EPI == EPI_DENSE || CE);
   // Step t's MFMAs with (wc, xf) while step t + 1's operands are read into (wn_, xf).
   auto step_read = [&](int t, const bf16x8 (&wc)[FN], bf16x8 (&wn_)[FN], auto st) {
     open(t + 1, st);
@@ -280,7 +309,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(wc[j], xf[i], acc[i][j]);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mma(wc[j], xf[i], acc[i][j]);
       if (i == 0) read_w(wn_, buf, kk);
       read_x(xf[i], buf, kk, i);
     }
@@ -289,7 +318,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(wc[j], xf[i], acc[i][j]);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mma(wc[j], xf[i], acc[i][j]);
   };
 
   // Tile order: row block outer, column tile inner, except for the head (EPI_CE: 16 column tiles of a W that
@@ -298,7 +327,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // 14.8, 16: 15.3, 32: 17.4).
   constexpr int CE_GROUP = 8;
   auto tile_mn = [&](int t, int which) {
-    if (EPI == EPI_CE) {
+    if (CE) {
       const int span = CE_GROUP * tiles_n, grp = t / span, rem = t % span;
       const int gm = min(CE_GROUP, tiles_m - grp * CE_GROUP);
       return which == 0 ? (grp * CE_GROUP + rem % gm) * BM : (rem / gm) * BN;
@@ -400,7 +429,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         } else {
           const float* arow = g.ra[seg] + (long)dir * g.ra_ld + scol + 4 * j;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) av[e] = arow[e];
+          for (int e = 0; e < 4; ++e) av[e] = F16 ? arow[e] * g.col_scale[cb + 4 * j + e] : arow[e];
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[4 * j + e] = (g.round_bf16 ? bf16r(acc[i][j][e]) : acc[i][j][e]) + su * av[e];
@@ -490,10 +519,15 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
         float* lg = g.logits && live ? g.logits + (long)row * g.ldo + cb : nullptr;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          float zq[4];
+          float zq[4], m[4] = {2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f};
+          if constexpr (F16) {
+            // v is the logit times the weight row's scale; m divides it out
+            const float4 m4 = *reinterpret_cast<const float4*>(&ep_m[lcol + 4 * j]);
+            m[0] = m4.x, m[1] = m4.y, m[2] = m4.z, m[3] = m4.w;
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float ez = __builtin_amdgcn_exp2f(v[4 * j + e] * (2.f * L2E / 15.f));
+            const float ez = __builtin_amdgcn_exp2f(v[4 * j + e] * m[e]);
             const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
             se += __builtin_amdgcn_exp2f(zl);
             zt = 4 * j + e == te ? zl : zt;
@@ -607,6 +641,64 @@ int weight_tiles_launch(const bf16* in, long ld, int N, int K, bf16* out, hipStr
   return NOISE_OK;
 }
 
+namespace {
+// One wave per weight row n: lane l holds columns 8 l .. 8 l + 7 of (w * gain), scaled by 2^e so that the row's
+// largest magnitude lies in [2^14, 2^15) (fp16 keeps 11 significant bits down to 2^-14: 2^-28 of that, and the
+// elements below it weigh nothing in a 512-term dot), then split into hi = fp16(v) and lo = fp16(v - hi).
+__global__ void __launch_bounds__(256) head_weight_f16_kernel(const float* __restrict__ w, long ldw,
+                                                              const float* __restrict__ gain, int N, int tiled,
+                                                              _Float16* __restrict__ out, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const long n = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const float4 w0 = *reinterpret_cast<const float4*>(w + n * ldw + 8 * lane);
+  const float4 w1 = *reinterpret_cast<const float4*>(w + n * ldw + 8 * lane + 4);
+  float v[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  if (gain) {
+    const float4 g0 = *reinterpret_cast<const float4*>(gain + 8 * lane);
+    const float4 g1 = *reinterpret_cast<const float4*>(gain + 8 * lane + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] *= gv[e];
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  int ex = 0;
+  if (mx > 0.f) {
+    frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1)
+    ex = min(max(15 - ex, -120), 120);
+  }
+  const float sc = ldexpf(1.f, ex);
+  _Float16 hi[8], lo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float s = v[e] * sc;
+    hi[e] = (_Float16)s;
+    lo[e] = (_Float16)(s - (float)hi[e]);
+  }
+  const long k = 8 * lane;
+  const long oh = tiled ? wtile_offset(n, k, 1024) : n * 1024 + k;
+  const long ol = tiled ? wtile_offset(n, 512 + k, 1024) : n * 1024 + 512 + k;
+  *reinterpret_cast<uint4*>(out + oh) = __builtin_bit_cast(uint4, hi);
+  *reinterpret_cast<uint4*>(out + ol) = __builtin_bit_cast(uint4, lo);
+  if (lane == 0) scale[n] = sc;
+}
+}  // namespace
+
+int head_weight_f16_launch(const float* w, long ldw, const float* gain, int N, int tiled, bf16* out, float* scale,
+                           hipStream_t stream) {
+  if (!w || !out || !scale || N <= 0 || N % 64 || ldw < 512 || ldw % 4 ||
+      (((uintptr_t)w | (uintptr_t)gain | (uintptr_t)out) & 15))
+    return NOISE_EINVAL;
+  hipLaunchKernelGGL(head_weight_f16_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, w, ldw, gain, N,
+                     tiled, reinterpret_cast<_Float16*>(out), scale);
+  NOISE_CHECK_LAUNCH();
+  return NOISE_OK;
+}
+
 int lowrank_gemm_parts(int N) {
   if (N <= 0 || N % 128) return 0;
   return use_big(N) ? N / cfg_wave_n<CFG_BIG>() : N / cfg_wave_n<CFG_SMALL>();
@@ -626,7 +718,10 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
     if (xs_dense_supported(g)) return xs_dense_launch(g, stream);
     return launch_epi<EPI_DENSE>(g, stream);
   }
-  if (g.a_fold && (epi != EPI_CE || g.a_fold < 0 || g.a_fold % 64 || g.K != 3 * g.a_fold))
+  if (g.a_fold && ((epi != EPI_CE && epi != EPI_CE_F16) || g.a_fold < 0 || g.a_fold % 64 ||
+                   g.K != (epi == EPI_CE ? 3 : 2) * g.a_fold))
+    return NOISE_EINVAL;
+  if (epi == EPI_CE_F16 && (!g.a_fold || !g.col_scale || ((uintptr_t)g.col_scale & 15) || g.round_bf16))
     return NOISE_EINVAL;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.T <= 0 || !g.A || !g.W || !g.sign || !g.u || g.u_parts <= 0 ||
       g.u_ld < 1 || g.lda % 8 || (!g.w_tiled && (g.ldw % 8 || g.ldw < g.K)) || g.a_mstride % 8 ||
@@ -656,10 +751,11 @@ int lowrank_gemm_launch(int epi, const LowrankGemmArgs& g, hipStream_t stream) {
         return NOISE_EINVAL;
       return launch_epi<EPI_QKV>(g, stream);
     case EPI_CE:
+    case EPI_CE_F16:
       if ((!g.targets && !g.logits) || !g.ce_tgt || !g.upart_out || g.upart_ld != lowrank_gemm_parts(g.N) ||
           (g.logits && g.ldo < g.N) || g.tok_mstride < 0)
         return NOISE_EINVAL;
-      return launch_epi<EPI_CE>(g, stream);
+      return epi == EPI_CE ? launch_epi<EPI_CE>(g, stream) : launch_epi<EPI_CE_F16>(g, stream);
   }
   return NOISE_EINVAL;
 }

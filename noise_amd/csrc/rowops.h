@@ -78,12 +78,12 @@ struct HeadNormArgs {
   const void* x;         // [M, 512] fp32, or bf16 when x_bf16
   int x_bf16;
   const float* gain;     // [512] or null
-  __bf16* h;             // fp32 head: [M, 1024] = [hi | lo]; bf16 head: [M, 512]
+  __bf16* h;             // fp32_head 1: bf16 [M, 1024] = [hi | lo]; 2: fp16 [M, 512]; 0: bf16 [M, 512]
   const float* b;        // [dirs, 512]
   float* u;              // [M]
   const float* sign;
   int M, T, pair_shift;
-  int fp32_head;
+  int fp32_head;         // operand format: 0 bf16(h gain), 1 bf16 [hi | lo] of h gain, 2 fp16(h) (no gain)
   // deferred residuals added (in order) to x (fp32 only) before the norm
   Pending pend[MAX_PENDING];
   int npend;

@@ -27,12 +27,6 @@ __device__ __forceinline__ void store8(float* p, const Row8& r) {
   *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
   *reinterpret_cast<float4*>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
 }
-__device__ __forceinline__ void store8_bf16(bf16* p, const Row8& r) {
-  bf16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = to_bf16(r.v[e]);
-  store_stream_x4(p, __builtin_bit_cast(u32x4, o));
-}
 // RMSNorm of a 512-wide row spread 8 per lane over one wave: x * rsqrt(mean(x^2) + eps), fp32.
 __device__ __forceinline__ void rms_norm_row(Row8& r) {
   float ss = 0.f;
@@ -281,11 +275,14 @@ __global__ void __launch_bounds__(256) norm_dot_kernel(NormDotArgs g) {
   if (lane == 0) g.u[row] = u;
 }
 
-// Final norm feeding the head (train/val/eggroll.py:94-99). fp32 head: the operand rows are the bf16
-// split [hi | lo] of h (hi = bf16(h), lo = bf16(h - hi)); the head GEMM forms hi W_hi + hi W_lo + lo W_hi from
-// them (its a_fold), so one bf16 MFMA GEMM of depth 1536 yields h W^T to ~2^-16 relative; the dot h.b is fp32.
-// bf16 head: the operand is bf16(h) and the dot follows autocast.
-// One row of the head's norm: x (plus the deferred residuals), RMSNorm, the optional gain; 8 values per lane.
+// Final norm feeding the head (train/val/eggroll.py:94-99). Three operand formats (HeadNormArgs::fp32_head):
+//   2: fp16(h) (|h| <= sqrt(512) after the norm, so fp16's range holds it; 11 significant bits) for the fp16
+//      head GEMM, which forms h W_hi + h W_lo against a 22-bit split of the weight (with the gain folded into the
+//      weight, so the operand carries none); the dot (h gain).b is fp32;
+//   1: the bf16 split [hi | lo] of h gain (hi = bf16(h), lo = bf16(h - hi)); the head GEMM forms
+//      hi W_hi + hi W_lo + lo W_hi from them (its a_fold), ~2^-16 relative; the dot h.b is fp32;
+//   0: bf16(h gain) (the bf16 head), the dot following autocast.
+// One row of the head's norm: x (plus the deferred residuals) and RMSNorm, without the gain; 8 values per lane.
 __device__ __forceinline__ Row8 head_row(const HeadNormArgs& g, long row, int lane, int p, int dir) {
   Row8 x;
   if (g.x_bf16) {
@@ -299,6 +296,9 @@ __device__ __forceinline__ Row8 head_row(const HeadNormArgs& g, long row, int la
     if (g.npend) add_pending(x, pr, g.pend, g.npend, g.sign[p]);
   }
   rms_norm_row(x);
+  return x;
+}
+__device__ __forceinline__ Row8 with_gain(const HeadNormArgs& g, Row8 x, int lane) {
   if (g.gain) {
     const Row8 gv = load8(g.gain + lane * 8);
 #pragma unroll
@@ -312,66 +312,73 @@ __device__ __forceinline__ u32x4 pack_row_x4(const Row8& r) {
   for (int e = 0; e < 8; ++e) o[e] = to_bf16(r.v[e]);
   return __builtin_bit_cast(u32x4, o);
 }
+__device__ __forceinline__ u32x4 pack_row_f16_x4(const Row8& r) {
+  _Float16 __attribute__((ext_vector_type(8))) o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (_Float16)r.v[e];
+  return __builtin_bit_cast(u32x4, o);
+}
+// fp32 dot of the lane's 8 values with the row's b, summed over the wave
+__device__ __forceinline__ float dot_f32_row(const Row8& x, const float* b, int lane) {
+  const Row8 bv = load8(b + lane * 8);
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc += x.v[e] * bv.v[e];
+  return group_sum<64>(acc);
+}
+// The row's operand units (unit 0 in op[0]; [hi | lo]: unit 64 + lane in op[1]) and its dot with b.
+__device__ __forceinline__ float head_operand(const HeadNormArgs& g, const Row8& h, int lane, int dir, u32x4 (&op)[2]) {
+  const float* b = g.b + (long)dir * D;
+  if (g.fp32_head == 2) {
+    op[0] = pack_row_f16_x4(h);
+    return dot_f32_row(with_gain(g, h, lane), b, lane);
+  }
+  const Row8 x = with_gain(g, h, lane);
+  if (g.fp32_head) {
+    Row8 lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
+    op[0] = pack_row_x4(x);
+    op[1] = pack_row_x4(lo);
+    return dot_f32_row(x, b, lane);
+  }
+  const RowBf hb = pack_row(x);
+  op[0] = u32x4{hb.p[0], hb.p[1], hb.p[2], hb.p[3]};
+  return dot_bf16(hb, load8(b + lane * 8));
+}
 
 __global__ void __launch_bounds__(256) head_norm_kernel(HeadNormArgs g) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
   const int p = (int)(row / g.T), dir = p >> g.pair_shift;
-  const Row8 x = head_row(g, row, lane, p, dir);
-  if (g.fp32_head) {
-    Row8 lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
-    bf16* o = g.h + row * (2 * D) + lane * 8;
-    store8_bf16(o, x);
-    store8_bf16(o + D, lo);
-    const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += x.v[e] * bv.v[e];
-    acc = group_sum<64>(acc);
-    if (lane == 0) g.u[row] = acc;
-  } else {
-    const RowBf hb = pack_row(x);
-    store_bf(g.h + row * D + lane * 8, hb);
-    const float u = dot_bf16(hb, load8(g.b + (long)dir * D + lane * 8));
-    if (lane == 0) g.u[row] = u;
-  }
+  u32x4 op[2];
+  const float u = head_operand(g, head_row(g, row, lane, p, dir), lane, dir, op);
+  const int W = g.fp32_head == 1 ? 2 * D : D;
+  bf16* o = g.h + row * W + lane * 8;
+  store_stream_x4(o, op[0]);
+  if (g.fp32_head == 1) store_stream_x4(o + D, op[1]);
+  if (lane == 0) g.u[row] = u;
 }
 
 // The same rows written in TILE16 (the tile GEMM's whole-line operand layout): element (r, c) of the [M, W]
-// operand (W = 1024 for [hi | lo], 512 for the bf16 head) at (r / 16) 16 W + (c / 32) 512 + 8 q + c % 8 with
+// operand (W = 1024 for [hi | lo], 512 otherwise) at (r / 16) 16 W + (c / 32) 512 + 8 q + c % 8 with
 // q = 4 (r % 16) + ((c % 32) / 8 ^ ((r % 16) / 2) % 4). A workgroup of 16 waves normalises one 16-row group, a row
-// per wave as above, into LDS, then writes the group's 16 W bf16 (one contiguous 32 or 16 KiB run) as whole lines:
-// row by row, four lanes would fill half a line each and the stores would scatter over 16 or 32 tiles.
+// per wave as above, into LDS, then writes the group's 16 W 16-bit values (one contiguous 32 or 16 KiB run) as
+// whole lines: row by row, four lanes would fill half a line each and the stores would scatter over 16 or 32 tiles.
 __global__ void __launch_bounds__(1024) head_norm_tiled_kernel(HeadNormArgs g) {
   constexpr int UNITS = 2 * D / 8;           // 16-byte units per row of [hi | lo]
   // + 4 units: consecutive rows start 16 banks apart, so the 4 rows of one 16-lane read pass cover all 64 banks
   __shared__ u32x4 rows16[16][UNITS + 4];
   const int lane = threadIdx.x & 63, r16 = threadIdx.x >> 6;
   const long r0 = (long)blockIdx.x * 16, row = r0 + r16;
-  const int W = g.fp32_head ? 2 * D : D, units = W / 8;
+  const int W = g.fp32_head == 1 ? 2 * D : D, units = W / 8;
   const int p = (int)(row / g.T), dir = p >> g.pair_shift;
-  const Row8 x = head_row(g, row, lane, p, dir);
-  if (g.fp32_head) {
-    Row8 lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) lo.v[e] = x.v[e] - bf16r(x.v[e]);
-    rows16[r16][lane] = pack_row_x4(x);
-    rows16[r16][64 + lane] = pack_row_x4(lo);
-    const Row8 bv = load8(g.b + (long)dir * D + lane * 8);
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += x.v[e] * bv.v[e];
-    acc = group_sum<64>(acc);
-    if (lane == 0) g.u[row] = acc;
-  } else {
-    const RowBf hb = pack_row(x);
-    rows16[r16][lane] = u32x4{hb.p[0], hb.p[1], hb.p[2], hb.p[3]};
-    const float u = dot_bf16(hb, load8(g.b + (long)dir * D + lane * 8));
-    if (lane == 0) g.u[row] = u;
-  }
+  u32x4 op[2];
+  const float u = head_operand(g, head_row(g, row, lane, p, dir), lane, dir, op);
+  rows16[r16][lane] = op[0];
+  if (g.fp32_head == 1) rows16[r16][64 + lane] = op[1];
+  if (lane == 0) g.u[row] = u;
   __syncthreads();
   // unit n of the group: tile n / 64, q = n % 64 -> row q / 4, 8-column chunk (q % 4) ^ ((q / 8) % 4) of the tile
   bf16* out = g.h + r0 * W;
@@ -556,7 +563,7 @@ int norm_dot_launch(const NormDotArgs& g, hipStream_t s) {
 
 int head_norm_launch(const HeadNormArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.T <= 0 || !g.x || !g.h || !g.b || !g.u || !g.sign || bad_pending(g.pend, g.npend) ||
-      (g.x_bf16 && g.npend))
+      (g.x_bf16 && g.npend) || g.fp32_head < 0 || g.fp32_head > 2)
     return NOISE_EINVAL;
   if (g.tiled) {
     if (g.M % 16) return NOISE_EINVAL;

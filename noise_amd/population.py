@@ -12,7 +12,10 @@ from . import _lib
 from .model import GPTConfig, has_ve, window_sizes
 
 D, H, HD, F = 512, 8, 64, 2048
-HEAD_MODES = ('fp32', 'bf16')
+# Head formats: 'fp32' = NOISE_HEAD_FP32 (h rounded once to fp16 against a 22-bit weight, two fp16 MFMA passes),
+# 'fp32_split' = NOISE_HEAD_FP32_SPLIT (bf16 hi / lo, three bf16 passes, ~2^-16), 'bf16' = the autocast head.
+HEAD_MODES = ('fp32', 'fp32_split', 'bf16')
+HEAD_FORMAT = {'fp32': _lib.HEAD_FP32, 'fp32_split': _lib.HEAD_FP32_SPLIT, 'bf16': _lib.HEAD_BF16}
 
 
 def _p(t):
@@ -35,7 +38,8 @@ def _need_cuda(t, dtype, name):
 class Weights:
     """Per-step device copies of the shared weights in the kernels' formats: bf16 GEMM operands (the
     autocast cast the reference performs inside every matmul, done once per step; the MLP c_proj weight in
-    the tile GEMM's WTILE layout) and the fp32-head split operand. Built from `p` = name -> fp32 parameter
+    the tile GEMM's WTILE layout) and the head weight in its format (the fp32 parameter itself for 'fp32', whose
+    operand the head call derives; the bf16 split for 'fp32_split'). Built from `p` = name -> fp32 parameter
     (train/val/eggroll.py:113)."""
 
     def __init__(self, p, config=None, head='fp32'):
@@ -64,6 +68,9 @@ class Weights:
         w_head = p['lm_head.weight']
         V = w_head.shape[0]
         if head == 'fp32':
+            _need_cuda(w_head, torch.float32, 'lm_head.weight')
+            self.head_w = w_head
+        elif head == 'fp32_split':
             self.head_w = torch.empty(V, 3 * D, device=dev, dtype=torch.bfloat16)
             _need_cuda(w_head, torch.float32, 'lm_head.weight')
             _lib.call('noise_cast_bf16', w_head.data_ptr(), self.head_w.data_ptr(), w_head.numel(), D, s)
@@ -100,7 +107,7 @@ class Buffers:
         self.parts = _lib.value('noise_mlp_fc_parts', F)
         self.hidden = torch.empty(M, F, device=device, dtype=b16)
         self.u_mlp = torch.empty(self.parts, M, device=device, dtype=f32)  # part-major
-        ws = _lib.size_query('noise_head_ce_workspace_size', members, T, vocab, int(head == 'fp32'))
+        ws = _lib.size_query('noise_head_ce_workspace_size', members, T, vocab, HEAD_FORMAT[head])
         self.head_ws = torch.empty(ws, device=device, dtype=torch.uint8)
 
     def fits(self, members, T):
@@ -253,7 +260,7 @@ def forward_chunk(W, buf, noise, sign, idx, targets, pair_shift, out, cos, sin, 
     Vh = W.head_w.shape[0]
     t0 = tm.mark('head')
     pend, npend = _lib.pending(*pend_prev)
-    _lib.call('noise_head_ce', _p(buf.x), 0, 0, _p(W.head_w), Vh, int(W.head == 'fp32'), _p(ah), _p(bh), _p(sign),
+    _lib.call('noise_head_ce', _p(buf.x), 0, 0, _p(W.head_w), Vh, HEAD_FORMAT[W.head], _p(ah), _p(bh), _p(sign),
               _p(targets), tok_mstride, m, T, ps, reduction, _p(out), _p(logits), _p(buf.head_ws), buf.head_ws.numel(),
               pend, npend, s)
     tm.close(t0)

@@ -59,8 +59,11 @@ def test_version_and_size_queries_run_on_cpu():
     assert n >= 4 * 256 * 2048 * 2
     with pytest.raises(_lib.NoiseHipError):
         _lib.size_query('noise_lowrank_mlp_workspace_size', 0, 256, 512, 2048)
-    assert _lib.size_query('noise_head_ce_workspace_size', 2, 256, 4096, 1) > _lib.size_query(
-        'noise_head_ce_workspace_size', 2, 256, 4096, 0)
+    head_ws = [_lib.size_query('noise_head_ce_workspace_size', 2, 256, 4096, f) for f in range(3)]
+    # the split fp32 head holds [hi | lo] rows and a 3-part weight; the fp16 one h rows and a 2-part weight
+    assert head_ws[_lib.HEAD_FP32_SPLIT] > head_ws[_lib.HEAD_FP32] > head_ws[_lib.HEAD_BF16]
+    with pytest.raises(_lib.NoiseHipError):
+        _lib.size_query('noise_head_ce_workspace_size', 2, 256, 4096, 3)
     assert _lib.value('noise_mlp_fc_parts', 2048) == 8
     assert _lib.value('noise_mlp_fc_parts', 100) == 0
 
@@ -111,6 +114,12 @@ def test_bad_arguments_are_rejected_without_touching_the_gpu():
     assert lib.noise_head_ce_workspace_size(2, 256, 640, 1, ctypes.byref(ctypes.c_size_t(0))) == EINVAL
     assert lib.noise_head_ce(1, 0, None, 1, 640, 1, 1, 1, 1, 1, 0, 1, 256, 0, 0, 1, None, 1, 1 << 40, None, 0,
                              None) == EINVAL
+    # the fp32 weight of NOISE_HEAD_FP32 (and its gain) must be 16-byte aligned; an unknown format is refused
+    fmt = lambda w, gain, f: lib.noise_head_ce(  # noqa: E731
+        16, 0, gain, w, 4096, f, 16, 16, 16, 16, 0, 1, 256, 0, 0, 16, None, 16, 1 << 40, None, 0, None)
+    assert fmt(8, None, _lib.HEAD_FP32) == EINVAL
+    assert fmt(16, 8, _lib.HEAD_FP32) == EINVAL
+    assert fmt(16, None, 3) == EINVAL
     # WTILE copies need rows % 64 == 0, cols % 32 == 0 and 16-byte aligned pointers; the dense product knows the
     # ROWS and WTILE weight layouts only
     assert lib.noise_weight_tiles(16, 96, 512, 16, None) == EINVAL

@@ -136,9 +136,11 @@ def test_config2_attention_moments_full_size(qk_norm, qk_format):
 
 
 @pytest.mark.timeout(600)
-def test_config3_norm_head_ce_full_size_with_gain():
+@pytest.mark.parametrize('fmt', [_lib.HEAD_FP32, _lib.HEAD_FP32_SPLIT])
+def test_config3_norm_head_ce_full_size_with_gain(fmt):
     """P = 512, T = 2048: bf16 h [512, 2048, 512], gain ~ U(0.9, 1.1), fp32 head [4096, 512] ~ N(0, 1/512) with
-    per-pair rank-1 perturbation, sigma = 1e-3, Zipf targets. Sampled members within 1e-4 of the fp32 oracle."""
+    per-pair rank-1 perturbation, sigma = 1e-3, Zipf targets, in both fp32 head formats. Sampled members within
+    1e-4 of the fp32 oracle."""
     P, T, V = 512, 2048, 4096
     g = torch.Generator().manual_seed(31)
     gd = torch.Generator(device=DEV).manual_seed(32)
@@ -150,12 +152,15 @@ def test_config3_norm_head_ce_full_size_with_gain():
     _, targets = zipf_tokens(T, seed=33)
     s = torch.cuda.current_stream().cuda_stream
     gdv, Wd, ad, bd, sd, td = (t.to(DEV) for t in (gain, W, a, b, sign, targets))
-    log_case(f'config3 head_ce P={P} T={T}')
-    wd = torch.empty(V, 1536, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512, s)
+    log_case(f'config3 head_ce P={P} T={T} fp32_head={fmt}')
+    if fmt == _lib.HEAD_FP32:
+        wd = Wd
+    else:
+        wd = torch.empty(V, 1536, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512, s)
     loss = torch.empty(P, device=DEV)
-    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', P, T, V, 1), device=DEV, dtype=torch.uint8)
-    _lib.call('noise_head_ce', h.data_ptr(), 1, gdv.data_ptr(), wd.data_ptr(), V, 1, ad.data_ptr(), bd.data_ptr(),
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', P, T, V, fmt), device=DEV, dtype=torch.uint8)
+    _lib.call('noise_head_ce', h.data_ptr(), 1, gdv.data_ptr(), wd.data_ptr(), V, fmt, ad.data_ptr(), bd.data_ptr(),
               sd.data_ptr(), td.data_ptr(), 0, P, T, 1, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None, ws.data_ptr(),
               ws.numel(), None, 0, s)
     torch.cuda.synchronize()

@@ -501,6 +501,21 @@ def test_attention_matches_oracle_and_moments(qk_norm, qk_format):
         assert torch.allclose(mom.cpu()[:, :, 1], m2, atol=1e-5)
 
 
+def _head_weight(W, fmt, s):
+    """The head weight on the device in noise_head_ce's format fmt (NOISE_HEAD_*): fp32 itself, the bf16 split
+    [W_hi | W_lo | W_hi], or bf16."""
+    Wd = W.contiguous().to(DEV)
+    if fmt == _lib.HEAD_FP32:
+        return Wd
+    wd = torch.empty(W.shape[0], 1536 if fmt == _lib.HEAD_FP32_SPLIT else 512, device=DEV, dtype=torch.bfloat16)
+    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fmt == _lib.HEAD_FP32_SPLIT else 0, s)
+    torch.cuda.synchronize()
+    return wd
+
+
+HEAD_FORMATS = (_lib.HEAD_FP32, _lib.HEAD_FP32_SPLIT, _lib.HEAD_BF16)
+
+
 def test_head_ce_matches_oracle_fp32_and_bf16_heads():
     g = torch.Generator().manual_seed(4)
     m, T, V = 4, 256, 4096
@@ -511,11 +526,10 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
     _, targets = zipf_tokens(T, seed=5)
     s = torch.cuda.current_stream().cuda_stream
     h = om.norm(x.view(m, T, 512))
-    xd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (x, W, a, b, sign, targets))
-    for fp32 in (1, 0):
+    xd, ad, bd, sd, td = (t.to(DEV) for t in (x, a, b, sign, targets))
+    for fp32 in HEAD_FORMATS:
         log_case(f'head_ce m={m} T={T} fp32_head={fp32}')
-        wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
-        _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+        wd = _head_weight(W, fp32, s)
         loss = torch.empty(m, device=DEV)
         ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV,
                          dtype=torch.uint8)
@@ -531,7 +545,7 @@ def test_head_ce_matches_oracle_fp32_and_bf16_heads():
             assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
 
 
-@pytest.mark.parametrize('fp32,T', [(1, 96), (0, 96), (1, 90), (0, 90)])
+@pytest.mark.parametrize('fp32,T', [(f, t) for t in (96, 90) for f in HEAD_FORMATS])
 def test_head_ce_other_vocab_and_partial_row_tile(fp32, T):
     """A 768-entry vocabulary (3 column tiles, 12 CE partials per row) and token counts that leave the last
     256-row tile partial: 96 (the normalised operand in TILE16) and 90 (not a multiple of 16: row-major)."""
@@ -544,10 +558,9 @@ def test_head_ce_other_vocab_and_partial_row_tile(fp32, T):
     targets = torch.randint(0, V, (T,), generator=g)
     s = torch.cuda.current_stream().cuda_stream
     h = om.norm(x.view(m, T, 512))
-    xd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (x, W, a, b, sign, targets))
+    xd, ad, bd, sd, td = (t.to(DEV) for t in (x, a, b, sign, targets))
     log_case(f'head_ce m={m} T={T} V={V} fp32_head={fp32}')
-    wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+    wd = _head_weight(W, fp32, s)
     loss = torch.empty(m, device=DEV)
     ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fp32), device=DEV, dtype=torch.uint8)
     _lib.call('noise_head_ce', xd.data_ptr(), 0, 0, wd.data_ptr(), V, fp32, ad.data_ptr(), bd.data_ptr(),
@@ -562,7 +575,7 @@ def test_head_ce_other_vocab_and_partial_row_tile(fp32, T):
         assert (loss.cpu() - ref).abs().max() < 2e-4, (loss.cpu(), ref)
 
 
-@pytest.mark.parametrize('fp32', [1, 0])
+@pytest.mark.parametrize('fp32', HEAD_FORMATS)
 def test_head_ce_tiled_and_row_major_operands_agree_bit_for_bit(fp32):
     """The head's whole-line path (operand rows in TILE16, weight in WTILE: rows in whole 16-row groups) and its
     row-major path (taken when T is not a multiple of 16) on the same 384 rows: 4 members x 96 tokens against 48
@@ -576,9 +589,8 @@ def test_head_ce_tiled_and_row_major_operands_agree_bit_for_bit(fp32):
     sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
     tok = torch.randint(0, V, (m * T,), generator=g)
     s = torch.cuda.current_stream().cuda_stream
-    xd, Wd, td = x.to(DEV), W.to(DEV), tok.to(DEV)
-    wd = torch.empty(V, 1536 if fp32 else 512, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512 if fp32 else 0, s)
+    xd, td = x.to(DEV), tok.to(DEV)
+    wd = _head_weight(W, fp32, s)
 
     def run(members, t, a_, b_, sign_):
         log_case(f'head_ce members={members} T={t} fp32_head={fp32} per-token losses')
@@ -598,7 +610,8 @@ def test_head_ce_tiled_and_row_major_operands_agree_bit_for_bit(fp32):
     assert torch.equal(tiled, rows), (tiled - rows).abs().max()
 
 
-def test_head_ce_config3_bf16_input_with_gain():
+@pytest.mark.parametrize('fmt', [_lib.HEAD_FP32, _lib.HEAD_FP32_SPLIT])
+def test_head_ce_config3_bf16_input_with_gain(fmt):
     """Config 3: bf16 hidden states, RMSNorm gain ~ U(0.9, 1.1), fp32 head with rank-1 perturbation."""
     g = torch.Generator().manual_seed(12)
     m, T, V = 4, 256, 4096
@@ -609,19 +622,59 @@ def test_head_ce_config3_bf16_input_with_gain():
     sign = antithetic_signs(m, 1e-3)
     _, targets = zipf_tokens(T, seed=13)
     s = torch.cuda.current_stream().cuda_stream
-    hd, gd, Wd, ad, bd, sd, td = (t.to(DEV) for t in (h, gain, W, a, b, sign, targets))
-    log_case(f'head_ce config3 m={m} T={T}')
-    wd = torch.empty(V, 1536, device=DEV, dtype=torch.bfloat16)
-    _lib.call('noise_cast_bf16', Wd.data_ptr(), wd.data_ptr(), W.numel(), 512, s)
+    hd, gd, ad, bd, sd, td = (t.to(DEV) for t in (h, gain, a, b, sign, targets))
+    log_case(f'head_ce config3 m={m} T={T} fp32_head={fmt}')
+    wd = _head_weight(W, fmt, s)
     loss = torch.empty(m, device=DEV)
-    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, 1), device=DEV, dtype=torch.uint8)
-    _lib.call('noise_head_ce', hd.data_ptr(), 1, gd.data_ptr(), wd.data_ptr(), V, 1, ad.data_ptr(), bd.data_ptr(),
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, fmt), device=DEV, dtype=torch.uint8)
+    _lib.call('noise_head_ce', hd.data_ptr(), 1, gd.data_ptr(), wd.data_ptr(), V, fmt, ad.data_ptr(), bd.data_ptr(),
               sd.data_ptr(), td.data_ptr(), 0, m, T, 1, _lib.CE_MEMBER_MEAN, loss.data_ptr(), None, ws.data_ptr(),
               ws.numel(), None, 0, s)
     torch.cuda.synchronize()
     rep = lambda t: t.repeat_interleave(2, 0)  # noqa: E731
     ref = om.norm_head_ce(h.float(), gain, W, rep(a), rep(b), sign, targets)
     assert (loss.cpu() - ref).abs().max() < 1e-4, (loss.cpu(), ref)
+
+
+def test_head_ce_fp32_format_logit_error_bound():
+    """NOISE_HEAD_FP32 rounds h once to fp16 (relative error <= 2^-12 per element) and carries each weight row times
+    a power of two as fp16 hi + lo (~22 significant bits), accumulating in fp32. Each capped logit then lies within
+    2^-11 sum_i |h_i g_i W_vi| (plus a 1e-5 floor for the hardware exp and reciprocal of the cap) of the fp32 oracle's,
+    whatever the row's magnitude: here rows scaled by 10^-7 .. 10^1 (the reference init's lm_head is ~1e-6; the
+    largest rows push logits far past the cap), a gain, and per-member rank-1 terms. A token's loss
+    logsumexp(z') - z'_target then moves by at most twice its largest logit error, which bounds each member's mean.
+    (At model-scale weights the members agree within 1e-4: the other head tests.)"""
+    g = torch.Generator().manual_seed(31)
+    m, T, V = 4, 64, 1024
+    x = torch.randn(m * T, 512, generator=g) * 3
+    gain = 0.5 + 1.5 * torch.rand(512, generator=g)
+    rows = 10.0 ** (-7 + 8 * torch.rand(V, 1, generator=g))
+    W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2 * rows
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
+    targets = torch.randint(0, V, (T,), generator=g)
+    s = torch.cuda.current_stream().cuda_stream
+    xd, gd, ad, bd, sd, td = (t.to(DEV) for t in (x, gain, a, b, sign, targets))
+    wd = _head_weight(W, _lib.HEAD_FP32, s)
+    log_case(f'head_ce fp32 format logits m={m} T={T} V={V}')
+    loss, logits = torch.empty(m, device=DEV), torch.empty(m * T, V, device=DEV)
+    ws = torch.empty(_lib.size_query('noise_head_ce_workspace_size', m, T, V, _lib.HEAD_FP32), device=DEV,
+                     dtype=torch.uint8)
+    _lib.call('noise_head_ce', xd.data_ptr(), 0, gd.data_ptr(), wd.data_ptr(), V, _lib.HEAD_FP32, ad.data_ptr(),
+              bd.data_ptr(), sd.data_ptr(), td.data_ptr(), 0, m, T, 0, _lib.CE_MEMBER_MEAN, loss.data_ptr(),
+              logits.data_ptr(), ws.data_ptr(), ws.numel(), None, 0, s)
+    torch.cuda.synchronize()
+    hn = om.norm(x.view(m, T, 512)) * gain
+    z = om.lowrank(hn, W, a, b, sign, 'fp32')
+    ref = 15 * torch.tanh(z / 15)
+    bound = 2.0 ** -11 * (hn.abs() @ W.abs().t()) + 1e-5 + 1e-5 * z.abs()
+    err = (logits.cpu().view(m, T, V) - ref).abs()
+    assert (err <= bound).all(), (err - bound).max()
+    # the bound is not vacuous: the largest rows' logits are O(1) and their errors well above the fp32 floor
+    assert ref.abs().max() > 1 and err.max() > 1e-6
+    ref_loss = om.head_loss(om.norm(x.view(m, T, 512)) * gain, W, a, b, sign, targets, 'fp32', 'fp32')
+    loss_bound = 2 * bound.amax(-1).mean(-1) + 1e-6
+    assert ((loss.cpu() - ref_loss).abs() <= loss_bound).all(), (loss.cpu() - ref_loss, loss_bound)
 
 
 # ---------------------------------------------------------------- whole population forward
