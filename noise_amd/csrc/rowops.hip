@@ -230,9 +230,10 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   block_entry_row<FIRST>(g, row, lane, vec);
 }
 // GROUP_ROWS rows of one member per workgroup (T % GROUP_ROWS == 0), GROUP_ROWS / 4 per wave in turn: the member's
-// six vectors (12 KiB) are staged in LDS once per workgroup (384 B per row) instead of being read from L2 by every
+// six vectors (12 KiB) are staged in LDS once per workgroup (1.5 KiB per row) instead of being read from L2 by every
 // row (12 KiB per row). Layers after the first take this instance; the result is bit for bit the per-row kernel's.
-constexpr int GROUP_ROWS = 32;
+// Measured (entry stage per step): 8 rows 66.5-66.7 ms, 4 rows 66.6-67.1, 16 rows 69.1-71.4, 32 rows 68.9-70.9.
+constexpr int GROUP_ROWS = 8;
 __global__ void __launch_bounds__(256) block_entry_group_kernel(BlockEntryArgs g) {
   __shared__ __attribute__((aligned(16))) float svec[6][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

@@ -337,11 +337,11 @@ def test_deferred_residuals_match_eager_lowrank():
 
 
 def test_block_entry_grouped_and_per_row_instances_agree_bit_for_bit():
-    """The block entry at T = 96 (workgroups of 32 rows of one member, the member's vectors staged in LDS) and the
-    same rows cut into T = 8 members (one row per wave, vectors read per row) write the same x, h, dots and gates,
+    """The block entry at T = 96 (workgroups of a few rows of one member, the member's vectors staged in LDS) and the
+    same rows cut into T = 6 members (one row per wave, vectors read per row) write the same x, h, dots and gates,
     bit for bit: with deferred residuals, the value-embedding gate and x0 both stored and recomputed."""
     g = torch.Generator().manual_seed(21)
-    m, T, D, V, R = 4, 96, 512, 4096, 12  # R: members of the cut layout per member
+    m, T, D, V, R = 4, 96, 512, 4096, 16  # R: members of the cut layout per member
     M = m * T
     x, x0 = torch.randn(M, D, generator=g) * 3, torch.randn(M, D, generator=g)
     y1, y2 = (torch.randn(M, D, generator=g).bfloat16() for _ in range(2))
