@@ -230,10 +230,12 @@ __global__ void __launch_bounds__(256) block_entry_kernel(BlockEntryArgs g) {
   block_entry_row<FIRST>(g, row, lane, vec);
 }
 // GROUP_ROWS rows of one member per workgroup (T % GROUP_ROWS == 0), GROUP_ROWS / 4 per wave in turn: the member's
-// six vectors (12 KiB) are staged in LDS once per workgroup (1.5 KiB per row) instead of being read from L2 by every
-// row (12 KiB per row). Layers after the first take this instance; the result is bit for bit the per-row kernel's.
+// vectors (up to six, 12 KiB) are staged in LDS once per workgroup (1.5 KiB per row) instead of being read from L2 by
+// every row (12 KiB per row); the result is bit for bit the per-row kernel's. Block 0 takes it too (FIRST, 61 VGPRs):
+// entry stage 68.9 → 67.4 ms per step (three runs each, one box).
 // Measured (entry stage per step): 8 rows 66.5-66.7 ms, 4 rows 66.6-67.1, 16 rows 69.1-71.4, 32 rows 68.9-70.9.
 constexpr int GROUP_ROWS = 8;
+template <bool FIRST>
 __global__ void __launch_bounds__(256) block_entry_group_kernel(BlockEntryArgs g) {
   __shared__ __attribute__((aligned(16))) float svec[6][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -253,7 +255,7 @@ __global__ void __launch_bounds__(256) block_entry_group_kernel(BlockEntryArgs g
 #pragma unroll 1
   for (int k = 0; k < GROUP_ROWS / 4; ++k) {
     asm volatile("" ::: "memory");
-    block_entry_row<false, true>(g, row0 + wave * (GROUP_ROWS / 4) + k, lane, vec);
+    block_entry_row<FIRST, true>(g, row0 + wave * (GROUP_ROWS / 4) + k, lane, vec);
   }
 }
 
@@ -544,10 +546,13 @@ int block_entry_launch(const BlockEntryArgs& g, hipStream_t s) {
   if (g.gate_w && (!g.gate_a || !g.gate_b || !g.gate || (((uintptr_t)g.gate_w | (uintptr_t)g.gate_b) & 15)))
     return NOISE_EINVAL;
   if (bad_pending(g.pend, g.npend)) return NOISE_EINVAL;
-  if (!g.x_in && !g.x0 && !g.npend)
+  const bool first = !g.x_in && !g.x0 && !g.npend, grouped = g.T % GROUP_ROWS == 0 && g.M % GROUP_ROWS == 0;
+  if (first && grouped)
+    hipLaunchKernelGGL(block_entry_group_kernel<true>, dim3((unsigned)(g.M / GROUP_ROWS)), dim3(256), 0, s, g);
+  else if (first)
     hipLaunchKernelGGL(block_entry_kernel<true>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
-  else if (g.T % GROUP_ROWS == 0 && g.M % GROUP_ROWS == 0)
-    hipLaunchKernelGGL(block_entry_group_kernel, dim3((unsigned)(g.M / GROUP_ROWS)), dim3(256), 0, s, g);
+  else if (grouped)
+    hipLaunchKernelGGL(block_entry_group_kernel<false>, dim3((unsigned)(g.M / GROUP_ROWS)), dim3(256), 0, s, g);
   else
     hipLaunchKernelGGL(block_entry_kernel<false>, dim3(grid_rows(g.M)), dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();

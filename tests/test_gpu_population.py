@@ -339,7 +339,8 @@ def test_deferred_residuals_match_eager_lowrank():
 def test_block_entry_grouped_and_per_row_instances_agree_bit_for_bit():
     """The block entry at T = 96 (workgroups of a few rows of one member, the member's vectors staged in LDS) and the
     same rows cut into T = 6 members (one row per wave, vectors read per row) write the same x, h, dots and gates,
-    bit for bit: with deferred residuals, the value-embedding gate and x0 both stored and recomputed."""
+    bit for bit: with deferred residuals, the value-embedding gate and x0 both stored and recomputed, and as block 0
+    (no incoming stream, no deferred residuals, x0 recomputed: the first-block instances)."""
     g = torch.Generator().manual_seed(21)
     m, T, D, V, R = 4, 96, 512, 4096, 16  # R: members of the cut layout per member
     M = m * T
@@ -372,19 +373,21 @@ def test_block_entry_grouped_and_per_row_instances_agree_bit_for_bit():
         pend, npend = _lib.pending(p1, p2)
         emb, emb_ptr = _lib.embed(common['w'].data_ptr(), V, d['ea'].data_ptr(), d['eb'].data_ptr(),
                                   common['idx'].data_ptr(), TT)
-        for x0_mode in ('stored', 'recomputed'):
+        for x0_mode in ('stored', 'recomputed', 'first'):
             log_case(f'block_entry {layout} m={mm} T={TT} x0 {x0_mode}')
-            stored = x0_mode == 'stored'
+            stored, first = x0_mode == 'stored', x0_mode == 'first'
             xo, h = torch.empty(M, D, device=DEV), torch.empty(M, D, device=DEV, dtype=torch.bfloat16)
             u, gate = torch.empty(M, 4, device=DEV), torch.empty(M, 8, device=DEV)
-            _lib.call('noise_block_entry', common['x'].data_ptr(), common['x0'].data_ptr() if stored else None,
+            _lib.call('noise_block_entry', None if first else common['x'].data_ptr(),
+                      common['x0'].data_ptr() if stored else None,
                       xo.data_ptr(), h.data_ptr(), u.data_ptr(), d['bq'].data_ptr(), d['bk'].data_ptr(),
                       d['bv'].data_ptr(), common['lr'].data_ptr(), common['l0'].data_ptr(), d['er'].data_ptr() + 4 * 3,
                       d['e0'].data_ptr() + 4 * 3, 8, common['gw'].data_ptr(), d['ga'].data_ptr(), d['gb'].data_ptr(),
-                      gate.data_ptr(), d['sign'].data_ptr(), mm, TT, ps, pend, npend, None if stored else emb_ptr, s)
+                      gate.data_ptr(), d['sign'].data_ptr(), mm, TT, ps, None if first else pend, 0 if first else npend,
+                      None if stored else emb_ptr, s)
             torch.cuda.synchronize()
             out[layout, x0_mode] = (xo.cpu(), h.cpu(), u.cpu(), gate.cpu())
-    for x0_mode in ('stored', 'recomputed'):
+    for x0_mode in ('stored', 'recomputed', 'first'):
         for a_, b_ in zip(out['grouped', x0_mode], out['per_row', x0_mode]):
             assert torch.equal(a_, b_), x0_mode
     # the recomputed x0 is a different x0 from the stored one: the two modes must differ
