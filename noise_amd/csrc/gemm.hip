@@ -220,7 +220,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
 
   // ---- epilogue vectors of a tile, loaded into registers ahead of time and staged through LDS.
   // Thread tid sums x.b partial group tid / BM of row tid % BM; threads [0, BN/4) fetch a float4 of
-  // a_p, threads [BN/4, BN/2) a float4 of b_next; thread 0 the sign (whole tile in one member only).
+  // a_p (EPI_CE_F16: and of the weight rows' scales); thread 0 the sign (whole tile in one member only).
   float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f), pre_sc = make_float4(1.f, 1.f, 1.f, 1.f);
   float pre_u = 0.f, pre_sign = 0.f;
   auto prefetch_ep = [&](int m0, int n0) {
@@ -643,8 +643,9 @@ int weight_tiles_launch(const bf16* in, long ld, int N, int K, bf16* out, hipStr
 
 namespace {
 // One wave per weight row n: lane l holds columns 8 l .. 8 l + 7 of (w * gain), scaled by 2^e so that the row's
-// largest magnitude lies in [2^14, 2^15) (fp16 keeps 11 significant bits down to 2^-14: 2^-28 of that, and the
-// elements below it weigh nothing in a 512-term dot), then split into hi = fp16(v) and lo = fp16(v - hi).
+// largest magnitude lies in [2^14, 2^15), then split into hi = fp16(v) and lo = fp16(v - hi). fp16 keeps 11
+// significant bits for magnitudes down to 2^-14, i.e. for every element within 2^-28 of the row's largest; the
+// smaller ones lose relative precision but keep an absolute error below 2^-24, which a 512-term dot does not see.
 __global__ void __launch_bounds__(256) head_weight_f16_kernel(const float* __restrict__ w, long ldw,
                                                               const float* __restrict__ gain, int N, int tiled,
                                                               _Float16* __restrict__ out, float* __restrict__ scale) {
