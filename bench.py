@@ -34,8 +34,7 @@ METRIC = 'perturbed member-tokens/sec on 1 GPU; fused-MLP MFMA % of bf16 peak'
 PEAK_BF16_TFLOPS = 2500.0         # MI355X dense bf16 MFMA
 D, F, T, V, L = 512, 2048, 2048, 4096, 8
 SIGMA = 1e-3
-# head formats (noise_head_ce's NOISE_HEAD_*) and how each runs
-HEAD_FORMAT = {'fp32': 2, 'fp32_split': 1, 'bf16': 0}
+# how each head format (noise_amd.population.HEAD_FORMAT: noise_head_ce's NOISE_HEAD_*) runs
 HEAD_DESC = {'fp32': 'fp32 (fp16 h x fp16 hi/lo weight: 2 MFMA passes)',
              'fp32_split': 'fp32 (bf16 hi/lo split: 3 MFMA passes)', 'bf16': 'bf16 (autocast rounding)'}
 MLP_FLOP_PER_MEMBER_TOKEN = 2 * (2 * D * F)  # both MLP GEMMs, counted per member
@@ -308,6 +307,7 @@ def run_head(args):
     a, b = torch.randn(P // 2, V, device=dev, generator=g), torch.randn(P // 2, D, device=dev, generator=g)
     sign = antithetic_signs(P, SIGMA).to(dev)
     tgt = zipf_tokens(T, seed=1)[1].to(dev)
+    from noise_amd.population import HEAD_FORMAT
     s = torch.cuda.current_stream().cuda_stream
     fmt = HEAD_FORMAT[args.head]
     if fmt == _lib.HEAD_FP32:
