@@ -54,3 +54,14 @@ def test_gather_losses_puts_every_rank_share_in_member_order(world):
     one = torch.arange(4.0)
     assert gather_losses(one, 1) is one
 
+
+
+def test_head_formats_map_to_the_library_and_unknown_ones_are_refused():
+    """The host's head names map onto noise_head_ce's NOISE_HEAD_* values, and an unknown name is refused before any
+    tensor is touched (no CPU path)."""
+    from noise_amd import _lib
+    from noise_amd.population import HEAD_FORMAT, HEAD_MODES, Weights
+    assert set(HEAD_FORMAT) == set(HEAD_MODES)
+    assert HEAD_FORMAT == {'fp32': _lib.HEAD_FP32, 'fp32_split': _lib.HEAD_FP32_SPLIT, 'bf16': _lib.HEAD_BF16}
+    with pytest.raises(ValueError, match='head must be one of'):
+        Weights({}, head='fp16')
