@@ -652,6 +652,9 @@ def test_head_ce_fp32_format_logit_error_bound():
     x = torch.randn(m * T, 512, generator=g) * 3
     gain = 0.5 + 1.5 * torch.rand(512, generator=g)
     rows = 10.0 ** (-7 + 8 * torch.rand(V, 1, generator=g))
+    # the scale's edge cases: an all-zero row (scale 1), a 1e-30 row (the largest scale), a 1e20 row (logits far past
+    # the cap: z' = +-15)
+    rows[0], rows[1], rows[2] = 0.0, 1e-30, 1e20
     W = torch.randn(V, 512, generator=g) * 512 ** -0.5 * 2 * rows
     a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
     sign = torch.tensor([1e-2, -1e-2, 5e-2, -5e-2])
@@ -671,8 +674,12 @@ def test_head_ce_fp32_format_logit_error_bound():
     z = om.lowrank(hn, W, a, b, sign, 'fp32')
     ref = 15 * torch.tanh(z / 15)
     bound = 2.0 ** -11 * (hn.abs() @ W.abs().t()) + 1e-5 + 1e-5 * z.abs()
-    err = (logits.cpu().view(m, T, V) - ref).abs()
+    got = logits.cpu().view(m, T, V)
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
     assert (err <= bound).all(), (err - bound).max()
+    # the 1e20 row saturates the cap (15 log2(e) ln(2) in fp32: within an ulp of 15)
+    assert ((got[..., 2].abs() - 15.0).abs() < 1e-5).all()
     # the bound is not vacuous: the largest rows' logits are O(1) and their errors well above the fp32 floor
     assert ref.abs().max() > 1 and err.max() > 1e-6
     ref_loss = om.head_loss(om.norm(x.view(m, T, 512)) * gain, W, a, b, sign, targets, 'fp32', 'fp32')
