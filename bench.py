@@ -16,7 +16,8 @@ shared x); `--workload attention` config 2 (windowed causal attention + per-head
 8 heads, T = 2048); `--workload head` config 3 (RMSNorm with gain + fp32 head + soft-capped CE,
 P = 512, T = 2048). `--workload stream` measures the HBM ceilings of the row kernels' read / write mixes with the
 library's own streaming kernel; `--workload library` times the vendor GEMM on the fused MLP's shapes (a reference
-point); `--workload copy` calibrates the PMC traffic counters. Prints one JSON line.
+point); `--workload copy` calibrates the PMC traffic counters; `--workload probes` and `--workload credit` time the
+readout probes (row f3) and the credit kernels of one rerun chunk (row f4). Prints one JSON line.
 """
 import argparse
 import json
@@ -417,12 +418,87 @@ def run_library(args):
                          'frac': pair / PEAK_BF16_TFLOPS, 'traffic': None, 'kernel': 'torch.matmul (vendor library)'}}
 
 
+def run_probes(args):
+    """Row f3: the readout-probe forward differences (noise_readout_probes, `cycle_derivatives`,
+    train/val/run.py:154-167) of 1024 tokens along 512 directions over a 4096 vocabulary. value = (token, direction,
+    vocabulary entry) terms per second; each costs two exp2, one reciprocal and ~6 other VALU operations."""
+    from noise_amd.probes import cycle_derivatives
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    n, P, Vv = 1024, 512, V
+    g = torch.Generator(device=dev).manual_seed(0)
+    base = torch.randn(n, Vv, device=dev, generator=g) * 3
+    C = torch.randn(P, Vv, device=dev, generator=g) * 0.5
+    y = torch.randint(0, Vv, (n,), device=dev, generator=g)
+    steps = 1e-2 * (1 + torch.rand(n, device=dev, generator=g))
+    sq = D * (1 + 0.1 * torch.rand(n, device=dev, generator=g))
+    dots = torch.randn(n, P, device=dev, generator=g)
+    dir_sq = D * (1 + 0.1 * torch.rand(P, device=dev, generator=g))
+    ms_step, ms_launch = _timed(lambda: cycle_derivatives(base, C, y, steps, sq, dots, dir_sq), args.steps, args.warmup)
+    entries = n * P * Vv
+    return {'metric': 'readout-probe terms per second (row f3)', 'value': entries / (ms_launch * 1e-3), 'unit': 'terms/s',
+            'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': ms_step, 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
+            'config': {'workload': 'readout_probes', 'tokens': n, 'directions': P, 'vocab': Vv, 'ms_per_launch': ms_launch},
+            'roofline': None}
+
+
+def run_credit(args):
+    """Row f4: the credit kernels of one rerun chunk at the reference's shapes (`query_key_errors`,
+    train/val/run.py:594-634: 64 draws, batch 1, 2048 tokens, 8 heads of 64): moved heads, head scores, the code
+    estimate (HBM streams of the bf16 draws and outputs) and the key filter (bf16 MFMA). value = the moved heads'
+    algorithmic HBM rate."""
+    from noise_amd import _lib
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    n, b, H = 64, 1, 8
+    g = torch.Generator(device=dev).manual_seed(0)
+    raw = torch.randn(b, T, H, 64, device=dev, generator=g)
+    a = torch.randn(n, b, T, H, 64, device=dev, generator=g).to(torch.bfloat16)
+    cos, sin = torch.rand(T, 32, device=dev, generator=g), torch.rand(T, 32, device=dev, generator=g)
+    out = torch.empty(n * b * T, H * 64, device=dev, dtype=torch.bfloat16)
+    base, hub = torch.randn(b, T, H, 64, device=dev, generator=g), torch.randn(b, T, H, 64, device=dev, generator=g)
+    score = torch.empty(b, H, T, n, device=dev)
+    cred = torch.randn(b, H, T, n, device=dev, generator=g)
+    est = torch.empty(b, T, H, 64, device=dev)
+    filt = torch.randn(b, H, T, T, device=dev, generator=g).to(torch.bfloat16)
+    kout = torch.empty(b, H, T, n, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    kernels = {
+        'moved_heads': (lambda: _lib.call('noise_moved_heads', raw.data_ptr(), a.data_ptr(), 0.1, cos.data_ptr(),
+                                          sin.data_ptr(), n, b, T, H, out.data_ptr(), H * 64, s),
+                        raw.numel() * 4 + a.numel() * 2 * 2 + cos.numel() * 8),
+        'head_scores': (lambda: _lib.call('noise_head_scores', out.data_ptr(), H * 64, base.data_ptr(), hub.data_ptr(),
+                                          n, b, T, H, score.data_ptr(), s),
+                        out.numel() * 2 + base.numel() * 8 + score.numel() * 4),
+        'code_estimate': (lambda: _lib.call('noise_code_estimate', cred.data_ptr(), a.data_ptr(), n, b, T, H,
+                                            est.data_ptr(), s),
+                          cred.numel() * 4 + a.numel() * 2 + est.numel() * 4),
+        'key_filter': (lambda: _lib.call('noise_key_filter', filt.data_ptr(), cred.data_ptr(), b, H, T, n,
+                                         kout.data_ptr(), s),
+                       filt.numel() * 2 + cred.numel() * 4 + kout.numel() * 4),
+    }
+    res = {}
+    for name, (fn, nbytes) in kernels.items():
+        _, ms = _timed(fn, args.steps, args.warmup)
+        res[name] = {'us': ms * 1e3, 'bytes': nbytes, 'TB/s': nbytes / (ms * 1e-3) / 1e12}
+    res['key_filter']['TFLOP/s'] = 2 * b * H * T * T * n / (res['key_filter']['us'] * 1e-6) / 1e12
+    mh = res['moved_heads']
+    return {'metric': 'credit kernels, algorithmic HBM rate (row f4)', 'value': mh['TB/s'] * 1e3, 'unit': 'GB/s',
+            'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': mh['us'] * 1e-3,
+            'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+            'config': {'workload': 'credit_chunk', 'draws': n, 'batch': b, 'tokens': T, 'heads': H, 'kernels': res},
+            'roofline': {'bound': 'hbm', 'achieved': mh['TB/s'] * 1e3, 'peak': 8000.0, 'unit': 'GB/s',
+                         'frac': mh['TB/s'] * 1e3 / 8000.0, 'traffic': mh['bytes'], 'kernel': 'moved_heads_vec_kernel'}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=10)
     ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy', 'stream', 'library'),
+    ap.add_argument('--workload', choices=('step', 'mlp', 'attention', 'head', 'copy', 'stream', 'library', 'probes',
+                                           'credit'),
                     default='step')
     ap.add_argument('--window', type=int, default=2048, help='attention window (config 2)')
     ap.add_argument('--qk-norm', action='store_true', help='config 2 with RMS-normalised q, k rows (the model case)')
@@ -448,9 +524,10 @@ def main():
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
         sys.exit(2)
-    result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head,
+    result = {'step': run_step, 'mlp': run_mlp, 'attention': run_attention, 'head': run_head, 'probes': run_probes,
+              'credit': run_credit,
               'copy': run_copy, 'stream': run_stream, 'library': run_library}[args.workload](args)
-    if not args.no_cpu_baseline and args.workload not in ('copy', 'stream', 'library'):
+    if not args.no_cpu_baseline and args.workload not in ('copy', 'stream', 'library', 'probes', 'credit'):
         result['cpu_baseline'] = cpu_baseline_mlp() if args.workload == 'mlp' else cpu_baseline_step()
     print(json.dumps(result), flush=True)
 

@@ -8,9 +8,15 @@
 //   (l, l + 32), so the rotation needs no exchange and the norm is one 32-lane sum.
 // head_scores: score[b, h, t, j] = sum_d (out[j, b, t, h, d] - baseline[b, t, h, d]) hub[b, t, h, d].
 // code_estimate: est[b, t, h, d] = sum_j credited[b, h, t, j] a[j, b, t, h, d], draws in order.
+// The three take 16- and 8-byte vector accesses when the pointers and strides allow (8 lanes per 64-dim row; 4 dims
+// per thread): at 64 draws x 2048 tokens x 8 heads, moved heads 2.5 -> 6.6 TB/s, head scores 1.2 -> 3.8-4.2 TB/s,
+// code estimate 3.2 -> 6.8 TB/s of their algorithmic bytes. Otherwise the scalar kernels (32 lanes per row, one
+// element per thread) run; the vector estimate is bit for bit the scalar one, the other two sum in another order.
 // key_filter: the key scores of `query_key_errors` (:622-623), (K.to(bf16) @ score.to(bf16)).float(): per (b, h), the
 //   matched filter K [T, T] times the query scores [T, n] on bf16 MFMA with fp32 accumulation, rounded to bf16 as
-//   the reference's bf16 matmul returns it.
+//   the reference's bf16 matmul returns it. 64-deep chunks with the next chunk prefetched into registers: at 64
+//   draws x 2048 tokens x 8 heads, 110 -> 45 us (1.7 TB/s of its algorithmic bytes, 0.38 PFLOP/s), bit for bit the
+//   32-deep unprefetched loop (the same products in the same order).
 #include "common.h"
 #include "credit.h"
 
@@ -44,6 +50,43 @@ __global__ void __launch_bounds__(256) moved_heads_kernel(const MovedHeadsArgs g
   o[lane + 32] = to_bf16(y2 * inv);
 }
 
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+// The same rows with 8 lanes per row (32 rows per workgroup): lane q owns the rotary pairs (d, d + 32) for
+// d = 4 q .. 4 q + 3, so every access is a 16-byte (fp32) or 8-byte (bf16) vector and the norm is an 8-lane sum.
+// Taken when every pointer and the output stride allow those accesses.
+__global__ void __launch_bounds__(256) moved_heads_vec_kernel(const MovedHeadsArgs g) {
+  const int q = threadIdx.x & 7;
+  const long r = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // (j, b, t, h) row
+  if (r >= g.rows) return;
+  const int h = (int)(r % g.H);
+  const long jbt = r / g.H, t = jbt % g.T, bt = jbt % (g.B * (long)g.T);
+  const float* raw = g.raw + (bt * g.H + h) * HD + 4 * q;
+  const __bf16* a = g.a + r * HD + 4 * q;
+  const float4 r1 = *reinterpret_cast<const float4*>(raw), r2 = *reinterpret_cast<const float4*>(raw + 32);
+  const bf16x4_t a1 = *reinterpret_cast<const bf16x4_t*>(a), a2 = *reinterpret_cast<const bf16x4_t*>(a + 32);
+  const float4 c4 = *reinterpret_cast<const float4*>(g.cos + t * 32 + 4 * q);
+  const float4 s4 = *reinterpret_cast<const float4*>(g.sin + t * 32 + 4 * q);
+  const float x1[4] = {r1.x + g.sigma * (float)a1[0], r1.y + g.sigma * (float)a1[1], r1.z + g.sigma * (float)a1[2],
+                       r1.w + g.sigma * (float)a1[3]};
+  const float x2[4] = {r2.x + g.sigma * (float)a2[0], r2.y + g.sigma * (float)a2[1], r2.z + g.sigma * (float)a2[2],
+                       r2.w + g.sigma * (float)a2[3]};
+  const float c[4] = {c4.x, c4.y, c4.z, c4.w}, s[4] = {s4.x, s4.y, s4.z, s4.w};
+  float y1[4], y2[4], ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y1[e] = x1[e] * c[e] + x2[e] * s[e];
+    y2[e] = -x1[e] * s[e] + x2[e] * c[e];
+    ss += y1[e] * y1[e] + y2[e] * y2[e];
+  }
+  const float inv = rsqrtf(group_sum<8>(ss) * (1.f / HD) + EPS);
+  bf16x4_t o1, o2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o1[e] = to_bf16(y1[e] * inv), o2[e] = to_bf16(y2[e] * inv);
+  __bf16* o = g.out + jbt * g.ldo + h * HD + 4 * q;
+  *reinterpret_cast<bf16x4_t*>(o) = o1;
+  *reinterpret_cast<bf16x4_t*>(o + 32) = o2;
+}
+
 __global__ void __launch_bounds__(256) head_scores_kernel(const HeadScoresArgs g) {
   const int lane = threadIdx.x & 31;
   const long r = (long)blockIdx.x * 8 + (threadIdx.x >> 5);  // (j, b, t, h) row
@@ -63,6 +106,48 @@ __global__ void __launch_bounds__(256) head_scores_kernel(const HeadScoresArgs g
   if (lane == 0) g.score[((b * g.H + h) * g.T + t) * g.n + j] = d;
 }
 
+// 8 lanes per row, lane q owning dims 8 q .. 8 q + 7 (16-byte bf16 and fp32 vector loads); the same sums otherwise
+__global__ void __launch_bounds__(256) head_scores_vec_kernel(const HeadScoresArgs g) {
+  const int q = threadIdx.x & 7;
+  const long r = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // (j, b, t, h) row
+  if (r >= g.rows) return;
+  const int h = (int)(r % g.H);
+  const long jbt = r / g.H, j = jbt / (g.B * (long)g.T), bt = jbt % (g.B * (long)g.T);
+  const long b = bt / g.T, t = bt % g.T;
+  const bf16x8 ov = *reinterpret_cast<const bf16x8*>(g.out + jbt * g.ld_out + h * HD + 8 * q);
+  const long base_off = (bt * g.H + h) * HD + 8 * q;
+  const float4 b0 = *reinterpret_cast<const float4*>(g.baseline + base_off);
+  const float4 b1 = *reinterpret_cast<const float4*>(g.baseline + base_off + 4);
+  const float4 h0 = *reinterpret_cast<const float4*>(g.hub + base_off);
+  const float4 h1 = *reinterpret_cast<const float4*>(g.hub + base_off + 4);
+  const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+  float d = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) d += ((float)ov[e] - bv[e]) * hv[e];
+  d = group_sum<8>(d);
+  if (q == 0) g.score[((b * g.H + h) * g.T + t) * g.n + j] = d;
+}
+
+// Four consecutive dims per thread (8-byte bf16 loads of a); each element's sum over the draws in order, as below.
+__global__ void __launch_bounds__(256) code_estimate_vec_kernel(const CodeEstimateArgs g) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;  // (b, t, h, d .. d + 3)
+  if (i >= g.elems) return;
+  const long bth = i / HD, h = bth % g.H, bt = bth / g.H, b = bt / g.T, t = bt % g.T;
+  const float* cr = g.credited + ((b * g.H + h) * g.T + t) * g.n;
+  const long stride = g.elems;  // one draw of a
+  const __bf16* a = g.a + i;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int j = 0; j < g.n; ++j) {
+    const bf16x4_t av = *reinterpret_cast<const bf16x4_t*>(a + j * stride);
+    const float c = cr[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += c * (float)av[e];
+  }
+  *reinterpret_cast<float4*>(g.est + i) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
 __global__ void __launch_bounds__(256) code_estimate_kernel(const CodeEstimateArgs g) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;  // (b, t, h, d)
   if (i >= g.elems) return;
@@ -78,11 +163,13 @@ __global__ void __launch_bounds__(256) code_estimate_kernel(const CodeEstimateAr
 }  // namespace
 
 namespace {
-// One workgroup = 64 rows t x 64 draws j of one (b, h); 4 waves of 16 rows. The contraction over s walks 32 at a
-// time through LDS: the K tile [64 t][32 s] as loaded (16-byte rows of 8), the scores [32 s][64 j] rounded to bf16
-// and stored transposed [64 j][32 s] so both MFMA operands are 16-byte reads along s. Lane l of wave w ends with
-// rows 16 w + 4 (l / 16) + e, column l % 16 of each 16-column block.
-constexpr int KF_LD = 32 + 8;  // LDS row pitch (bf16): 80 bytes, so 16 rows of a fragment read hit distinct banks
+// One workgroup = 64 rows t x 64 draws j of one (b, h); 4 waves of 16 rows. The contraction over s walks 64 at a
+// time through LDS: the K tile [64 t][64 s] as loaded (16-byte rows of 8), the scores [64 s][64 j] rounded to bf16
+// and stored transposed [64 j][64 s] so both MFMA operands are 16-byte reads along s. Lane l of wave w ends with
+// rows 16 w + 4 (l / 16) + e, column l % 16 of each 16-column block. The next chunk's K and score values are loaded
+// into registers while the current chunk's MFMAs run (the loop was load-latency bound: one workgroup per CU).
+constexpr int KF_BK = 64;
+constexpr int KF_LD = KF_BK + 8;  // LDS row pitch (bf16): 144 bytes, so 16 rows of a fragment read hit distinct banks
 __global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) {
   __shared__ __attribute__((aligned(16))) bf16 sa[64 * KF_LD];
   __shared__ __attribute__((aligned(16))) bf16 sb[64 * KF_LD];
@@ -92,26 +179,48 @@ __global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) 
   const float* score = g.score + (long)bh * g.T * g.n;
   f32x4 acc[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
                   f32x4{0.f, 0.f, 0.f, 0.f}};
-  // loaders: K row tid / 4, s chunk tid % 4 (8 values); scores row s = tid / 8, columns 8 (tid % 8) .. + 7
-  const int ar = tid >> 2, ac = (tid & 3) * 8, bs = tid >> 3, bc = (tid & 7) * 8;
-  for (int s0 = 0; s0 < g.T; s0 += 32) {
-    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(filt + (long)(t0 + ar) * g.T + s0 + ac);
-    float sv[8];
+  // loaders: K row tid / 4, s columns 16 (tid % 4) .. + 15; scores row s = tid / 4, columns 16 (tid % 4) .. + 15
+  const int ar = tid >> 2, ac = (tid & 3) * 16, bs = tid >> 2, bc = (tid & 3) * 16;
+  // whole float4 groups of scores when n % 4 == 0 (a group is then either all below n or all above)
+  const bool vec = (g.n & 3) == 0 && !((uintptr_t)g.score & 15);
+  auto load = [&](int s0, bf16x8 (&kv)[2], float (&sv)[16]) {
+    const bf16* kr = filt + (long)(t0 + ar) * g.T + s0 + ac;
+    kv[0] = *reinterpret_cast<const bf16x8*>(kr);
+    kv[1] = *reinterpret_cast<const bf16x8*>(kr + 8);
+    const float* sr = score + (long)(s0 + bs) * g.n + j0 + bc;
+    if (vec) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int j = j0 + bc + e;
-      sv[e] = j < g.n ? score[(long)(s0 + bs) * g.n + j] : 0.f;
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = j0 + bc + 4 * q < g.n ? *reinterpret_cast<const float4*>(sr + 4 * q)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        sv[4 * q] = v.x, sv[4 * q + 1] = v.y, sv[4 * q + 2] = v.z, sv[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sv[e] = j0 + bc + e < g.n ? sr[e] : 0.f;
     }
+  };
+  bf16x8 kv[2];
+  float sv[16];
+  load(0, kv, sv);
+  for (int s0 = 0; s0 < g.T; s0 += KF_BK) {
     __syncthreads();  // the previous chunk's fragments have been read
-    *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac]) = kv;
+    *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac]) = kv[0];
+    *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac + 8]) = kv[1];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sb[(bc + e) * KF_LD + bs] = to_bf16(sv[e]);
+    for (int e = 0; e < 16; ++e) sb[(bc + e) * KF_LD + bs] = to_bf16(sv[e]);
     __syncthreads();
-    const bf16x8 af = *reinterpret_cast<const bf16x8*>(&sa[(16 * wave + (lane & 15)) * KF_LD + 8 * (lane >> 4)]);
+    if (s0 + KF_BK < g.T) load(s0 + KF_BK, kv, sv);
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sb[(16 * cb + (lane & 15)) * KF_LD + 8 * (lane >> 4)]);
-      acc[cb] = mfma16x16x32(af, bfr, acc[cb]);
+    for (int kk = 0; kk < KF_BK / 32; ++kk) {
+      const bf16x8 af =
+          *reinterpret_cast<const bf16x8*>(&sa[(16 * wave + (lane & 15)) * KF_LD + 32 * kk + 8 * (lane >> 4)]);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const bf16x8 bfr =
+            *reinterpret_cast<const bf16x8*>(&sb[(16 * cb + (lane & 15)) * KF_LD + 32 * kk + 8 * (lane >> 4)]);
+        acc[cb] = mfma16x16x32(af, bfr, acc[cb]);
+      }
     }
   }
 #pragma unroll
@@ -142,6 +251,14 @@ int moved_heads_launch(const MovedHeadsArgs& g, hipStream_t s) {
   if (!g.raw || !g.a || !g.cos || !g.sin || !g.out || g.n <= 0 || g.B <= 0 || g.T <= 0 || g.H <= 0 ||
       g.ldo < (long)g.H * HD)
     return NOISE_EINVAL;
+  if (g.ldo % 4 == 0 && !(((uintptr_t)g.raw | (uintptr_t)g.cos | (uintptr_t)g.sin) & 15) &&
+      !(((uintptr_t)g.a | (uintptr_t)g.out) & 7)) {
+    const long grid = (g.rows + 31) / 32;
+    if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
+    hipLaunchKernelGGL(moved_heads_vec_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+    return NOISE_OK;
+  }
   const long grid = (g.rows + 7) / 8;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   hipLaunchKernelGGL(moved_heads_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
@@ -153,6 +270,13 @@ int head_scores_launch(const HeadScoresArgs& g, hipStream_t s) {
   if (!g.out || !g.baseline || !g.hub || !g.score || g.n <= 0 || g.B <= 0 || g.T <= 0 || g.H <= 0 ||
       g.ld_out < (long)g.H * HD)
     return NOISE_EINVAL;
+  if (g.ld_out % 8 == 0 && !(((uintptr_t)g.out | (uintptr_t)g.baseline | (uintptr_t)g.hub) & 15)) {
+    const long grid = (g.rows + 31) / 32;
+    if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
+    hipLaunchKernelGGL(head_scores_vec_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+    return NOISE_OK;
+  }
   const long grid = (g.rows + 7) / 8;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   hipLaunchKernelGGL(head_scores_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
@@ -162,6 +286,13 @@ int head_scores_launch(const HeadScoresArgs& g, hipStream_t s) {
 
 int code_estimate_launch(const CodeEstimateArgs& g, hipStream_t s) {
   if (!g.credited || !g.a || !g.est || g.n <= 0 || g.elems <= 0 || g.H <= 0 || g.T <= 0) return NOISE_EINVAL;
+  if (!(((uintptr_t)g.a | (uintptr_t)g.est) & 15)) {  // elems = B T H 64: whole 4-dim groups
+    const long grid = (g.elems / 4 + 255) / 256;
+    if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
+    hipLaunchKernelGGL(code_estimate_vec_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
+    NOISE_CHECK_LAUNCH();
+    return NOISE_OK;
+  }
   const long grid = (g.elems + 255) / 256;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
   hipLaunchKernelGGL(code_estimate_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);

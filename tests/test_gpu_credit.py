@@ -153,3 +153,44 @@ def test_query_credit_full_length_sampled_positions():
     floor = rel_err(ref16, ref32)
     log_case(f'full-length query credit: gpu {rel_err(got, ref32):.3e} floor {floor:.3e}')
     assert rel_err(got, ref32) <= 2 * floor + 1e-3
+
+
+def test_vector_and_scalar_credit_kernels_agree():
+    """moved_heads, head_scores and code_estimate take vector accesses when pointers and strides allow and scalar
+    ones otherwise (an odd output stride, an offset pointer). On the same inputs: the estimate bit for bit, the moved
+    heads within one bf16 step (the norm's sum runs in another order), the scores within fp32 rounding."""
+    from noise_amd import _lib
+    g = torch.Generator().manual_seed(23)
+    n, b, T, H = 4, 2, 128, 8
+    log_case(f'credit vector / scalar paths n={n} b={b} T={T}')
+    raw, a = (t.to(DEV) for t in _heads(g, n, b, T, H))
+    cos, sin = (t.to(DEV).contiguous() for t in _tables(T))
+    s = torch.cuda.current_stream().cuda_stream
+    W = H * 64
+    heads = {}
+    for ld in (W, W + 1):  # W + 1: odd stride, the scalar kernel
+        o = torch.zeros(n * b * T * ld, device=DEV, dtype=torch.bfloat16)
+        _lib.call('noise_moved_heads', raw.data_ptr(), a.data_ptr(), 0.1, cos.data_ptr(), sin.data_ptr(), n, b, T, H,
+                  o.data_ptr(), ld, s)
+        heads[ld] = o.view(n * b * T, ld)[:, :W].float().cpu()
+    vec, sca = heads[W], heads[W + 1]
+    assert ((vec - sca).abs() <= sca.abs() * 2.0 ** -7 + 1e-6).all()
+    assert float((vec == sca).float().mean()) > 0.999
+    base, hub = torch.randn(b, T, H, 64, generator=g).to(DEV), torch.randn(b, T, H, 64, generator=g).to(DEV)
+    out = torch.randn(n * b * T, W, generator=g).bfloat16().to(DEV)
+    out_odd = torch.zeros(n * b * T, W + 1, device=DEV, dtype=torch.bfloat16)
+    out_odd[:, :W] = out
+    scores = []
+    for o, ld in ((out, W), (out_odd, W + 1)):
+        sc = torch.empty(b, H, T, n, device=DEV)
+        _lib.call('noise_head_scores', o.data_ptr(), ld, base.data_ptr(), hub.data_ptr(), n, b, T, H, sc.data_ptr(), s)
+        scores.append(sc.cpu())
+    assert torch.allclose(scores[0], scores[1], rtol=1e-5, atol=1e-5)
+    cr = torch.randn(b, H, T, n, generator=g).to(DEV)
+    est_buf = torch.empty(b * T * H * 64 + 1, device=DEV)
+    ests = []
+    for off in (0, 1):  # offset 1: a misaligned output, the scalar kernel
+        _lib.call('noise_code_estimate', cr.data_ptr(), a.data_ptr(), n, b, T, H, est_buf.data_ptr() + 4 * off, s)
+        ests.append(est_buf[off:off + b * T * H * 64].cpu().clone())
+    torch.cuda.synchronize()
+    assert torch.equal(ests[0], ests[1])
