@@ -9,8 +9,8 @@
 // head_scores: score[b, h, t, j] = sum_d (out[j, b, t, h, d] - baseline[b, t, h, d]) hub[b, t, h, d].
 // code_estimate: est[b, t, h, d] = sum_j credited[b, h, t, j] a[j, b, t, h, d], draws in order.
 // The three take 16- and 8-byte vector accesses when the pointers and strides allow (8 lanes per 64-dim row; 4 dims
-// per thread): at 64 draws x 2048 tokens x 8 heads, moved heads 2.5 -> 6.6 TB/s, head scores 1.2 -> 3.8-4.2 TB/s,
-// code estimate 3.2 -> 6.8 TB/s of their algorithmic bytes. Otherwise the scalar kernels (32 lanes per row, one
+// per thread): at 64 draws x 2048 tokens x 8 heads, moved heads 2.5 -> 6.6 TB/s, head scores 1.2 -> 5.5 TB/s, code
+// estimate 3.2 -> 6.8 TB/s of their algorithmic bytes. Otherwise the scalar kernels (32 lanes per row, one
 // element per thread) run; the vector estimate is bit for bit the scalar one, the other two sum in another order.
 // key_filter: the key scores of `query_key_errors` (:622-623), (K.to(bf16) @ score.to(bf16)).float(): per (b, h), the
 //   matched filter K [T, T] times the query scores [T, n] on bf16 MFMA with fp32 accumulation, rounded to bf16 as
@@ -106,27 +106,50 @@ __global__ void __launch_bounds__(256) head_scores_kernel(const HeadScoresArgs g
   if (lane == 0) g.score[((b * g.H + h) * g.T + t) * g.n + j] = d;
 }
 
-// 8 lanes per row, lane q owning dims 8 q .. 8 q + 7 (16-byte bf16 and fp32 vector loads); the same sums otherwise
+// 8 lanes per row, lane q owning dims 8 q .. 8 q + 7 (16-byte bf16 and fp32 vector loads); the same sums otherwise.
+// Workgroup (x, y) takes the tile of 8 consecutive (b, t, h) rows bth = 8 x .. 8 x + 7 by 32 draws j = 32 y ..
+// 32 y + 31. Pass it of 8-lane group g reads row (8 x + g % 8, 32 y + g / 8 + 4 it): a wave's 8 rows are consecutive
+// in memory (1 KiB per load instruction), and each group keeps its (b, t, h)'s baseline and target in registers. The
+// scores go through LDS so that each (b, t, h) leaves its 32 draws as one whole 128-byte line.
 __global__ void __launch_bounds__(256) head_scores_vec_kernel(const HeadScoresArgs g) {
-  const int q = threadIdx.x & 7;
-  const long r = (long)blockIdx.x * 32 + (threadIdx.x >> 3);  // (j, b, t, h) row
-  if (r >= g.rows) return;
-  const int h = (int)(r % g.H);
-  const long jbt = r / g.H, j = jbt / (g.B * (long)g.T), bt = jbt % (g.B * (long)g.T);
-  const long b = bt / g.T, t = bt % g.T;
-  const bf16x8 ov = *reinterpret_cast<const bf16x8*>(g.out + jbt * g.ld_out + h * HD + 8 * q);
-  const long base_off = (bt * g.H + h) * HD + 8 * q;
-  const float4 b0 = *reinterpret_cast<const float4*>(g.baseline + base_off);
-  const float4 b1 = *reinterpret_cast<const float4*>(g.baseline + base_off + 4);
-  const float4 h0 = *reinterpret_cast<const float4*>(g.hub + base_off);
-  const float4 h1 = *reinterpret_cast<const float4*>(g.hub + base_off + 4);
-  const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-  const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-  float d = 0.f;
+  __shared__ float sc[8][33];
+  const int q = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const long bth_all = g.rows / g.n, bth = (long)blockIdx.x * 8 + (grp & 7);
+  const long j0 = (long)blockIdx.y * 32;
+  if (bth < bth_all) {
+    const int h = (int)(bth % g.H);
+    const long bt = bth / g.H;
+    const long base_off = (bt * g.H + h) * HD + 8 * q;
+    const float4 b0 = *reinterpret_cast<const float4*>(g.baseline + base_off);
+    const float4 b1 = *reinterpret_cast<const float4*>(g.baseline + base_off + 4);
+    const float4 h0 = *reinterpret_cast<const float4*>(g.hub + base_off);
+    const float4 h1 = *reinterpret_cast<const float4*>(g.hub + base_off + 4);
+    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const long jstride = g.B * (long)g.T;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) d += ((float)ov[e] - bv[e]) * hv[e];
-  d = group_sum<8>(d);
-  if (q == 0) g.score[((b * g.H + h) * g.T + t) * g.n + j] = d;
+    for (int it = 0; it < 8; ++it) {
+      const int jl = (grp >> 3) + 4 * it;
+      const long j = j0 + jl;
+      float d = 0.f;
+      if (j < g.n) {
+        const bf16x8 ov = *reinterpret_cast<const bf16x8*>(g.out + (j * jstride + bt) * g.ld_out + h * HD + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d += ((float)ov[e] - bv[e]) * hv[e];
+      }
+      d = group_sum<8>(d);
+      if (q == 0) sc[grp & 7][jl] = d;
+    }
+  }
+  __syncthreads();
+  // thread i: draw 32 y + i % 32 of row 8 x + i / 32
+  const int rl = threadIdx.x >> 5, jl = threadIdx.x & 31;
+  const long row = (long)blockIdx.x * 8 + rl, j = j0 + jl;
+  if (row < bth_all && j < g.n) {
+    const int h = (int)(row % g.H);
+    const long bt = row / g.H, b = bt / g.T, t = bt % g.T;
+    g.score[((b * g.H + h) * g.T + t) * g.n + j] = sc[rl][jl];
+  }
 }
 
 // Four consecutive dims per thread (8-byte bf16 loads of a); each element's sum over the draws in order, as below.
@@ -271,9 +294,9 @@ int head_scores_launch(const HeadScoresArgs& g, hipStream_t s) {
       g.ld_out < (long)g.H * HD)
     return NOISE_EINVAL;
   if (g.ld_out % 8 == 0 && !(((uintptr_t)g.out | (uintptr_t)g.baseline | (uintptr_t)g.hub) & 15)) {
-    const long grid = (g.rows + 31) / 32;
-    if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
-    hipLaunchKernelGGL(head_scores_vec_kernel, dim3((unsigned)grid), dim3(256), 0, s, g);
+    const long tiles = (g.rows / g.n + 7) / 8, chunks = (g.n + 31) / 32;  // rows = n B T H
+    if (tiles > 0x7fffffffL || chunks > 65535) return NOISE_ENOTSUP;
+    hipLaunchKernelGGL(head_scores_vec_kernel, dim3((unsigned)tiles, (unsigned)chunks), dim3(256), 0, s, g);
     NOISE_CHECK_LAUNCH();
     return NOISE_OK;
   }
