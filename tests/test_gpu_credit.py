@@ -91,6 +91,29 @@ def test_key_scores_match_the_bf16_product(n):
     assert ((got.double() - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6).all()
 
 
+@pytest.mark.parametrize('window', [256, 96])
+def test_key_scores_through_an_attention_map_filter(window):
+    """The matched filter as the reference builds it (train/val/run.py:572-592): the clean attention map A of
+    RMS-normalised rotary q, k under the causal window, K[t, s] = A[s, t] / max_t' A[s, t'] in bf16 (upper
+    triangular and banded: t <= s <= t + window, the opposite side of the diagonal from the test above). The key
+    scores through it within one bf16 step of the exact product of the same bf16 operands."""
+    g = torch.Generator().manual_seed(28)
+    b, h, T, n = 1, 8, 256, 24
+    log_case(f'key_scores attention-map filter T={T} window={window} n={n}')
+    cos, sin = _tables(T)
+    q, k = (om.norm(om.apply_rotary(torch.randn(b, T, h, 64, generator=g), cos, sin)) for _ in range(2))
+    logits = q.transpose(1, 2) @ k.transpose(1, 2).transpose(-1, -2) / 8.0
+    lag = torch.arange(T)[:, None] - torch.arange(T)[None, :]
+    A = logits.masked_fill(~((lag >= 0) & (lag <= window)), float('-inf')).softmax(-1)
+    filt = (A / A.amax(-1, keepdim=True)).transpose(-1, -2).bfloat16().contiguous()
+    assert torch.equal(filt.float().tril(-1), torch.zeros_like(filt.float()))  # nothing below the diagonal
+    score = torch.randn(b, h, T, n, generator=g)
+    got = credit.key_scores(filt.to(DEV), score.to(DEV)).cpu()
+    exact = filt.double() @ score.bfloat16().double()
+    assert torch.equal(got, got.bfloat16().float())
+    assert ((got.double() - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6).all()
+
+
 @pytest.mark.parametrize('kind', ['q', 'k'])
 def test_credit_chunk_matches_oracle(kind):
     """One chunk of query / key credit: GPU estimate within twice the oracle's own bf16-output floor (oracle
