@@ -131,6 +131,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   __shared__ __attribute__((aligned(16))) float ep_m[F16 ? BN : 4];   // F16: the exp argument's factor per column
   __shared__ float ep_u[C::UGROUPS][BM];                               // partial sums of x.b per row
   __shared__ float ep_sign;
+  __shared__ int ep_t[CE ? BM : 1];                                    // the head: target token per row (-1: none)
 
   // (a wave index made uniform with readfirstlane measured slower here: config 1 2.20 -> 2.50 ms, head +6%)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -223,6 +224,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
   // a_p (EPI_CE_F16: and of the weight rows' scales); thread 0 the sign (whole tile in one member only).
   float4 pre_ab = make_float4(0.f, 0.f, 0.f, 0.f), pre_sc = make_float4(1.f, 1.f, 1.f, 1.f);
   float pre_u = 0.f, pre_sign = 0.f;
+  int pre_t = -1;
   auto prefetch_ep = [&](int m0, int n0) {
     if constexpr (EPI == EPI_DENSE) return;
     const int pfirst = m0 / g.T, plast = min(m0 + BM - 1, g.M - 1) / g.T;
@@ -236,6 +238,13 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     float u = 0.f;
     for (int q = q0; q < q1; ++q) u += up[q * g.u_qstride];
     pre_u = u;
+    // the head: the tile's target tokens, so that its epilogue makes no global load (a load there, issued after the
+    // next tile's stage loads, would wait for all of them: vector memory operations complete in issue order)
+    // (a token id past the int range, like a negative one, matches no column)
+    if (CE && g.targets && tid < BM) {
+      const long tk = g.targets[(long)(row / g.T) * g.tok_mstride + row % g.T];
+      pre_t = tk < 0 || tk > 0x7fffffffL ? -1 : (int)tk;
+    }
   };
   auto stage_ep = [&]() {
     if constexpr (EPI == EPI_DENSE) return;
@@ -253,6 +262,7 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     }
     if (tid == 0) ep_sign = pre_sign;
     ep_u[tid / BM][tid % BM] = pre_u;
+    if (CE && tid < BM) ep_t[tid] = pre_t;
   };
 
   // ---- MFMA operands of one 32-deep k step: x rows wm*WM + 16 i + (lane & 15) and W rows
@@ -395,13 +405,11 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
     const int sl = n0 / g.seg_n, seg = g.seg0 + sl, scol = cb - sl * g.seg_n;  // column inside the segment
     const bool uniform = m0 / g.T == min(m0 + BM - 1, g.M - 1) / g.T;
     const float s_uni = ep_sign;
+    if constexpr (EPI == EPI_DENSE) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int lr = wm * WM + i * 16 + (lane & 15), row = m0 + lr;
-      const bool live = row < g.M;
-      const int rrow = live ? row : g.M - 1;
-      if constexpr (EPI == EPI_DENSE) {
-        if (live) {
+      for (int i = 0; i < FM; ++i) {
+        const int row = m0 + wm * WM + i * 16 + (lane & 15);
+        if (row < g.M) {
           bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
           for (int e = 0; e < CW; e += 8)
@@ -409,139 +417,160 @@ lowrank_gemm_kernel(const LowrankGemmArgs g) {
                             pack_bf16(acc[i][e / 4 + 1][0], acc[i][e / 4 + 1][1]),
                             pack_bf16(acc[i][e / 4 + 1][2], acc[i][e / 4 + 1][3]));
         }
-        continue;
       }
-      float u = 0.f;
+      if (next >= t_hi) break;
+      tile = next;
+      continue;
+    }
+    // bf16 rounding of the product and of u (the bf16 paths); the fp16 head never rounds
+    const bool rnd = !F16 && g.round_bf16;
+    // The epilogue, instantiated for a tile inside one member (UNI: its vectors from LDS and no global load, so no
+    // wait on the next tile's stage loads issued above) and for a tile that straddles members.
+    auto epilogue = [&](auto uni_c) {
+      constexpr bool UNI = decltype(uni_c)::value;
 #pragma unroll
-      for (int q = 0; q < C::UGROUPS; ++q) u += ep_u[q][lr];
-      float sgn = s_uni;
-      const int p = rrow / g.T, dir = p >> g.pair_shift;
-      if (!uniform) sgn = g.sign[p];  // tile straddles members: per-row vectors from global memory
-      const float su = sgn * (g.round_bf16 ? bf16r(u) : u);
-      // v = dense + s u a over the lane's CW columns
-      float v[CW];
+      for (int i = 0; i < FM; ++i) {
+        const int lr = wm * WM + i * 16 + (lane & 15), row = m0 + lr;
+        const bool live = row < g.M;
+        const int rrow = live ? row : g.M - 1;
+        float u = 0.f;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        float av[4];
-        if (uniform) {
-          const float4 a4 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j]);
-          av[0] = a4.x, av[1] = a4.y, av[2] = a4.z, av[3] = a4.w;
-        } else {
-          const float* arow = g.ra[seg] + (long)dir * g.ra_ld + scol + 4 * j;
+        for (int q = 0; q < C::UGROUPS; ++q) u += ep_u[q][lr];
+        // the row's member: for a tile that straddles members (per-row vectors from global memory) and for the value
+        // embedding's gather; a tile inside one member takes its vectors from LDS
+        int p = 0;
+        if (EPI == EPI_QKV || !UNI) p = rrow / g.T;
+        const int dir = p >> g.pair_shift;
+        float sgn = s_uni;
+        if constexpr (!UNI) sgn = g.sign[p];
+        const float su = sgn * (rnd ? bf16r(u) : u);
+        // v = dense + s u a over the lane's CW columns
+        float v[CW];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) av[e] = F16 ? arow[e] * g.col_scale[cb + 4 * j + e] : arow[e];
-        }
+        for (int j = 0; j < FN; ++j) {
+          float av[4];
+          if constexpr (UNI) {
+            const float4 a4 = *reinterpret_cast<const float4*>(&ep_a[lcol + 4 * j]);
+            av[0] = a4.x, av[1] = a4.y, av[2] = a4.z, av[3] = a4.w;
+          } else {
+            const float* arow = g.ra[seg] + (long)dir * g.ra_ld + scol + 4 * j;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[4 * j + e] = (g.round_bf16 ? bf16r(acc[i][j][e]) : acc[i][j][e]) + su * av[e];
-      }
-      if constexpr (EPI == EPI_STORE) {
-        if (live) {
-          if (g.out_f32) {
-            float* o = g.out_f32 + (long)row * g.ldo + cb;
-#pragma unroll
-            for (int j = 0; j < FN; ++j) store_f4(o + 4 * j, v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            for (int e = 0; e < 4; ++e) av[e] = F16 ? arow[e] * g.col_scale[cb + 4 * j + e] : arow[e];
           }
-          if (g.out_bf16) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * j + e] = (rnd ? bf16r(acc[i][j][e]) : acc[i][j][e]) + su * av[e];
+        }
+        if constexpr (EPI == EPI_STORE) {
+          if (live) {
+            if (g.out_f32) {
+              float* o = g.out_f32 + (long)row * g.ldo + cb;
+#pragma unroll
+              for (int j = 0; j < FN; ++j) store_f4(o + 4 * j, v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            }
+            if (g.out_bf16) {
+              bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
+#pragma unroll
+              for (int e = 0; e < CW; e += 8)
+                store_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
+                                pack_bf16(v[e + 6], v[e + 7]));
+            }
+          }
+        } else if constexpr (EPI == EPI_RESID) {
+          if (live) {
+            float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+              float4 r = o[j];
+              r.x += v[4 * j];
+              r.y += v[4 * j + 1];
+              r.z += v[4 * j + 2];
+              r.w += v[4 * j + 3];
+              o[j] = r;
+            }
+          }
+        } else if constexpr (EPI == EPI_QKV) {
+          // the wave's WN = 64 columns are one head; lane group lane / 16 holds head dims 16 (lane / 16) ..
+          const int t = rrow % g.T;
+          if (seg < 2) {
+            // rotary (utils/model.py:55-58): dims d and d + 32 pair up, held by lanes l and l ^ 32 (exchanged by
+            // v_permlane32_swap)
+            const int dd = (lane >> 4) * CW & 31;
+            const bool first = (lane >> 4) < 2;
+            const __bf16* cr = g.rot_cos + (long)t * 32 + dd;
+            const __bf16* sr = g.rot_sin + (long)t * 32 + dd;
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < CW; ++e) {
+              const f32pair hv = halves32(v[e]);  // dims d (lanes 0-31) and d + 32 (lanes 32-63)
+              const float c = (float)cr[e], sn = (float)sr[e];
+              const float y = first ? hv.lo * c + hv.hi * sn : hv.hi * c - hv.lo * sn;
+              v[e] = y;
+              ss += y * y;
+            }
+            // QK RMSNorm over the head's 64 dims (eps = 2^-23, utils/model.py:46-47)
+            ss = sum_rows4(ss);
+            // q (segment 0) leaves pre-multiplied by log2(e) / 8, the attention's score scale in base-2 units
+            const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f) * (seg ? 1.f : 0.18033688011112042f);
+#pragma unroll
+            for (int e = 0; e < CW; ++e) v[e] *= r;
+          } else if (g.gate) {
+            // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
+            const long tok = g.idx[(long)p * g.tok_mstride + t];
+            const float gt = g.gate[(long)rrow * 8 + scol / 64];
+            const float sa = sgn * g.ve_a[(long)dir * g.ve_v + tok];
+            const float* wr = g.ve_w + tok * 512 + scol;
+            const float* br = g.ve_b + (long)dir * 512 + scol;
+#pragma unroll
+            for (int e = 0; e < CW; ++e) v[e] += gt * (wr[e] + sa * br[e]);
+          }
+          if (live) {
+            // q, k and v: fp16 of the fp32 values (the reference feeds flex fp32 operands, train/val/eggroll.py:91)
             bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
 #pragma unroll
             for (int e = 0; e < CW; e += 8)
-              store_x4(o + e, pack_bf16(v[e], v[e + 1]), pack_bf16(v[e + 2], v[e + 3]), pack_bf16(v[e + 4], v[e + 5]),
-                              pack_bf16(v[e + 6], v[e + 7]));
+              store_x4(o + e, pack_f16(v[e], v[e + 1]), pack_f16(v[e + 2], v[e + 3]), pack_f16(v[e + 4], v[e + 5]),
+                              pack_f16(v[e + 6], v[e + 7]));
           }
-        }
-      } else if constexpr (EPI == EPI_RESID) {
-        if (live) {
-          float4* o = reinterpret_cast<float4*>(g.out_f32 + (long)row * g.ldo + cb);
+        } else {  // EPI_CE
+          // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,
+          // so the sum of exp(z') over 4096 columns needs no running maximum.
+          // Everything in log2 units: ez = exp(2 z / 15) = 2^(z 2 log2(e) / 15); zl = z' log2(e) =
+          // 15 log2(e) - 30 log2(e) / (ez + 1); exp(z') = 2^zl. The reciprocal is the hardware one
+          // (v_rcp_f32, 1 ulp): an IEEE division would cost ~10 VALU operations per logit.
+          constexpr float L2E = 1.4426950408889634f;
+          // the target's column among the lane's CW, if any (a target of -1, or none, matches no column)
+          const int tk = ep_t[lr];
+          const int te = tk < 0 ? -1 : (int)(tk - cb);
+          float se = 0.f, zt = 0.f;
+          float* lg = g.logits && live ? g.logits + (long)row * g.ldo + cb : nullptr;
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
-            float4 r = o[j];
-            r.x += v[4 * j];
-            r.y += v[4 * j + 1];
-            r.z += v[4 * j + 2];
-            r.w += v[4 * j + 3];
-            o[j] = r;
+            float zq[4], m[4] = {2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f};
+            if constexpr (F16) {
+              // v is the logit times the weight row's scale; m divides it out
+              const float4 m4 = *reinterpret_cast<const float4*>(&ep_m[lcol + 4 * j]);
+              m[0] = m4.x, m[1] = m4.y, m[2] = m4.z, m[3] = m4.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float ez = __builtin_amdgcn_exp2f(v[4 * j + e] * m[e]);
+              const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
+              se += __builtin_amdgcn_exp2f(zl);
+              zt = 4 * j + e == te ? zl : zt;
+              zq[e] = zl;
+            }
+            // the capped logits themselves (utils/model.py:203-204, returned when no targets are given)
+            if (lg) store_f4(lg + 4 * j, zq[0] * 0.6931471805599453f, zq[1] * 0.6931471805599453f,
+                             zq[2] * 0.6931471805599453f, zq[3] * 0.6931471805599453f);
           }
+          if (live && te >= 0 && te < CW) g.ce_tgt[row] = zt * 0.6931471805599453f;
+          se = sum_rows4(se);
+          if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = se;
         }
-      } else if constexpr (EPI == EPI_QKV) {
-        // the wave's WN = 64 columns are one head; lane group lane / 16 holds head dims 16 (lane / 16) ..
-        const int t = rrow % g.T;
-        if (seg < 2) {
-          // rotary (utils/model.py:55-58): dims d and d + 32 pair up, held by lanes l and l ^ 32 (exchanged by
-          // v_permlane32_swap)
-          const int dd = (lane >> 4) * CW & 31;
-          const bool first = (lane >> 4) < 2;
-          const __bf16* cr = g.rot_cos + (long)t * 32 + dd;
-          const __bf16* sr = g.rot_sin + (long)t * 32 + dd;
-          float ss = 0.f;
-#pragma unroll
-          for (int e = 0; e < CW; ++e) {
-            const f32pair hv = halves32(v[e]);  // dims d (lanes 0-31) and d + 32 (lanes 32-63)
-            const float c = (float)cr[e], sn = (float)sr[e];
-            const float y = first ? hv.lo * c + hv.hi * sn : hv.hi * c - hv.lo * sn;
-            v[e] = y;
-            ss += y * y;
-          }
-          // QK RMSNorm over the head's 64 dims (eps = 2^-23, utils/model.py:46-47)
-          ss = sum_rows4(ss);
-          // q (segment 0) leaves pre-multiplied by log2(e) / 8, the attention's score scale in base-2 units
-          const float r = rsqrtf(ss * (1.f / 64.f) + 1.1920928955078125e-07f) * (seg ? 1.f : 0.18033688011112042f);
-#pragma unroll
-          for (int e = 0; e < CW; ++e) v[e] *= r;
-        } else if (g.gate) {
-          // value embedding (train/val/eggroll.py:85-89): v += 2 sigmoid(gate) (W[idx] + s a[idx] b)
-          const long tok = g.idx[(long)p * g.tok_mstride + t];
-          const float gt = g.gate[(long)rrow * 8 + scol / 64];
-          const float sa = sgn * g.ve_a[(long)dir * g.ve_v + tok];
-          const float* wr = g.ve_w + tok * 512 + scol;
-          const float* br = g.ve_b + (long)dir * 512 + scol;
-#pragma unroll
-          for (int e = 0; e < CW; ++e) v[e] += gt * (wr[e] + sa * br[e]);
-        }
-        if (live) {
-          // q, k and v: fp16 of the fp32 values (the reference feeds flex fp32 operands, train/val/eggroll.py:91)
-          bf16* o = g.out_bf16 + (long)row * g.ldo + cb;
-#pragma unroll
-          for (int e = 0; e < CW; e += 8)
-            store_x4(o + e, pack_f16(v[e], v[e + 1]), pack_f16(v[e + 2], v[e + 3]), pack_f16(v[e + 4], v[e + 5]),
-                            pack_f16(v[e + 6], v[e + 7]));
-        }
-      } else {  // EPI_CE
-        // soft cap 15 tanh(z / 15) (train/val/eggroll.py:100) with tanh(y) = 1 - 2 / (exp(2y) + 1); |z'| <= 15,
-        // so the sum of exp(z') over 4096 columns needs no running maximum.
-        // Everything in log2 units: ez = exp(2 z / 15) = 2^(z 2 log2(e) / 15); zl = z' log2(e) =
-        // 15 log2(e) - 30 log2(e) / (ez + 1); exp(z') = 2^zl. The reciprocal is the hardware one
-        // (v_rcp_f32, 1 ulp): an IEEE division would cost ~10 VALU operations per logit.
-        constexpr float L2E = 1.4426950408889634f;
-        // the target's column among the lane's CW, if any (a target of -1, or none, matches no column)
-        const long tk = g.targets ? g.targets[(long)p * g.tok_mstride + rrow % g.T] : -1;
-        const int te = tk < 0 ? -1 : (int)(tk - cb);
-        float se = 0.f, zt = 0.f;
-        float* lg = g.logits && live ? g.logits + (long)row * g.ldo + cb : nullptr;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          float zq[4], m[4] = {2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f, 2.f * L2E / 15.f};
-          if constexpr (F16) {
-            // v is the logit times the weight row's scale; m divides it out
-            const float4 m4 = *reinterpret_cast<const float4*>(&ep_m[lcol + 4 * j]);
-            m[0] = m4.x, m[1] = m4.y, m[2] = m4.z, m[3] = m4.w;
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float ez = __builtin_amdgcn_exp2f(v[4 * j + e] * m[e]);
-            const float zl = fmaf(__builtin_amdgcn_rcpf(ez + 1.f), -30.f * L2E, 15.f * L2E);
-            se += __builtin_amdgcn_exp2f(zl);
-            zt = 4 * j + e == te ? zl : zt;
-            zq[e] = zl;
-          }
-          // the capped logits themselves (utils/model.py:203-204, returned when no targets are given)
-          if (lg) store_f4(lg + 4 * j, zq[0] * 0.6931471805599453f, zq[1] * 0.6931471805599453f,
-                           zq[2] * 0.6931471805599453f, zq[3] * 0.6931471805599453f);
-        }
-        if (live && te >= 0 && te < CW) g.ce_tgt[row] = zt * 0.6931471805599453f;
-        se = sum_rows4(se);
-        if (live && (lane >> 4) == 0) g.upart_out[(long)row * g.upart_ld + (n0 + wn * WN) / WN] = se;
       }
-    }
+    };
+    if (uniform) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
     if (next >= t_hi) break;
     tile = next;
   }
