@@ -10,8 +10,10 @@
 // The reference materialises z[n, P, V]; here one wave owns a token: its V logits stay in registers (V / 64
 // per lane) while the C rows of its directions stream through (1 KiB coalesced loads), and each (token,
 // direction) sum of V exponentials ends in one wave reduction. The C row of the next direction is loaded while the
-// current one is summed (two rows in registers: 2 waves per SIMD instead of 5, and 3.21 -> 1.43 ms on 1024 tokens x
-// 512 directions x 4096 vocabulary: the row's load latency, not the arithmetic, had set the time). The cap and exp
+// current one is summed, into the other of two register sets (2 waves per SIMD instead of 5: 3.21 -> 1.43 ms on 1024
+// tokens x 512 directions x 4096 vocabulary, the row's load latency, not the arithmetic, had set the time). The
+// per-token scalars come through the scalar data cache, and nothing the sum needs is loaded after that row, so the
+// sum does not wait for it (vector loads complete in issue order): 1.43 -> 0.92 ms. The cap and exp
 // run in log2 units with the hardware exp2 and reciprocal, as the head's cross-entropy epilogue does; the moved
 // RMS's reciprocal and the cap's 2 log2(e) / 15 are one multiplier.
 #include "common.h"
@@ -31,15 +33,26 @@ __device__ __forceinline__ float cap_log2_y(float y) {
 }
 __device__ __forceinline__ float cap_log2(float z) { return cap_log2_y(z * K2); }
 
+// ROWS: the directions' rows come from g.rows (per token); otherwise direction k is row k.
+// A wave-uniform load through the scalar data cache (s_load), for inputs the kernel never writes: it waits on its own
+// counter, not behind the vector loads of the C rows.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// NCT: the vocabulary's 256-entry chunks when fixed at compile time (16: the model's 4096), 0 when read from g.V;
+// a fixed count leaves the loop without branches, so the next row's loads stay where they are issued.
+template <bool ROWS, int NCT>
 __global__ void __launch_bounds__(256) probe_kernel(const ProbeArgs g) {
   const int lane = threadIdx.x & 63;
-  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int i = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));  // this wave's token
   if (i >= g.n) return;
-  const int nc = g.V >> 8;
-  const long yi = g.y[i];
+  const int nc = NCT ? NCT : g.V >> 8;
+  const long yi = ld_uniform(g.y + i);
   const bool valid = yi >= 0;
   const long t = valid ? yi : 0;
-  const float s = g.steps[i], sq = g.sq[i];
+  const float s = ld_uniform(g.steps + i), sq = ld_uniform(g.sq + i);
   const float* bi = g.base + (long)i * g.base_ld;
   float4 b[MAXC];
 #pragma unroll
@@ -57,32 +70,51 @@ __global__ void __launch_bounds__(256) probe_kernel(const ProbeArgs g) {
     }
   se = group_sum<64>(se);
   const float clean = logf(se) - cap_log2(base_t * inv0) * LN2;
-  // the C row of direction k + 1 is loaded while direction k is summed
-  auto row_of = [&](int k) -> long {
-    const long j = g.rows ? g.rows[(long)i * g.K + k] : k;
-    return j >= 0 && j < g.P ? j : -1;
+  // Everything direction k + 1 needs (its C row, into the other of two register sets; its dot, |D|^2 and target C
+  // entry; the row index of direction k + 2) is loaded before direction k is summed, so that those loads land during
+  // the sum and the sum waits for none of them: vector memory operations complete in issue order, so a load the sum
+  // needed, issued after them, would wait for all of them.
+  // Every load below is unconditional, from an address kept in bounds, and no value is computed from a loaded one
+  // before it is used: hipcc places such a computation next to the load, where its wait would also wait for the loads
+  // issued since. A row index is checked where the next direction's loads need it; an invalid row or target leaves
+  // NaN in the output whatever |D|^2 and the target's C entry hold, so those are used as loaded.
+  auto row_raw = [&](int k) -> long {
+    if constexpr (ROWS) return ld_uniform(g.rows + (long)i * g.K + k);
+    else return k;
   };
-  float4 cn[MAXC];
-  long jn = row_of(0);
+  auto row_ok = [&](long j) -> long { return j >= 0 && j < g.P ? j : -1; };
+  auto load_row = [&](long j, float4 (&dst)[MAXC]) {
+    const float* cr = g.C + (j >= 0 ? j : 0) * g.c_ld + 4 * lane;
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c)
-    if (c < nc) cn[c] = *reinterpret_cast<const float4*>(g.C + (jn >= 0 ? jn : 0) * g.c_ld + 256 * c + 4 * lane);
-  for (int k = 0; k < g.K; ++k) {
+    for (int c = 0; c < MAXC; ++c) dst[c] = *reinterpret_cast<const float4*>(cr + 256 * min(c, nc - 1));
+  };
+  const long tc = t < g.V ? t : 0;
+  float dj, ds, ct;  // the scalars of the direction summed next
+  auto load_scalars = [&](int k, long j) {
+    const long jc = j >= 0 ? j : 0;
+    dj = ld_uniform(g.dots + (long)i * g.dots_ld + k);
+    ds = ld_uniform(g.dir_sq + (g.dir_sq_tok ? (long)i * g.K + k : jc));
+    ct = ld_uniform(g.C + jc * g.c_ld + tc);
+  };
+  long jn = row_ok(row_raw(0)), jn2 = g.K > 1 ? row_raw(1) : -1;  // the rows of the next two directions (jn2 raw)
+  float4 ca[MAXC], cb[MAXC];
+  load_row(jn, ca);
+  load_scalars(0, jn);
+  auto direction = [&](int k, const float4 (&cv)[MAXC], float4 (&cn)[MAXC]) {
     const long j = jn;
     const bool jok = j >= 0;
-    float4 cv[MAXC];
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) cv[c] = cn[c];
+    const float djk = dj, dsk = ds, ctk = ct;
     if (k + 1 < g.K) {
-      jn = row_of(k + 1);
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c)
-        if (c < nc) cn[c] = *reinterpret_cast<const float4*>(g.C + (jn >= 0 ? jn : 0) * g.c_ld + 256 * c + 4 * lane);
+      jn = row_ok(jn2);
+      load_row(jn, cn);
+      load_scalars(k + 1, jn);
+      if (k + 2 < g.K) jn2 = row_raw(k + 2);
+      // Direction k's row (loaded before these 16) has landed once at most 16 vector loads are outstanding (the
+      // scalars count on the scalar-load counter). Stated here, the compiler keeps it instead of the stricter wait its
+      // tracking across the loop's back edge would place before the sum.
+      __builtin_amdgcn_s_waitcnt((MAXC & 15) | (7 << 4) | (15 << 8) | ((MAXC >> 4) << 14));
     }
-    const float dj = g.dots[(long)i * g.dots_ld + k];
-    const float ds = g.dir_sq_tok ? g.dir_sq[(long)i * g.K + k] : (jok ? g.dir_sq[j] : 0.f);
-    const float inv = rsqrtf((sq + 2.f * s * dj + s * s * ds) / (float)g.width + EPS), mv = inv * K2;
-    const float* cj = g.C + (jok ? j : 0) * g.c_ld;
+    const float inv = rsqrtf((sq + 2.f * s * djk + s * s * dsk) / (float)g.width + EPS), mv = inv * K2;
     float sm = 0.f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c)
@@ -93,8 +125,12 @@ __global__ void __launch_bounds__(256) probe_kernel(const ProbeArgs g) {
               __builtin_amdgcn_exp2f(cap_log2_y(fmaf(s, cv[c].w, b[c].w) * mv));
       }
     sm = group_sum<64>(sm);
-    const float moved = logf(sm) - cap_log2(fmaf(s, t < g.V ? cj[t] : 0.f, base_t) * inv) * LN2;
+    const float moved = logf(sm) - cap_log2(fmaf(s, ctk, base_t) * inv) * LN2;
     if (lane == 0) g.out[(long)i * g.K + k] = jok ? (moved - clean) / s * (valid ? 1.f : 0.f) : __builtin_nanf("");
+  };
+  for (int k = 0; k < g.K; k += 2) {
+    direction(k, ca, cb);
+    if (k + 1 < g.K) direction(k + 1, cb, ca);
   }
 }
 
@@ -108,7 +144,15 @@ int probe_launch(const ProbeArgs& g, hipStream_t stream) {
     return NOISE_EINVAL;
   const long grid = ((long)g.n + 3) / 4;
   if (grid > 0x7fffffffL) return NOISE_ENOTSUP;
-  hipLaunchKernelGGL(probe_kernel, dim3((unsigned)grid), dim3(256), 0, stream, g);
+  const bool full = g.V == 256 * MAXC;
+  if (g.rows && full)
+    hipLaunchKernelGGL((probe_kernel<true, MAXC>), dim3((unsigned)grid), dim3(256), 0, stream, g);
+  else if (g.rows)
+    hipLaunchKernelGGL((probe_kernel<true, 0>), dim3((unsigned)grid), dim3(256), 0, stream, g);
+  else if (full)
+    hipLaunchKernelGGL((probe_kernel<false, MAXC>), dim3((unsigned)grid), dim3(256), 0, stream, g);
+  else
+    hipLaunchKernelGGL((probe_kernel<false, 0>), dim3((unsigned)grid), dim3(256), 0, stream, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
