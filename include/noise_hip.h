@@ -293,7 +293,8 @@ int noise_head_ce(const void* x, int x_bf16, const float* gain, const void* w_he
  * steps[i], L the soft-capped cross-entropy of the head on norm(x_i + steps[i] D_j) (its RMS from sq, dots and
  * dir_sq) and L_i0 on norm(x_i); 0 where the target is -1. rows null: every direction, K == P, dir_sq [P]
  * (cycle_derivatives); rows [n, K] int64: the token's own directions, dir_sq [n, K] with dir_sq_per_token != 0
- * (row_derivatives). fp32; vocab % 256 == 0, vocab <= 4096; width is the stream width of the RMS. */
+ * (row_derivatives); a row outside [0, P) gives NaN at its entry (no read outside dirs). fp32; vocab % 256 == 0,
+ * vocab <= 4096; width is the stream width of the RMS. */
 int noise_readout_probes(const float* base, long base_ld, const float* dirs, long dirs_ld, const int64_t* rows, int K,
                          const int64_t* targets, const float* steps, const float* sq, const float* dots, long dots_ld,
                          const float* dir_sq, int dir_sq_per_token, int n, int vocab, int P, int width, float* out,

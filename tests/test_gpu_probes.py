@@ -68,3 +68,27 @@ def test_row_derivatives_equal_cycle_entries():
     ref = op.row_derivatives(base.double(), C.double(), rows, y, steps.double(), sq.double(),
                              dots.gather(1, rows).double(), dir_sq[rows].double(), width=width)
     assert ((got.cpu().double() - ref).abs() <= _bound(base, C, y, steps, sq, dots, dir_sq, width)).all()
+
+
+def test_probes_runtime_vocab_odd_counts_and_invalid_rows():
+    """A vocabulary other than the model's 4096 (the kernel instance that reads the chunk count at run time), odd
+    direction counts (the unpaired last direction of the kernel's two-direction steps), and row lists holding
+    invalid rows (-1 and past P): NaN at those entries, every other entry bit for bit the full cycle's, and the
+    cycle within the bound of the oracle."""
+    n, width, V, P, K = 20, 512, 768, 33, 7
+    log_case(f'probes n={n} V={V} P={P} K={K} invalid rows')
+    args = _case(n, width, V, P, 5e-2, seed=5)
+    base, C, y, steps, sq, dots, dir_sq = args
+    full = probes.cycle_derivatives(*(t.to(DEV) for t in args), width=width).cpu()
+    ref = op.cycle_derivatives(*(t.double() if t.is_floating_point() else t for t in args), width=width)
+    assert ((full.double() - ref).abs() <= _bound(*args, width)).all()
+    rows = torch.randint(0, P, (n, K), generator=torch.Generator().manual_seed(11))
+    rows[::3, 0] = -1
+    rows[1::4, K - 1] = P + 3
+    valid = (rows >= 0) & (rows < P)
+    rc = rows.clamp(0, P - 1)
+    got = probes.row_derivatives(base.to(DEV), C.to(DEV), rows.to(DEV), y.to(DEV), steps.to(DEV), sq.to(DEV),
+                                 dots.gather(1, rc).to(DEV), dir_sq[rc].to(DEV), width=width).cpu()
+    assert torch.isnan(got[~valid]).all()
+    assert torch.equal(got[valid], full.gather(1, rc)[valid])
+
