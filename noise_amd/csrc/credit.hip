@@ -14,9 +14,10 @@
 // element per thread) run; the vector estimate is bit for bit the scalar one, the other two sum in another order.
 // key_filter: the key scores of `query_key_errors` (:622-623), (K.to(bf16) @ score.to(bf16)).float(): per (b, h), the
 //   matched filter K [T, T] times the query scores [T, n] on bf16 MFMA with fp32 accumulation, rounded to bf16 as
-//   the reference's bf16 matmul returns it. 64-deep chunks with the next chunk prefetched into registers: at 64
-//   draws x 2048 tokens x 8 heads, 110 -> 45 us (1.7 TB/s of its algorithmic bytes, 0.38 PFLOP/s), bit for bit the
-//   32-deep unprefetched loop (the same products in the same order).
+//   the reference's bf16 matmul returns it. 64-deep chunks with the next chunk prefetched into registers, and
+//   32-draw blocks when 64-draw ones would leave fewer than two workgroups per CU: at 64 draws x 2048 tokens x 8
+//   heads, 110 -> 45 -> 33 us (2.3 TB/s of its algorithmic bytes), bit for bit the 32-deep unprefetched loop (the same
+//   products in the same order).
 #include "common.h"
 #include "credit.h"
 
@@ -193,45 +194,50 @@ namespace {
 // into registers while the current chunk's MFMAs run (the loop was load-latency bound: one workgroup per CU).
 constexpr int KF_BK = 64;
 constexpr int KF_LD = KF_BK + 8;  // LDS row pitch (bf16): 144 bytes, so 16 rows of a fragment read hit distinct banks
+// JB draws per workgroup (64, or 32 when the 64-wide grid leaves fewer than two workgroups per CU: each output's
+// products and their order are the same either way).
+template <int JB>
 __global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) {
+  constexpr int JC = JB / 4, NCB = JB / 16;  // scores per loader thread, 16-column MFMA blocks
   __shared__ __attribute__((aligned(16))) bf16 sa[64 * KF_LD];
-  __shared__ __attribute__((aligned(16))) bf16 sb[64 * KF_LD];
+  __shared__ __attribute__((aligned(16))) bf16 sb[JB * KF_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t0 = blockIdx.x * 64, j0 = blockIdx.y * 64, bh = blockIdx.z;
+  const int t0 = blockIdx.x * 64, j0 = blockIdx.y * JB, bh = blockIdx.z;
   const bf16* filt = g.filt + (long)bh * g.T * g.T;
   const float* score = g.score + (long)bh * g.T * g.n;
-  f32x4 acc[4] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
-                  f32x4{0.f, 0.f, 0.f, 0.f}};
-  // loaders: K row tid / 4, s columns 16 (tid % 4) .. + 15; scores row s = tid / 4, columns 16 (tid % 4) .. + 15
-  const int ar = tid >> 2, ac = (tid & 3) * 16, bs = tid >> 2, bc = (tid & 3) * 16;
+  f32x4 acc[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // loaders: K row tid / 4, s columns 16 (tid % 4) .. + 15; scores row s = tid / 4, columns JC (tid % 4) .. + JC - 1
+  const int ar = tid >> 2, ac = (tid & 3) * 16, bs = tid >> 2, bc = (tid & 3) * JC;
   // whole float4 groups of scores when n % 4 == 0 (a group is then either all below n or all above)
   const bool vec = (g.n & 3) == 0 && !((uintptr_t)g.score & 15);
-  auto load = [&](int s0, bf16x8 (&kv)[2], float (&sv)[16]) {
+  auto load = [&](int s0, bf16x8 (&kv)[2], float (&sv)[JC]) {
     const bf16* kr = filt + (long)(t0 + ar) * g.T + s0 + ac;
     kv[0] = *reinterpret_cast<const bf16x8*>(kr);
     kv[1] = *reinterpret_cast<const bf16x8*>(kr + 8);
     const float* sr = score + (long)(s0 + bs) * g.n + j0 + bc;
     if (vec) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < JC / 4; ++q) {
         const float4 v = j0 + bc + 4 * q < g.n ? *reinterpret_cast<const float4*>(sr + 4 * q)
                                                : make_float4(0.f, 0.f, 0.f, 0.f);
         sv[4 * q] = v.x, sv[4 * q + 1] = v.y, sv[4 * q + 2] = v.z, sv[4 * q + 3] = v.w;
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sv[e] = j0 + bc + e < g.n ? sr[e] : 0.f;
+      for (int e = 0; e < JC; ++e) sv[e] = j0 + bc + e < g.n ? sr[e] : 0.f;
     }
   };
   bf16x8 kv[2];
-  float sv[16];
+  float sv[JC];
   load(0, kv, sv);
   for (int s0 = 0; s0 < g.T; s0 += KF_BK) {
     __syncthreads();  // the previous chunk's fragments have been read
     *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac]) = kv[0];
     *reinterpret_cast<bf16x8*>(&sa[ar * KF_LD + ac + 8]) = kv[1];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sb[(bc + e) * KF_LD + bs] = to_bf16(sv[e]);
+    for (int e = 0; e < JC; ++e) sb[(bc + e) * KF_LD + bs] = to_bf16(sv[e]);
     __syncthreads();
     if (s0 + KF_BK < g.T) load(s0 + KF_BK, kv, sv);
 #pragma unroll
@@ -239,7 +245,7 @@ __global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) 
       const bf16x8 af =
           *reinterpret_cast<const bf16x8*>(&sa[(16 * wave + (lane & 15)) * KF_LD + 32 * kk + 8 * (lane >> 4)]);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < NCB; ++cb) {
         const bf16x8 bfr =
             *reinterpret_cast<const bf16x8*>(&sb[(16 * cb + (lane & 15)) * KF_LD + 32 * kk + 8 * (lane >> 4)]);
         acc[cb] = mfma16x16x32(af, bfr, acc[cb]);
@@ -247,7 +253,7 @@ __global__ void __launch_bounds__(256) key_filter_kernel(const KeyFilterArgs g) 
     }
   }
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int j = j0 + 16 * cb + (lane & 15);
     if (j >= g.n) continue;
 #pragma unroll
@@ -263,9 +269,18 @@ int key_filter_launch(const KeyFilterArgs& g, hipStream_t s) {
   if (!g.filt || !g.score || !g.out || g.BH <= 0 || g.T <= 0 || g.n <= 0 || g.T % 64 ||
       ((uintptr_t)g.filt & 15))
     return NOISE_EINVAL;
-  if (g.BH > 65535 || (g.n + 63) / 64 > 65535) return NOISE_ENOTSUP;
-  hipLaunchKernelGGL(key_filter_kernel, dim3((unsigned)(g.T / 64), (unsigned)((g.n + 63) / 64), (unsigned)g.BH),
-                     dim3(256), 0, s, g);
+  if (g.BH > 65535 || (g.n + 31) / 32 > 65535) return NOISE_ENOTSUP;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const long wide = (long)(g.T / 64) * ((g.n + 63) / 64) * g.BH;
+  if (wide < 2L * cus)
+    hipLaunchKernelGGL(key_filter_kernel<32>, dim3((unsigned)(g.T / 64), (unsigned)((g.n + 31) / 32), (unsigned)g.BH),
+                       dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(key_filter_kernel<64>, dim3((unsigned)(g.T / 64), (unsigned)((g.n + 63) / 64), (unsigned)g.BH),
+                       dim3(256), 0, s, g);
   NOISE_CHECK_LAUNCH();
   return NOISE_OK;
 }
