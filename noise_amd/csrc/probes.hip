@@ -13,9 +13,12 @@
 // current one is summed, into the other of two register sets (2 waves per SIMD instead of 5: 3.21 -> 1.43 ms on 1024
 // tokens x 512 directions x 4096 vocabulary, the row's load latency, not the arithmetic, had set the time). The
 // per-token scalars come through the scalar data cache, and nothing the sum needs is loaded after that row, so the
-// sum does not wait for it (vector loads complete in issue order): 1.43 -> 0.92 ms. The cap and exp
+// sum does not wait for it (vector loads complete in issue order): 1.43 -> 0.92 ms; with each direction's wait
+// stated (the previous output store may stay in flight) and the last direction outside the loop: 0.84 ms. The cap and exp
 // run in log2 units with the hardware exp2 and reciprocal, as the head's cross-entropy epilogue does; the moved
 // RMS's reciprocal and the cap's 2 log2(e) / 15 are one multiplier.
+#include <type_traits>
+
 #include "common.h"
 #include "probes.h"
 
@@ -100,20 +103,24 @@ __global__ void __launch_bounds__(256) probe_kernel(const ProbeArgs g) {
   float4 ca[MAXC], cb[MAXC];
   load_row(jn, ca);
   load_scalars(0, jn);
-  auto direction = [&](int k, const float4 (&cv)[MAXC], float4 (&cn)[MAXC]) {
+  // Direction k (row in cv): with PF, first the loads of direction k + 1 (its row into cn), then the wait for
+  // direction k's own loads, stated here: VW vector operations may stay in flight, the 16 of that row and, after the
+  // first direction, the previous direction's output store (vector memory operations complete in issue order). With
+  // the waits stated and no direction without prefetch inside the loop, the compiler keeps them instead of the
+  // stricter ones its tracking would place across the loop's joins.
+  auto direction = [&](int k, const float4 (&cv)[MAXC], float4 (&cn)[MAXC], auto pf, auto vw) {
+    constexpr bool PF = decltype(pf)::value;
+    constexpr int VW = decltype(vw)::value;
     const long j = jn;
     const bool jok = j >= 0;
     const float djk = dj, dsk = ds, ctk = ct;
-    if (k + 1 < g.K) {
+    if constexpr (PF) {
       jn = row_ok(jn2);
       load_row(jn, cn);
       load_scalars(k + 1, jn);
       if (k + 2 < g.K) jn2 = row_raw(k + 2);
-      // Direction k's row (loaded before these 16) has landed once at most 16 vector loads are outstanding (the
-      // scalars count on the scalar-load counter). Stated here, the compiler keeps it instead of the stricter wait its
-      // tracking across the loop's back edge would place before the sum.
-      __builtin_amdgcn_s_waitcnt((MAXC & 15) | (7 << 4) | (15 << 8) | ((MAXC >> 4) << 14));
     }
+    __builtin_amdgcn_s_waitcnt((VW & 15) | (7 << 4) | (15 << 8) | ((VW >> 4) << 14));
     const float inv = rsqrtf((sq + 2.f * s * djk + s * s * dsk) / (float)g.width + EPS), mv = inv * K2;
     float sm = 0.f;
 #pragma unroll
@@ -128,9 +135,26 @@ __global__ void __launch_bounds__(256) probe_kernel(const ProbeArgs g) {
     const float moved = logf(sm) - cap_log2(fmaf(s, ctk, base_t) * inv) * LN2;
     if (lane == 0) g.out[(long)i * g.K + k] = jok ? (moved - clean) / s * (valid ? 1.f : 0.f) : __builtin_nanf("");
   };
-  for (int k = 0; k < g.K; k += 2) {
-    direction(k, ca, cb);
-    if (k + 1 < g.K) direction(k + 1, cb, ca);
+  using pf_t = std::true_type;
+  using last_t = std::false_type;
+  using first_w = std::integral_constant<int, MAXC>;   // nothing but the prefetched row after direction 0's
+  using next_w = std::integral_constant<int, MAXC + 1>; // and the previous direction's output store
+  using none_w = std::integral_constant<int, 0>;
+  if (g.K == 1) {
+    direction(0, ca, cb, last_t{}, none_w{});
+    return;
+  }
+  direction(0, ca, cb, pf_t{}, first_w{});  // direction k's row is in cb at the top of each trip
+  int k = 1;
+  for (; k + 2 < g.K; k += 2) {
+    direction(k, cb, ca, pf_t{}, next_w{});
+    direction(k + 1, ca, cb, pf_t{}, next_w{});
+  }
+  if (k + 1 < g.K) {
+    direction(k, cb, ca, pf_t{}, next_w{});
+    direction(k + 1, ca, cb, last_t{}, none_w{});
+  } else {
+    direction(k, cb, ca, last_t{}, none_w{});
   }
 }
 

@@ -91,4 +91,9 @@ def test_probes_runtime_vocab_odd_counts_and_invalid_rows():
                                  dots.gather(1, rc).to(DEV), dir_sq[rc].to(DEV), width=width).cpu()
     assert torch.isnan(got[~valid]).all()
     assert torch.equal(got[valid], full.gather(1, rc)[valid])
+    for k in (1, 2):  # one direction (no prefetch at all) and two (the first and the last, no loop trip)
+        rk = rows[:, :k].clamp(0, P - 1).contiguous()
+        gk = probes.row_derivatives(base.to(DEV), C.to(DEV), rk.to(DEV), y.to(DEV), steps.to(DEV), sq.to(DEV),
+                                    dots.gather(1, rk).to(DEV), dir_sq[rk].to(DEV), width=width).cpu()
+        assert torch.equal(gk, full.gather(1, rk)), k
 
